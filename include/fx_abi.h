@@ -1,0 +1,225 @@
+/*
+ * fx_abi.h -- C ABI of libfxforge.so, the gfx950 (MI355X, CDNA4) kernels behind
+ * the fxlm / fxgpu Python surface.
+ *
+ * Conventions
+ *   - Every pointer is HIP device memory unless the comment says "host".
+ *   - bf16 tensors are passed as uint16_t* holding IEEE bfloat16 bit patterns.
+ *   - `stream` is a hipStream_t passed as void* (torch.cuda.current_stream().cuda_stream).
+ *   - Every entry point only enqueues work on `stream`; none synchronises and none
+ *     allocates device memory.  Workspace buffers are owned by the caller.
+ *   - Return value: 0 on success, FX_EINVAL when an argument check fails, otherwise
+ *     the hipError_t of the failed HIP call.  fx_last_error() gives a message.
+ *
+ * Each entry point names the reference interface it replaces
+ * (berattunca21-byte/radeon-igpu-forge, paths relative to the repo root).
+ */
+#ifndef FX_ABI_H
+#define FX_ABI_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FX_EINVAL (-1)
+#define FX_ABI_VERSION 1
+
+/* ---- library ------------------------------------------------------------ */
+
+/* ABI version (FX_ABI_VERSION).  No reference counterpart (the reference has no
+ * prebuilt library; its loader is ml/fxgpu/hip_kernel.py:50-145). */
+int fx_abi_version(void);
+
+/* Message for the last non-zero return on the calling host thread. */
+const char* fx_last_error(void);
+
+/* Loader smoke kernel: p[i] = value for i < n.
+ * Replaces the fill42 smoke of ml/fxgpu/hip_kernel.py:148-163. */
+int fx_fill_f32(float* p, int64_t n, float value, void* stream);
+
+/* ---- RMSNorm ------------------------------------------------------------ */
+
+/* y = x * rstd * w, rstd[r] = 1/sqrt(mean_d(x[r,d]^2) + eps) (fp32, one per row).
+ * x, y: (N, D) bf16 contiguous; w: (D,) bf16; D % 8 == 0, 8 <= D <= 8192.
+ * Replaces _RMSNorm.forward + rms_norm_fwd
+ * (ml/fxlm/norm.py:47-62, ml/fxlm/kernels/norm.hip:32-59). */
+int fx_rms_norm_fwd(const uint16_t* x, const uint16_t* w, uint16_t* y, float* rstd,
+                    int64_t N, int32_t D, float eps, void* stream);
+
+/* Bytes of fp32 workspace fx_rms_norm_bwd needs for (N, D). */
+int64_t fx_rms_norm_bwd_workspace(int64_t N, int32_t D);
+
+/* dx = rstd*w*dy - x*(rstd^3 * sum_d(x*w*dy) / D)   (bf16, (N, D))
+ * dw = sum_rows x*rstd*dy                             (fp32 dw_f32 and bf16 dw, (D,))
+ * One pass over x and dy: dx and per-strip dw partials in one kernel, then a column
+ * reduction of the partials.  `work` holds fx_rms_norm_bwd_workspace(N, D) bytes.
+ * dw (bf16) may be NULL.
+ * Replaces _RMSNorm.backward + rms_norm_bwd_dx + rms_norm_bwd_dw + part.sum(0)
+ * (ml/fxlm/norm.py:64-85, ml/fxlm/kernels/norm.hip:63-127). */
+int fx_rms_norm_bwd(const uint16_t* x, const uint16_t* dy, const uint16_t* w,
+                    const float* rstd, uint16_t* dx, float* dw_f32, uint16_t* dw,
+                    float* work, int64_t N, int32_t D, void* stream);
+
+/* ---- softmax cross-entropy ---------------------------------------------- */
+
+/* inv_n = 1/count(target != ignore_index) (0 when the count is 0);
+ * mul = inv_n * (grad_scale ? *grad_scale : grad_scale_value).
+ * Out-of-range targets count here (they are ignored by fx_ce_fwd_grad), exactly as
+ * _inv_nvalid does.  Replaces _inv_nvalid and the `mul = inv_n * gs_t` line
+ * (ml/fxlm/cross_entropy.py:41-44, :117-121). */
+int fx_ce_inv_nvalid(const int64_t* target, int64_t N, int64_t ignore_index,
+                     const float* grad_scale, float grad_scale_value,
+                     float* inv_n, float* mul, void* stream);
+
+/* Argument block of the fused CE kernel; mirrors CEArgs
+ * (ml/fxlm/kernels/ce.hip:10-19, ml/fxlm/cross_entropy.py:23-30) with bf16 logits
+ * and a per-row loss vector instead of one atomically accumulated scalar. */
+typedef struct fxCEArgs {
+    const uint16_t* logits;   /* (N, V) bf16, row stride ld (elements) */
+    const int64_t* target;    /* (N,) int64 */
+    uint16_t* grad;           /* (N, V) bf16 row stride ldg, or NULL (loss only) */
+    float* row_loss;          /* (N,) fp32: lse - x_t for valid rows, 0 otherwise */
+    const float* mul;         /* () fp32 grad multiplier (grad_scale / n_valid) */
+    int64_t N;
+    int64_t V;
+    int64_t ld;               /* logits row stride, elements */
+    int64_t ldg;              /* grad row stride, elements */
+    int64_t ignore_index;
+} fxCEArgs;
+
+/* Per row r: m, Z = max and sum(exp(x - m)) of logits[r]; valid = (t != ignore_index
+ * && 0 <= t < V); row_loss[r] = valid ? m + log Z - x[t] : 0;
+ * grad[r, :] = valid ? (softmax - onehot(t)) * (*mul) : 0.
+ * Replaces _ce_rows + ce_fwd_grad (ml/fxlm/cross_entropy.py:47-59,
+ * ml/fxlm/kernels/ce.hip:32-116). */
+int fx_ce_fwd_grad(const fxCEArgs* args, void* stream);
+
+/* loss = (sum_r row_loss[r]) * (*inv_n), summed in a fixed order (deterministic).
+ * Replaces `loss_sum * inv_n` (ml/fxlm/cross_entropy.py:88, :139, :183). */
+int fx_ce_loss_finalize(const float* row_loss, int64_t N, const float* inv_n,
+                        float* loss, void* stream);
+
+/* grad *= (*g) / (*applied); *applied = *g.  Exits at once when the ratio is 1, so
+ * the usual loss.backward() (g == 1) costs one tiny launch and no pass over grad.
+ * Replaces _FusedCE.backward's `grad * g` (ml/fxlm/cross_entropy.py:90-93). */
+int fx_ce_scale_grad(uint16_t* grad, int64_t numel, const float* g, float* applied,
+                     void* stream);
+
+/* ---- FlatAdamW ---------------------------------------------------------- */
+
+#define FX_ADAMW_MAX_TENSORS 64
+
+/* By-value tensor list; mirrors TensorList (ml/fxlm/kernels/optim.hip:15-21,
+ * ml/fxlm/optim.py:28-35).  Gradients are bf16, contiguous, 16-byte aligned;
+ * off[] are element offsets into the flat buffers (multiples of 8). */
+typedef struct fxTensorList {
+    const uint16_t* g[FX_ADAMW_MAX_TENSORS];
+    int64_t off[FX_ADAMW_MAX_TENSORS];
+    int64_t n[FX_ADAMW_MAX_TENSORS];
+    int32_t wd[FX_ADAMW_MAX_TENSORS];
+    int32_t count;
+} fxTensorList;
+
+/* Flat optimiser state and hyper-parameters. */
+typedef struct fxAdamWState {
+    float* master;            /* fp32 flat master weights */
+    float* m;                 /* fp32 first moment */
+    float* v;                 /* fp32 second moment */
+    uint16_t* p16;            /* bf16 flat params (model parameters are views of it) */
+    int32_t* step;            /* () step counter, incremented before bias correction */
+    float* found_inf;         /* () 1.0 when any gradient is non-finite, else 0.0 */
+    float* grad_norm;         /* () sqrt(sum g^2) / scale */
+    float* scale;             /* () dynamic loss scale, updated in place */
+    int32_t* growth;          /* () clean steps since the last scale change */
+    float* work;              /* fx_adamw_workspace(...) bytes */
+    float lr, beta1, beta2, eps, weight_decay, max_grad_norm;
+    float growth_factor;      /* 2.0 in the reference */
+    float backoff_factor;     /* 0.5 in the reference */
+    int32_t growth_interval;
+} fxAdamWState;
+
+/* Bytes of workspace fx_adamw_step needs for these tensor lists. */
+int64_t fx_adamw_workspace(const fxTensorList* lists, int32_t nlists);
+
+/* One optimiser step, fully on the device (no host synchronisation):
+ *   sumsq = sum g^2 over all lists, bad = any non-finite g or non-finite sumsq;
+ *   found_inf = bad; grad_norm = sqrt(sumsq)/scale; clip = bad ? 0 : min(1, max/(norm+1e-6));
+ *   if !bad: step += 1 and, per element, g' = g*clip/scale;
+ *            w -= lr*wd*w (wd flag); m = b1 m + (1-b1) g'; v = b2 v + (1-b2) g'^2;
+ *            w -= lr*(m/(1-b1^step)) / (sqrt(v/(1-b2^step)) + eps); p16 = bf16(w);
+ *   then the loss-scale update of torch._amp_update_scale_ (backoff on bad, growth
+ *   after growth_interval clean steps).
+ * Replaces FlatAdamW.step: adamw_sumsq + adamw_final + adamw_update +
+ * torch._amp_update_scale_ (ml/fxlm/optim.py:136-173,
+ * ml/fxlm/kernels/optim.hip:25-162). */
+int fx_adamw_step(const fxAdamWState* state, const fxTensorList* lists, int32_t nlists,
+                  void* stream);
+
+/* ---- flash attention ------------------------------------------------------ */
+
+/* Argument block of the attention kernels; mirrors AttnArgs
+ * (ml/fxlm/kernels/attention.hip:35-47, ml/fxlm/attention.py:22-38) with bf16 tensors,
+ * the head dimension as a field and one Delta workspace.
+ * q, k, v, dq, dk, dv: (B, T, H, D) with unit stride along D and the element strides
+ * below along b, t, h (views of a fused (B, T, 3, H, D) buffer are fine);
+ * o, dout: (B, T, H, D) contiguous; lse, delta: (B, H, T) fp32. */
+typedef struct fxAttnArgs {
+    const uint16_t* q;
+    const uint16_t* k;
+    const uint16_t* v;
+    const uint16_t* o;        /* forward output, read by the backward */
+    const uint16_t* dout;     /* upstream gradient */
+    uint16_t* o_out;          /* forward output */
+    uint16_t* dq;
+    uint16_t* dk;
+    uint16_t* dv;
+    const float* lse;         /* logsumexp from the forward, read by the backward */
+    float* lse_out;           /* logsumexp written by the forward */
+    float* delta;             /* backward workspace: rowsum(dout * o) */
+    int64_t qsb, qst, qsh, ksb, kst, ksh, vsb, vst, vsh;
+    int64_t dqb, dqt, dqh, dkb, dkt, dkh, dvb, dvt, dvh;
+    int32_t B, T, H, D;       /* D in {64, 128} */
+    float scale;
+    int32_t causal;
+} fxAttnArgs;
+
+/* O = softmax(Q K^T * scale [causal: key <= query]) V, lse = max + log(sum exp)
+ * (-inf and O = 0 for a row with no visible key).  bf16 MFMA, fp32 online softmax.
+ * Replaces _fwd + attn_fwd (ml/fxlm/attention.py:87-104,
+ * ml/fxlm/kernels/attention.hip:103-224). */
+int fx_attn_fwd(const fxAttnArgs* args, void* stream);
+
+/* Delta = rowsum(dout * o); P = exp(S*scale - lse); dS = P * (dP - Delta) * scale;
+ * dQ = dS K, dK = dS^T Q, dV = P^T dout (dP = dout V^T).  Two kernels: per query
+ * tile (Delta and dQ), then per key tile (dK and dV).  No atomics: deterministic.
+ * Replaces _bwd + attn_bwd_prep/_dkv/_dq (ml/fxlm/attention.py:107-134,
+ * ml/fxlm/kernels/attention.hip:228-534). */
+int fx_attn_bwd(const fxAttnArgs* args, void* stream);
+
+/* ---- fused (gather) linear ------------------------------------------------- */
+
+/* Y = act(A W^T + bias), A (M, K): dense rows (A row m = X + m*ldx) when idx is NULL,
+ * otherwise gathered windows A[m, w*F + f] = X[idx[m] + w, f] of X (R, F) (K = W*F,
+ * F % 8 == 0; a window outside X reads as zeros).  W (N, K) bf16 contiguous, bias (N,)
+ * or NULL, Y (M, N).  act: 0 identity, 1 GELU (tanh approximation).  H (M, N), when
+ * not NULL, receives the pre-activation; Xg (M, K), when not NULL, the gathered A.
+ * bf16 MFMA, fp32 accumulation.  K % 8 == 0.
+ * Replaces FusedGatherLinear.forward + gather_gemm (ml/fxgpu/fused_linear.py:35-88,
+ * ml/fxgpu/gather_gemm.hip:16-180) and the fc -> gelu_tanh of the GPT MLP
+ * (ml/fxlm/model.py:71). */
+int fx_linear_fwd(const uint16_t* X, int64_t ldx, const int32_t* idx, int64_t F, int64_t R,
+                  const uint16_t* W, const uint16_t* bias, uint16_t* Y, uint16_t* H,
+                  uint16_t* Xg, int64_t M, int64_t N, int64_t K, int32_t act, void* stream);
+
+/* dh = dy * gelu_tanh'(h), elementwise over n bf16 values (16-byte aligned buffers).
+ * The activation half of the fused linear's backward (the reference's torch autograd
+ * of F.gelu(approximate="tanh"), ml/fxlm/model.py:71). */
+int fx_gelu_bwd(const uint16_t* dy, const uint16_t* h, uint16_t* dh, int64_t n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FX_ABI_H */

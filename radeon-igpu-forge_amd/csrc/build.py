@@ -1,0 +1,80 @@
+"""Build libfxforge.so, the gfx950 kernel library behind fxlm/fxgpu.
+
+    python radeon-igpu-forge_amd/csrc/build.py [--report]
+
+Every ``*.hip`` file in this directory is one translation unit, compiled in
+parallel by hipcc for gfx950 only and linked into
+``radeon-igpu-forge_amd/libfxforge.so`` (written to a temporary name and
+renamed, so a concurrent loader never sees a half-written file).
+``--report`` adds ``-Rpass-analysis=kernel-resource-usage`` so hipcc prints
+VGPR/AGPR/SGPR, scratch (spill) and LDS use per kernel.
+"""
+import concurrent.futures
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.dirname(HERE)
+OUT = os.path.join(PKG, "libfxforge.so")
+OBJ_DIR = os.path.join(HERE, "_build")
+ARCH = "gfx950"
+
+# -packed-fp32-ops: keep the compiler from emitting v_pk_{add,mul,fma}_f32.
+FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-munsafe-fp-atomics", "-Wall", "-Wno-unused-function",
+]
+
+
+def _hipcc():
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    for cand in (os.path.join(rocm, "bin", "hipcc"), shutil.which("hipcc")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found (set ROCM_PATH)")
+
+
+def sources():
+    return sorted(os.path.join(HERE, f) for f in os.listdir(HERE) if f.endswith(".hip"))
+
+
+def _compile(hipcc, src, report):
+    obj = os.path.join(OBJ_DIR, os.path.basename(src)[:-4] + ".o")
+    cmd = [hipcc] + FLAGS + (["-Rpass-analysis=kernel-resource-usage"] if report else []) \
+        + ["-c", src, "-o", obj]
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    log = "\n".join(l for l in (p.stdout + p.stderr).splitlines()
+                    if "packed-fp32-ops" not in l)
+    if p.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {os.path.basename(src)}:\n{log}")
+    return obj, log
+
+
+def build(verbose=False, report=False, jobs=None):
+    """Compile every .hip source and link libfxforge.so; returns its path."""
+    hipcc = _hipcc()
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    srcs = sources()
+    jobs = jobs or min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
+    objs = []
+    with concurrent.futures.ThreadPoolExecutor(jobs) as ex:
+        for obj, log in ex.map(lambda s: _compile(hipcc, s, report), srcs):
+            objs.append(obj)
+            if log.strip() and (verbose or report):
+                print(log)
+    tmp = OUT + f".tmp{os.getpid()}"
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    if p.returncode != 0:
+        raise RuntimeError(f"link failed:\n{p.stdout}{p.stderr}")
+    os.replace(tmp, OUT)
+    if verbose:
+        print(f"built {OUT} from {len(srcs)} sources")
+    return OUT
+
+
+if __name__ == "__main__":
+    build(verbose=True, report="--report" in sys.argv)

@@ -1,0 +1,281 @@
+// RMSNorm forward / backward for gfx950.
+//
+// Row layout shared by both kernels: a "row group" of LPR consecutive lanes owns one
+// row.  Lane j of the group holds the 16-byte vectors j, j+LPR, ..., j+(NV-1)*LPR of
+// the row (8 bf16 each), so every load and store is a coalesced 128-bit access and
+// the row statistics are a butterfly reduction inside the group (no LDS, no barrier).
+// LPR divides 64, so a group never straddles two waves.
+//
+// Semantics follow ml/fxlm/kernels/norm.hip:32-127 (fp32 math, bf16 I/O here):
+//   rstd = rsqrt(mean(x^2) + eps); y = (x * rstd) * w
+//   dx = rstd * w * dy - x * (rstd^3 * sum(x*w*dy) / D)
+//   dw = sum_rows x * rstd * dy
+#include "fx_device.h"
+
+namespace fx {
+
+template <int LPR, int NV>
+__global__ void __launch_bounds__(256)
+rms_fwd_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+               uint16_t* __restrict__ y, float* __restrict__ rstd, int64_t N, int D, float eps) {
+    constexpr int G = 256 / LPR;
+    const int lane = threadIdx.x % LPR;
+    const int64_t row = (int64_t)blockIdx.x * G + threadIdx.x / LPR;
+    if (row >= N) return;  // uniform per group: partners of the shuffles below stay active
+    const int V8 = D >> 3;
+    const uint16_t* xr = x + row * D;
+
+    uint4 xv[NV];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = i * LPR + lane;
+        xv[i] = make_uint4(0u, 0u, 0u, 0u);
+        if (c < V8) xv[i] = ld16_nt(xr + (int64_t)c * 8);
+        float f[8];
+        unpack8(xv[i], f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
+    }
+    ss = group_sum<LPR>(ss);
+    const float r = rsqrtf(ss / (float)D + eps);
+    if (lane == 0) rstd[row] = r;
+
+    uint16_t* yr = y + row * D;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = i * LPR + lane;
+        if (c < V8) {
+            float f[8], g[8], o[8];
+            unpack8(xv[i], f);
+            unpack8(ld16(w + c * 8), g);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = (f[j] * r) * g[j];
+            st16_nt(yr + (int64_t)c * 8, pack8(o));
+        }
+    }
+}
+
+// dx for every row of a strip of `rows_per_block` rows, plus the strip's partial dw
+// (fp32, one row of `part` per block).
+template <int LPR, int NV>
+__global__ void __launch_bounds__(256)
+rms_bwd_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ dy,
+               const uint16_t* __restrict__ w, const float* __restrict__ rstd,
+               uint16_t* __restrict__ dx, float* __restrict__ part, int64_t N, int D,
+               int64_t rows_per_block) {
+    constexpr int G = 256 / LPR;
+    extern __shared__ float red[];  // D floats
+    const int lane = threadIdx.x % LPR;
+    const int grp = threadIdx.x / LPR;
+    const int V8 = D >> 3;
+    const float invD = 1.f / (float)D;
+
+    uint4 wv[NV];
+    float acc[NV][8];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = i * LPR + lane;
+        wv[i] = (c < V8) ? ld16(w + c * 8) : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = 0.f;
+    }
+
+    const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
+    const int64_t r1 = (r0 + rows_per_block < N) ? r0 + rows_per_block : N;
+    for (int64_t row = r0 + grp; row < r1; row += G) {
+        const uint16_t* xr = x + row * D;
+        const uint16_t* dr = dy + row * D;
+        uint4 xv[NV], dv[NV];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int c = i * LPR + lane;
+            xv[i] = make_uint4(0u, 0u, 0u, 0u);
+            dv[i] = make_uint4(0u, 0u, 0u, 0u);
+            if (c < V8) {
+                xv[i] = ld16_nt(xr + (int64_t)c * 8);
+                dv[i] = ld16_nt(dr + (int64_t)c * 8);
+            }
+        }
+        const float r = rstd[row];
+        float t = 0.f;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            float fx_[8], fd[8], fw[8];
+            unpack8(xv[i], fx_);
+            unpack8(dv[i], fd);
+            unpack8(wv[i], fw);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                t += fx_[j] * fw[j] * fd[j];
+                acc[i][j] += fx_[j] * r * fd[j];
+            }
+        }
+        t = group_sum<LPR>(t);
+        const float corr = r * r * r * t * invD;
+        uint16_t* dxr = dx + row * D;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int c = i * LPR + lane;
+            if (c < V8) {
+                float fx_[8], fd[8], fw[8], o[8];
+                unpack8(xv[i], fx_);
+                unpack8(dv[i], fd);
+                unpack8(wv[i], fw);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) o[j] = r * fw[j] * fd[j] - fx_[j] * corr;
+                st16_nt(dxr + (int64_t)c * 8, pack8(o));
+            }
+        }
+    }
+
+    // fold the G row groups' partials in a fixed order (deterministic)
+    for (int g = 0; g < G; ++g) {
+        if (grp == g) {
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                const int c = i * LPR + lane;
+                if (c < V8) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        red[c * 8 + j] = (g == 0) ? acc[i][j] : red[c * 8 + j] + acc[i][j];
+                }
+            }
+        }
+        __syncthreads();
+    }
+    float* pr = part + (int64_t)blockIdx.x * D;
+    for (int c = threadIdx.x; c < D; c += 256) pr[c] = red[c];
+}
+
+// dw[c] = sum_p part[p][c]: 8 columns x 32 partial-row lanes per block, fixed order.
+__global__ void __launch_bounds__(256)
+rms_dw_reduce_kernel(const float* __restrict__ part, int64_t P, int D, float* __restrict__ dw_f32,
+                     uint16_t* __restrict__ dw) {
+    __shared__ float red[32][9];
+    const int cl = threadIdx.x & 7, rl = threadIdx.x >> 3;
+    const int col = blockIdx.x * 8 + cl;
+    float s = 0.f;
+    if (col < D)
+        for (int64_t p = rl; p < P; p += 32) s += part[p * D + col];
+    red[rl][cl] = s;
+    __syncthreads();
+    if (rl == 0 && col < D) {
+        float t = 0.f;
+        for (int k = 0; k < 32; ++k) t += red[k][cl];
+        dw_f32[col] = t;
+        if (dw) dw[col] = f32_to_bf16(t);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// host dispatch
+
+struct RowShape {
+    int lpr, nv;
+};
+
+// Pick the (LPR, NV) instantiation covering D/8 vectors with the fewest idle slots,
+// preferring wider groups on ties.
+static RowShape pick_shape(int D) {
+    static const int lprs[] = {64, 32, 16, 8};
+    static const int nvs[] = {1, 2, 3, 4, 6, 8, 12, 16};
+    const int v8 = D / 8;
+    RowShape best{0, 0};
+    int best_waste = 1 << 30;
+    for (int l : lprs)
+        for (int n : nvs)
+            if (l * n >= v8 && l * n - v8 < best_waste) {
+                best_waste = l * n - v8;
+                best = {l, n};
+            }
+    return best;
+}
+
+#define FX_NORM_NV_CASES(LPR, CALL) \
+    case 1: CALL(LPR, 1); break;    \
+    case 2: CALL(LPR, 2); break;    \
+    case 3: CALL(LPR, 3); break;    \
+    case 4: CALL(LPR, 4); break;    \
+    case 6: CALL(LPR, 6); break;    \
+    case 8: CALL(LPR, 8); break;    \
+    case 12: CALL(LPR, 12); break;  \
+    case 16: CALL(LPR, 16); break;
+
+#define FX_NORM_DISPATCH(shape, CALL)                                           \
+    switch (shape.lpr) {                                                        \
+        case 64: switch (shape.nv) { FX_NORM_NV_CASES(64, CALL) } break;        \
+        case 32: switch (shape.nv) { FX_NORM_NV_CASES(32, CALL) } break;        \
+        case 16: switch (shape.nv) { FX_NORM_NV_CASES(16, CALL) } break;        \
+        case 8: switch (shape.nv) { FX_NORM_NV_CASES(8, CALL) } break;          \
+    }
+
+static int64_t bwd_blocks(int64_t N) {
+    // about four strips per CU on a 256-CU part; never more strips than rows
+    const int64_t target = 1024;
+    return N < target ? (N > 0 ? N : 1) : target;
+}
+
+}  // namespace fx
+
+using namespace fx;
+
+static int norm_check(const void* x, const void* w, int64_t N, int32_t D, const char* who) {
+    FX_REQUIRE(x != nullptr && w != nullptr, "%s: null pointer", who);
+    FX_REQUIRE(N >= 0, "%s: N=%lld < 0", who, (long long)N);
+    FX_REQUIRE(D >= 8 && D <= 8192 && D % 8 == 0, "%s: D=%d needs D%%8==0 and 8<=D<=8192", who, D);
+    return 0;
+}
+
+extern "C" int fx_rms_norm_fwd(const uint16_t* x, const uint16_t* w, uint16_t* y, float* rstd,
+                               int64_t N, int32_t D, float eps, void* stream) {
+    if (int e = norm_check(x, w, N, D, "fx_rms_norm_fwd")) return e;
+    FX_REQUIRE(y != nullptr && rstd != nullptr, "fx_rms_norm_fwd: null output");
+    if (N == 0) return 0;
+    const RowShape s = pick_shape(D);
+    const int G = 256 / s.lpr;
+    const int64_t blocks = (N + G - 1) / G;
+    FX_REQUIRE(blocks <= 0x7fffffff, "fx_rms_norm_fwd: N=%lld too large", (long long)N);
+#define FX_CALL(L, V)                                                                       \
+    hipLaunchKernelGGL((rms_fwd_kernel<L, V>), dim3((unsigned)blocks), dim3(256), 0,        \
+                       (hipStream_t)stream, x, w, y, rstd, N, (int)D, eps)
+    FX_NORM_DISPATCH(s, FX_CALL)
+#undef FX_CALL
+    return check_launch("rms_norm_fwd");
+}
+
+extern "C" int64_t fx_rms_norm_bwd_workspace(int64_t N, int32_t D) {
+    if (N <= 0 || D <= 0) return 0;
+    return bwd_blocks(N) * (int64_t)D * (int64_t)sizeof(float);
+}
+
+extern "C" int fx_rms_norm_bwd(const uint16_t* x, const uint16_t* dy, const uint16_t* w,
+                               const float* rstd, uint16_t* dx, float* dw_f32, uint16_t* dw,
+                               float* work, int64_t N, int32_t D, void* stream) {
+    if (int e = norm_check(x, w, N, D, "fx_rms_norm_bwd")) return e;
+    FX_REQUIRE(dy != nullptr && rstd != nullptr && dx != nullptr && dw_f32 != nullptr,
+               "fx_rms_norm_bwd: null pointer");
+    if (N == 0) {
+        // dw of an empty batch is zero
+        hipLaunchKernelGGL(rms_dw_reduce_kernel, dim3((D + 7) / 8), dim3(256), 0,
+                           (hipStream_t)stream, (const float*)nullptr, (int64_t)0, (int)D, dw_f32, dw);
+        return check_launch("rms_dw_reduce");
+    }
+    FX_REQUIRE(work != nullptr, "fx_rms_norm_bwd: null workspace");
+    const RowShape s = pick_shape(D);
+    const int G = 256 / s.lpr;
+    const int64_t P0 = bwd_blocks(N);
+    int64_t rows = (N + P0 - 1) / P0;
+    rows = (rows + G - 1) / G * G;
+    const int64_t P = (N + rows - 1) / rows;  // <= P0, so `work` is large enough
+    const size_t lds = (size_t)D * sizeof(float);
+#define FX_CALL(L, V)                                                                          \
+    hipLaunchKernelGGL((rms_bwd_kernel<L, V>), dim3((unsigned)P), dim3(256), lds,              \
+                       (hipStream_t)stream, x, dy, w, rstd, dx, work, N, (int)D, rows)
+    FX_NORM_DISPATCH(s, FX_CALL)
+#undef FX_CALL
+    if (int e = check_launch("rms_norm_bwd")) return e;
+    hipLaunchKernelGGL(rms_dw_reduce_kernel, dim3((D + 7) / 8), dim3(256), 0, (hipStream_t)stream,
+                       (const float*)work, P, (int)D, dw_f32, dw);
+    return check_launch("rms_dw_reduce");
+}

@@ -1,0 +1,262 @@
+// FlatAdamW step for gfx950: three launches, no host synchronisation.
+//
+//   adamw_sumsq   one fp32 partial sum of g^2 per chunk of kChunk elements
+//   adamw_final   one block: fixed-order fp64 sum of the partials, found_inf, grad
+//                 norm, clip coefficient, step counter and the loss-scale update
+//   adamw_update  the elementwise AdamW update over the flat master/m/v buffers,
+//                 writing the bf16 parameter copy
+//
+// Work is split into equal chunks across all tensors of a list (a chunk never spans
+// two tensors), so small tensors do not pay for the grid of the largest one.
+// A non-finite gradient makes its chunk's partial non-finite (squares are >= 0, inf
+// or nan), so the final sum alone tells whether the step must be skipped, as the
+// reference's separate flag word did (ml/fxlm/kernels/optim.hip:44-51, :85-91).
+#include <math.h>
+
+#include "fx_device.h"
+
+namespace fx {
+
+constexpr int kOptThreads = 256;
+constexpr int kOptVec = 4;                                   // 16-byte vectors per thread
+constexpr int64_t kChunk = (int64_t)kOptThreads * 8 * kOptVec;  // 8192 elements
+
+struct ChunkList {
+    const uint16_t* g[FX_ADAMW_MAX_TENSORS];
+    int64_t off[FX_ADAMW_MAX_TENSORS];
+    int64_t n[FX_ADAMW_MAX_TENSORS];
+    int32_t wd[FX_ADAMW_MAX_TENSORS];
+    int32_t cstart[FX_ADAMW_MAX_TENSORS + 1];  // first chunk of each tensor
+    int32_t count;
+    int32_t pbase;                              // index of this list's first partial
+};
+
+__device__ __forceinline__ int find_tensor(const ChunkList& L, int b) {
+    int t = 0;
+    while (t + 1 < L.count && L.cstart[t + 1] <= b) ++t;
+    return t;
+}
+
+// work layout (fp32): [0] = clip/scale, [1] = skip flag, [2..3] pad, [4..] partials
+constexpr int kWorkHead = 4;
+
+__global__ void __launch_bounds__(kOptThreads) adamw_sumsq_kernel(ChunkList L, float* __restrict__ work) {
+    __shared__ float sh[kOptThreads / 64];
+    const int b = blockIdx.x;
+    const int t = find_tensor(L, b);
+    const uint16_t* g = L.g[t];
+    const int64_t n = L.n[t];
+    const int64_t base = (int64_t)(b - L.cstart[t]) * kChunk;
+    float ss = 0.f;
+    uint4 gv[kOptVec];
+#pragma unroll
+    for (int u = 0; u < kOptVec; ++u) {
+        const int64_t e = base + ((int64_t)u * kOptThreads + threadIdx.x) * 8;
+        gv[u] = make_uint4(0u, 0u, 0u, 0u);
+        if (e + 8 <= n) {
+            gv[u] = ld16(g + e);
+        } else if (e < n) {
+            uint16_t tmp[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            for (int j = 0; j < 8 && e + j < n; ++j) tmp[j] = g[e + j];
+            gv[u] = *reinterpret_cast<uint4*>(tmp);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kOptVec; ++u) {
+        float f[8];
+        unpack8(gv[u], f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
+    }
+    ss = group_sum<64>(ss);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < kOptThreads / 64; ++i) s += sh[i];
+        work[kWorkHead + L.pbase + b] = s;
+    }
+}
+
+__global__ void __launch_bounds__(1024)
+adamw_final_kernel(float* __restrict__ work, int64_t nparts, int32_t* __restrict__ step,
+                   float* __restrict__ found_inf, float* __restrict__ grad_norm,
+                   float* __restrict__ scale, int32_t* __restrict__ growth, float max_norm,
+                   float growth_factor, float backoff_factor, int32_t growth_interval) {
+    __shared__ double sh[16];
+    double s = 0.0;
+    for (int64_t i = threadIdx.x; i < nparts; i += 1024) s += (double)work[kWorkHead + i];
+    s = group_sum_d<64>(s);
+    if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    double tot = 0.0;
+    for (int i = 0; i < 16; ++i) tot += sh[i];
+    const float sumsq = (float)tot;
+    const bool bad = !isfinite(sumsq);
+    const float sc = *scale;
+    const float norm = sqrtf(sumsq) / sc;
+    const float clip = bad ? 0.f : fminf(1.f, max_norm / (norm + 1e-6f));
+    *found_inf = bad ? 1.f : 0.f;
+    *grad_norm = norm;
+    work[0] = clip / sc;
+    work[1] = bad ? 1.f : 0.f;
+    if (!bad) *step += 1;
+    // loss-scale update (semantics of torch._amp_update_scale_)
+    if (bad) {
+        *scale = sc * backoff_factor;
+        *growth = 0;
+    } else {
+        const int32_t ok = *growth + 1;
+        if (ok == growth_interval) {
+            const float ns = sc * growth_factor;
+            if (isfinite(ns)) *scale = ns;
+            *growth = 0;
+        } else {
+            *growth = ok;
+        }
+    }
+}
+
+__device__ __forceinline__ void adamw_elem(float g, float& w, float& m, float& v, float lr, float lrwd,
+                                           float b1, float b2, float b1c, float b2c, float ibc1,
+                                           float ibc2, float eps, bool wd_on) {
+    if (wd_on) w -= lrwd * w;
+    m = m * b1 + b1c * g;
+    v = v * b2 + b2c * g * g;
+    w -= lr * (m * ibc1) / (sqrtf(v * ibc2) + eps);
+}
+
+__global__ void __launch_bounds__(kOptThreads)
+adamw_update_kernel(ChunkList L, const float* __restrict__ work, const int32_t* __restrict__ step,
+                    float* __restrict__ master, float* __restrict__ mom, float* __restrict__ var,
+                    uint16_t* __restrict__ p16, float lr, float b1, float b2, float eps, float wd) {
+    if (work[1] != 0.f) return;  // non-finite gradients: skip the step
+    const int b = blockIdx.x;
+    const int t = find_tensor(L, b);
+    const uint16_t* g = L.g[t];
+    const int64_t n = L.n[t];
+    const int64_t off = L.off[t];
+    const bool wd_on = L.wd[t] != 0;
+    const int64_t base = (int64_t)(b - L.cstart[t]) * kChunk;
+    const float inv = work[0];
+    const int st = *step;
+    const float ibc1 = 1.f / (1.f - powf(b1, (float)st));
+    const float ibc2 = 1.f / (1.f - powf(b2, (float)st));
+    const float b1c = 1.f - b1, b2c = 1.f - b2, lrwd = lr * wd;
+
+#pragma unroll
+    for (int u = 0; u < kOptVec; ++u) {
+        const int64_t e = base + ((int64_t)u * kOptThreads + threadIdx.x) * 8;
+        if (e + 8 <= n) {
+            float gf[8];
+            unpack8(ld16(g + e), gf);
+            float* mp = master + off + e;
+            float* m1 = mom + off + e;
+            float* v1 = var + off + e;
+            float4 w0 = *reinterpret_cast<const float4*>(mp), w1 = *reinterpret_cast<const float4*>(mp + 4);
+            float4 a0 = *reinterpret_cast<const float4*>(m1), a1 = *reinterpret_cast<const float4*>(m1 + 4);
+            float4 c0 = *reinterpret_cast<const float4*>(v1), c1 = *reinterpret_cast<const float4*>(v1 + 4);
+            float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+            float m[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+            float v[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                adamw_elem(gf[j] * inv, w[j], m[j], v[j], lr, lrwd, b1, b2, b1c, b2c, ibc1, ibc2, eps, wd_on);
+            *reinterpret_cast<float4*>(mp) = make_float4(w[0], w[1], w[2], w[3]);
+            *reinterpret_cast<float4*>(mp + 4) = make_float4(w[4], w[5], w[6], w[7]);
+            *reinterpret_cast<float4*>(m1) = make_float4(m[0], m[1], m[2], m[3]);
+            *reinterpret_cast<float4*>(m1 + 4) = make_float4(m[4], m[5], m[6], m[7]);
+            *reinterpret_cast<float4*>(v1) = make_float4(v[0], v[1], v[2], v[3]);
+            *reinterpret_cast<float4*>(v1 + 4) = make_float4(v[4], v[5], v[6], v[7]);
+            st16(p16 + off + e, pack8(w));
+        } else if (e < n) {
+            for (int64_t i = e; i < n; ++i) {
+                float w = master[off + i], m = mom[off + i], v = var[off + i];
+                adamw_elem(bf16_to_f32(g[i]) * inv, w, m, v, lr, lrwd, b1, b2, b1c, b2c, ibc1, ibc2, eps,
+                           wd_on);
+                master[off + i] = w;
+                mom[off + i] = m;
+                var[off + i] = v;
+                p16[off + i] = f32_to_bf16(w);
+            }
+        }
+    }
+}
+
+static int build_chunks(const fxTensorList& in, int32_t pbase, ChunkList& out, int64_t& nchunks) {
+    FX_REQUIRE(in.count >= 0 && in.count <= FX_ADAMW_MAX_TENSORS, "fx_adamw: list count %d out of range",
+               in.count);
+    out.count = in.count;
+    out.pbase = pbase;
+    int64_t c = 0;
+    for (int t = 0; t < in.count; ++t) {
+        FX_REQUIRE(in.n[t] >= 0, "fx_adamw: tensor %d has n=%lld", t, (long long)in.n[t]);
+        FX_REQUIRE(in.off[t] % 8 == 0, "fx_adamw: tensor %d offset %lld not a multiple of 8", t,
+                   (long long)in.off[t]);
+        FX_REQUIRE(in.n[t] == 0 || in.g[t] != nullptr, "fx_adamw: tensor %d has a null gradient", t);
+        FX_REQUIRE(((uintptr_t)in.g[t] & 15) == 0, "fx_adamw: gradient %d not 16-byte aligned", t);
+        out.g[t] = in.g[t];
+        out.off[t] = in.off[t];
+        out.n[t] = in.n[t];
+        out.wd[t] = in.wd[t];
+        out.cstart[t] = (int32_t)c;
+        c += (in.n[t] + kChunk - 1) / kChunk;
+        FX_REQUIRE(c < 0x7fffffff, "fx_adamw: too many chunks");
+    }
+    out.cstart[in.count] = (int32_t)c;
+    nchunks = c;
+    return 0;
+}
+
+}  // namespace fx
+
+using namespace fx;
+
+extern "C" int64_t fx_adamw_workspace(const fxTensorList* lists, int32_t nlists) {
+    int64_t parts = 0;
+    for (int i = 0; i < nlists; ++i)
+        for (int t = 0; t < lists[i].count && t < FX_ADAMW_MAX_TENSORS; ++t)
+            parts += (lists[i].n[t] + kChunk - 1) / kChunk;
+    return (kWorkHead + parts) * (int64_t)sizeof(float);
+}
+
+extern "C" int fx_adamw_step(const fxAdamWState* st, const fxTensorList* lists, int32_t nlists,
+                             void* stream) {
+    FX_REQUIRE(st != nullptr, "fx_adamw_step: null state");
+    FX_REQUIRE(nlists >= 0 && (nlists == 0 || lists != nullptr), "fx_adamw_step: bad lists");
+    FX_REQUIRE(st->master && st->m && st->v && st->p16 && st->step && st->found_inf && st->grad_norm &&
+                   st->scale && st->growth && st->work,
+               "fx_adamw_step: null state pointer");
+    FX_REQUIRE(((uintptr_t)st->master & 31) == 0 && ((uintptr_t)st->m & 31) == 0 &&
+                   ((uintptr_t)st->v & 31) == 0 && ((uintptr_t)st->p16 & 15) == 0,
+               "fx_adamw_step: flat buffers must be 32-byte (fp32) / 16-byte (bf16) aligned");
+    hipStream_t s = (hipStream_t)stream;
+    // At most a few lists: keep their chunk tables on the host stack.
+    FX_REQUIRE(nlists <= 64, "fx_adamw_step: %d lists (max 64)", nlists);
+    ChunkList cl[64];
+    int64_t nch[64];
+    int64_t total = 0;
+    for (int i = 0; i < nlists; ++i) {
+        if (int e = build_chunks(lists[i], (int32_t)total, cl[i], nch[i])) return e;
+        total += nch[i];
+    }
+    for (int i = 0; i < nlists; ++i) {
+        if (nch[i] == 0) continue;
+        hipLaunchKernelGGL(adamw_sumsq_kernel, dim3((unsigned)nch[i]), dim3(kOptThreads), 0, s, cl[i], st->work);
+        if (int e = check_launch("adamw_sumsq")) return e;
+    }
+    hipLaunchKernelGGL(adamw_final_kernel, dim3(1), dim3(1024), 0, s, st->work, total, st->step,
+                       st->found_inf, st->grad_norm, st->scale, st->growth, st->max_grad_norm,
+                       st->growth_factor, st->backoff_factor, st->growth_interval);
+    if (int e = check_launch("adamw_final")) return e;
+    for (int i = 0; i < nlists; ++i) {
+        if (nch[i] == 0) continue;
+        hipLaunchKernelGGL(adamw_update_kernel, dim3((unsigned)nch[i]), dim3(kOptThreads), 0, s, cl[i],
+                           (const float*)st->work, (const int32_t*)st->step, st->master, st->m, st->v,
+                           st->p16, st->lr, st->beta1, st->beta2, st->eps, st->weight_decay);
+        if (int e = check_launch("adamw_update")) return e;
+    }
+    return 0;
+}

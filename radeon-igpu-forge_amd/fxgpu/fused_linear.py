@@ -1,0 +1,134 @@
+"""fxgpu.fused_linear: fused (gather) linear layers on gfx950 bf16 MFMA.
+
+* ``FusedGatherLinear.apply(X16, idx32, weight, bias)`` -- surface of
+  ml/fxgpu/fused_linear.py:27-101: out[b, n] = bias[n] + sum_k Xg[b, k] W[n, k]
+  with Xg[b, w*F + f] = X[idx[b] + w, f] (window-major).  The forward kernel
+  also writes Xg when a gradient is needed; the backward is dW = g^T Xg and
+  db = sum_b g (no dX, as in the reference).
+* ``FusedLinear.apply(x, weight, bias, activation)`` / ``fused_linear`` -- the
+  dense form with the activation fused into the GEMM epilogue, used by the
+  GPT MLP as fc -> GELU(tanh): y = gelu(x W^T + b).  The pre-activation is kept
+  for the backward: dh = dy * gelu'(h) (one elementwise kernel), then dx = dh W
+  and dW = dh^T x on the library GEMM.
+"""
+import torch
+
+from fxgpu.abi import call, ptr, stream_of
+
+_ACTS = {None: 0, "none": 0, "identity": 0, "gelu_tanh": 1}
+
+
+class FusedGatherLinear(torch.autograd.Function):
+    """out[b, n] = sum_k Xg[b, k] * weight[n, k] + bias[n]
+
+    Xg[b, w*F + f] = X[idx[b] + w, f] (window-major flattening).
+    X16: (R, F) bf16 contiguous; idx32: (B,) int32 contiguous;
+    weight: (N, K) bf16 contiguous, K = W*F; bias: (N,) bf16.
+    """
+
+    @staticmethod
+    def forward(ctx, X16, idx32, weight, bias):
+        F = X16.shape[1]
+        K = weight.shape[1]
+        if K % F != 0:
+            raise ValueError(f"weight.shape[1]={K} is not a multiple of X16.shape[1]={F} "
+                             f"(K = window * F)")
+        if F % 8 != 0:
+            raise ValueError("pad F to a multiple of 8 with zero columns "
+                             f"(F={F}; the kernel uses 16-byte loads)")
+        if X16.dtype != torch.bfloat16:
+            raise TypeError(f"X16 must be bfloat16, got {X16.dtype}")
+        if idx32.dtype != torch.int32:
+            raise TypeError(f"idx32 must be int32, got {idx32.dtype}")
+        if weight.dtype != torch.bfloat16 or bias.dtype != torch.bfloat16:
+            raise TypeError("weight and bias must be bfloat16")
+        if not (X16.is_cuda and idx32.is_cuda and weight.is_cuda and bias.is_cuda):
+            raise TypeError("all tensors must be cuda tensors")
+        if not (X16.is_contiguous() and idx32.is_contiguous() and weight.is_contiguous()
+                and bias.is_contiguous()):
+            raise ValueError("all tensors must be contiguous (call .contiguous())")
+        if idx32.dim() != 1:
+            raise ValueError(f"idx32 must be (B,), shape={tuple(idx32.shape)}")
+        if weight.dim() != 2 or bias.dim() != 1 or bias.shape[0] != weight.shape[0]:
+            raise ValueError("weight must be (N,K) and bias (N,)")
+        Bsz = idx32.numel()
+        N = weight.shape[0]
+        C = torch.empty(Bsz, N, device=X16.device, dtype=torch.bfloat16)
+        need_grad = any(ctx.needs_input_grad)
+        # Xg only serves the backward (dW); inference skips the write-out.
+        Xg = torch.empty(Bsz, K, device=X16.device, dtype=torch.bfloat16) if need_grad else None
+        call("fx_linear_fwd", ptr(X16), F, ptr(idx32), F, X16.shape[0], ptr(weight), ptr(bias),
+             ptr(C), None, ptr(Xg), Bsz, N, K, 0, stream_of(X16))
+        if need_grad:
+            ctx.save_for_backward(Xg)
+        return C
+
+    @staticmethod
+    def backward(ctx, g):
+        (Xg,) = ctx.saved_tensors
+        g = g.contiguous()
+        dW = torch.mm(g.t(), Xg)          # (N, K)
+        db = g.sum(0)
+        return None, None, dW, db
+
+
+def fused_gather_linear(X16, idx32, weight, bias):
+    """Thin wrapper over FusedGatherLinear.apply."""
+    return FusedGatherLinear.apply(X16, idx32, weight, bias)
+
+
+class FusedLinear(torch.autograd.Function):
+    """y = act(x W^T + b) for x (..., K) bf16, weight (N, K) bf16, bias (N,) bf16 or None."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, activation):
+        if activation not in _ACTS:
+            raise ValueError(f"activation {activation!r} not in {sorted(k for k in _ACTS if k)}")
+        act = _ACTS[activation]
+        if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 or (
+                bias is not None and bias.dtype != torch.bfloat16):
+            raise TypeError("x, weight and bias must be bfloat16")
+        if not (x.is_cuda and weight.is_cuda):
+            raise TypeError("x and weight must be cuda tensors")
+        K = x.shape[-1]
+        if weight.dim() != 2 or weight.shape[1] != K:
+            raise ValueError(f"weight must be (N, {K}), got {tuple(weight.shape)}")
+        if K % 8 != 0:
+            raise ValueError(f"in_features={K} must be a multiple of 8")
+        if not weight.is_contiguous() or (bias is not None and not bias.is_contiguous()):
+            raise ValueError("weight and bias must be contiguous")
+        N = weight.shape[0]
+        x2 = x.reshape(-1, K)
+        if x2.stride(1) != 1 or x2.stride(0) % 8 or x2.data_ptr() % 16:
+            x2 = x2.contiguous()
+        M = x2.shape[0]
+        y = torch.empty(M, N, device=x.device, dtype=torch.bfloat16)
+        h = torch.empty_like(y) if (act and any(ctx.needs_input_grad)) else None
+        call("fx_linear_fwd", ptr(x2), x2.stride(0), None, 0, 0, ptr(weight), ptr(bias), ptr(y),
+             ptr(h), None, M, N, K, act, stream_of(x))
+        ctx.save_for_backward(x2, weight, h)
+        ctx.act, ctx.has_bias, ctx.xshape = act, bias is not None, x.shape
+        return y.view(*x.shape[:-1], N)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, weight, h = ctx.saved_tensors
+        N = weight.shape[0]
+        dy2 = dy.reshape(-1, N)
+        if dy2.dtype != torch.bfloat16:
+            dy2 = dy2.to(torch.bfloat16)
+        dy2 = dy2.contiguous()
+        if ctx.act:
+            dh = torch.empty_like(dy2)
+            call("fx_gelu_bwd", ptr(dy2), ptr(h), ptr(dh), dh.numel(), stream_of(dy2))
+        else:
+            dh = dy2
+        dx = torch.mm(dh, weight).view(ctx.xshape) if ctx.needs_input_grad[0] else None
+        dW = torch.mm(dh.t(), x2) if ctx.needs_input_grad[1] else None
+        db = dh.sum(0) if (ctx.has_bias and ctx.needs_input_grad[2]) else None
+        return dx, dW, db, None
+
+
+def fused_linear(x, weight, bias=None, activation="gelu_tanh"):
+    """y = activation(x @ weight.T + bias) with the activation fused into the GEMM."""
+    return FusedLinear.apply(x, weight, bias, activation)

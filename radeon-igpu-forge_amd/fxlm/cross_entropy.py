@@ -1,0 +1,205 @@
+"""fxlm.cross_entropy: fused softmax cross-entropy and linear cross-entropy (gfx950).
+
+Surface of ml/fxlm/cross_entropy.py:41-199 with bf16 logits:
+
+* ``fused_cross_entropy(logits, target, ignore_index=-100)``: mean CE over the
+  valid rows; the forward kernel also writes dlogits = (softmax - onehot)/n_valid
+  (one read and one write of the logits), the backward rescales them by the
+  incoming gradient only when it is not 1.
+* ``linear_cross_entropy(x, weight, target, grad_scale=1.0, ...)``: CE(x W^T)
+  whose backward is computed inside the forward, chunk by chunk; each chunk's
+  logits are overwritten in place by their gradient.
+
+n_valid counts targets != ignore_index (out-of-range targets count, but their
+rows get no loss and no gradient); n_valid == 0 gives loss 0 (reference
+behaviour, ml/fxlm/cross_entropy.py:41-44 and ml/fxlm/kernels/ce.hip:43).
+"""
+import ctypes
+
+import torch
+
+from fxgpu.abi import call, fxCEArgs, ptr, stream_of
+
+# rows per linear-CE chunk: bound the chunk's bf16 logits to this many bytes
+_CHUNK_BYTES = 2 << 30
+
+
+def _inv_nvalid(target, ignore_index, grad_scale=None):
+    """(inv_n, mul) device scalars: inv_n = 1/n_valid (0 if none), mul = inv_n*grad_scale."""
+    dev = target.device
+    inv_n = torch.empty((), device=dev, dtype=torch.float32)
+    mul = torch.empty((), device=dev, dtype=torch.float32)
+    gs_ptr, gs_val = None, 1.0
+    if torch.is_tensor(grad_scale):
+        gs_t = grad_scale.detach().to(device=dev, dtype=torch.float32).reshape(())
+        gs_ptr = ptr(gs_t)
+    elif grad_scale is not None:
+        gs_val = float(grad_scale)
+    call("fx_ce_inv_nvalid", ptr(target), target.numel(), int(ignore_index), gs_ptr,
+         float(gs_val), ptr(inv_n), ptr(mul), stream_of(target))
+    return inv_n, mul
+
+
+def _ce_rows(logits, target, grad, row_loss, mul, ignore_index):
+    """One launch over the rows of (C, V) logits: per-row loss and, if grad, dlogits."""
+    N, V = logits.shape
+    a = fxCEArgs()
+    a.logits = logits.data_ptr()
+    a.target = target.data_ptr()
+    a.grad = grad.data_ptr() if grad is not None else None
+    a.row_loss = row_loss.data_ptr()
+    a.mul = mul.data_ptr()
+    a.N, a.V = N, V
+    a.ld = logits.stride(0)
+    a.ldg = grad.stride(0) if grad is not None else V
+    a.ignore_index = int(ignore_index)
+    call("fx_ce_fwd_grad", ctypes.byref(a), stream_of(logits))
+
+
+def _finalize(row_loss, inv_n):
+    loss = torch.empty((), device=row_loss.device, dtype=torch.float32)
+    call("fx_ce_loss_finalize", ptr(row_loss), row_loss.numel(), ptr(inv_n), ptr(loss),
+         stream_of(row_loss))
+    return loss
+
+
+def _check_logits(logits, target):
+    if logits.dtype != torch.bfloat16:
+        raise TypeError(f"logits must be bfloat16, got {logits.dtype}")
+    if not (logits.is_cuda and target.is_cuda):
+        raise TypeError("logits and target must be cuda tensors")
+    if not logits.is_contiguous() or not target.is_contiguous():
+        raise ValueError("logits and target must be contiguous")
+    if target.dtype != torch.int64:
+        raise TypeError(f"target must be int64, got {target.dtype}")
+    if logits.dim() != 2 or target.dim() != 1 or target.shape[0] != logits.shape[0]:
+        raise ValueError(f"expected logits (N,V) and target (N,): "
+                         f"{tuple(logits.shape)} vs {tuple(target.shape)}")
+
+
+class _FusedCE(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, logits, target, ignore_index):
+        _check_logits(logits, target)
+        N, V = logits.shape
+        dev = logits.device
+        inv_n, mul = _inv_nvalid(target, ignore_index)
+        row_loss = torch.empty(N, device=dev, dtype=torch.float32)
+        grad = None
+        if ctx.needs_input_grad[0]:
+            grad = torch.empty(N, V, device=dev, dtype=torch.bfloat16)
+        _ce_rows(logits, target, grad, row_loss, mul, ignore_index)
+        ctx.save_for_backward(grad)
+        ctx.applied = torch.ones((), device=dev, dtype=torch.float32)
+        return _finalize(row_loss, inv_n)
+
+    @staticmethod
+    def backward(ctx, g):
+        (grad,) = ctx.saved_tensors
+        g32 = g.detach().to(torch.float32).reshape(()).contiguous()
+        call("fx_ce_scale_grad", ptr(grad), grad.numel(), ptr(g32), ptr(ctx.applied),
+             stream_of(grad))
+        return grad, None, None
+
+
+def fused_cross_entropy(logits, target, ignore_index=-100):
+    """logits (N,V) bf16, target (N,) int64 -> fp32 scalar: mean CE over valid rows."""
+    return _FusedCE.apply(logits, target, int(ignore_index))
+
+
+def _auto_chunk(D, V):
+    """Rows per chunk so that one chunk's bf16 logits stay within _CHUNK_BYTES."""
+    c = (_CHUNK_BYTES // (2 * max(1, V))) // 256 * 256
+    return max(256, c)
+
+
+def _mm_f32(a, b):
+    """a @ b with fp32 output from bf16 operands (fp32 accumulation in the GEMM)."""
+    try:
+        return torch.mm(a, b, out_dtype=torch.float32)
+    except (RuntimeError, TypeError):
+        return torch.mm(a, b).float()
+
+
+class _LinearCE(torch.autograd.Function):
+    """loss = CE(x @ W.T, target); the (N, V) logits never exist beyond one chunk."""
+
+    @staticmethod
+    def forward(ctx, x, weight, target, grad_scale, ignore_index, chunk_rows):
+        N, D, V = _check_lin(x, weight, target)
+        dev = x.device
+        if chunk_rows is None:
+            chunk_rows = _auto_chunk(D, V)
+        inv_n, mul = _inv_nvalid(target, ignore_index, grad_scale)
+        row_loss = torch.empty(N, device=dev, dtype=torch.float32)
+        dx = torch.empty(N, D, device=dev, dtype=torch.bfloat16)
+        dW = None
+        for r0 in range(0, N, chunk_rows):
+            r1 = min(r0 + chunk_rows, N)
+            xc = x[r0:r1]
+            lg = torch.mm(xc, weight.t())                       # (C, V) bf16
+            _ce_rows(lg, target[r0:r1], lg, row_loss[r0:r1], mul, ignore_index)  # in place
+            torch.mm(lg, weight, out=dx[r0:r1])                 # dx_c
+            part = _mm_f32(lg.t(), xc)                          # (V, D) fp32
+            dW = part if dW is None else dW.add_(part)
+            del lg
+        if dW is None:
+            dW = torch.zeros(V, D, device=dev, dtype=torch.float32)
+        ctx.save_for_backward(dx, dW)
+        ctx.grad_scale = grad_scale
+        ctx.wdtype = weight.dtype
+        return _finalize(row_loss, inv_n)
+
+    @staticmethod
+    def backward(ctx, g):
+        dx, dW = ctx.saved_tensors
+        gs = ctx.grad_scale
+        inv = torch.reciprocal(gs.float()) if torch.is_tensor(gs) else 1.0 / gs
+        gx = dx * (g * inv)
+        gw = (dW * (g * inv)).to(ctx.wdtype)
+        return gx, gw, None, None, None, None
+
+
+def _check_lin(x, weight, target):
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError("x and weight must be bfloat16")
+    if not (x.is_cuda and weight.is_cuda and target.is_cuda):
+        raise TypeError("all tensors must be cuda tensors")
+    if not (x.is_contiguous() and weight.is_contiguous() and target.is_contiguous()):
+        raise ValueError("x, weight and target must be contiguous")
+    if target.dtype != torch.int64:
+        raise TypeError("target must be int64")
+    N, D = x.shape
+    V, Dw = weight.shape
+    if Dw != D or target.shape != (N,):
+        raise ValueError(f"shape mismatch: x{tuple(x.shape)} W{tuple(weight.shape)} "
+                         f"t{tuple(target.shape)}")
+    return N, D, V
+
+
+def _linear_ce_loss_only(x, weight, target, ignore_index, chunk_rows):
+    """No-grad path: neither dx/dW nor dlogits are allocated."""
+    N, D, V = _check_lin(x, weight, target)
+    if chunk_rows is None:
+        chunk_rows = _auto_chunk(D, V)
+    inv_n, _mul = _inv_nvalid(target, ignore_index)
+    row_loss = torch.empty(N, device=x.device, dtype=torch.float32)
+    for r0 in range(0, N, chunk_rows):
+        r1 = min(r0 + chunk_rows, N)
+        lg = torch.mm(x[r0:r1], weight.t())
+        _ce_rows(lg, target[r0:r1], None, row_loss[r0:r1], _mul, ignore_index)
+    return _finalize(row_loss, inv_n)
+
+
+def linear_cross_entropy(x, weight, target, grad_scale=1.0, ignore_index=-100,
+                         chunk_rows=None):
+    """x (N,D) bf16, weight (V,D) bf16, target (N,) int64 -> fp32 scalar loss.
+
+    grad_scale: python float or 0-dim fp32 cuda tensor (loss scale); the
+    gradients carried through the chunks are multiplied by it and divided
+    back out in backward.  chunk_rows: None -> automatic.
+    Without grad, the loss-only path is used (no dx/dW buffers).
+    """
+    if not (torch.is_grad_enabled() and (x.requires_grad or weight.requires_grad)):
+        return _linear_ce_loss_only(x, weight, target, ignore_index, chunk_rows)
+    return _LinearCE.apply(x, weight, target, grad_scale, int(ignore_index), chunk_rows)

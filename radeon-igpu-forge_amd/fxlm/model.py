@@ -1,0 +1,133 @@
+"""fxlm.model: GPTConfig + GPT -- pre-norm transformer trained in bf16 on gfx950.
+
+Block: RMSNorm -> qkv Linear(D -> 3D, no bias) -> flash_attention_qkv on the
+(B,T,3,H,Dh) view (no permute) -> proj Linear -> residual; RMSNorm -> fused
+linear+GELU(tanh) (D -> 4D) -> fc2 -> residual.  Final RMSNorm; LM head = tied
+embedding (or a separate Linear).  Same structure, names and initialisation
+as ml/fxlm/model.py:22-130.  Implementation switches pick the gfx950 kernels
+("flash" / "fused") or the plain PyTorch paths ("sdpa" / "torch") for
+ablation and parity; mlp_impl covers the fused linear layer the reference
+computes as fc followed by F.gelu.
+"""
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as Fn
+from torch import nn
+
+from fxgpu.fused_linear import fused_linear
+
+from .attention import flash_attention_qkv
+from .cross_entropy import linear_cross_entropy
+from .norm import rms_norm
+
+
+@dataclass
+class GPTConfig:
+    vocab_size: int
+    seq_len: int
+    n_layer: int
+    n_head: int
+    d_model: int
+    mlp_ratio: int = 4
+    tie_embeddings: bool = True
+    attn_impl: str = "flash"      # "flash" | "sdpa"
+    norm_impl: str = "fused"      # "fused" | "torch"
+    ce_impl: str = "fused"        # "fused" | "torch"
+    mlp_impl: str = "fused"       # "fused" | "torch"
+    eps: float = 1e-6
+
+
+class Block(nn.Module):
+    def __init__(self, cfg):
+        super().__init__()
+        D, H = cfg.d_model, cfg.n_head
+        self.n_head = H
+        self.head_dim = D // H
+        self.attn_impl = cfg.attn_impl
+        self.norm_impl = cfg.norm_impl
+        self.mlp_impl = cfg.mlp_impl
+        self.eps = cfg.eps
+        self.ln1_w = nn.Parameter(torch.ones(D))
+        self.ln2_w = nn.Parameter(torch.ones(D))
+        self.qkv = nn.Linear(D, 3 * D, bias=False)
+        self.proj = nn.Linear(D, D, bias=False)
+        self.fc = nn.Linear(D, cfg.mlp_ratio * D, bias=False)
+        self.fc2 = nn.Linear(cfg.mlp_ratio * D, D, bias=False)
+
+    def _norm(self, x, w):
+        if self.norm_impl == "fused":
+            return rms_norm(x, w, self.eps)
+        return Fn.rms_norm(x, (x.shape[-1],), w, self.eps)
+
+    def forward(self, x):
+        B, T, D = x.shape
+        h = self._norm(x, self.ln1_w)
+        qkv = self.qkv(h).view(B, T, 3, self.n_head, self.head_dim)
+        if self.attn_impl == "flash":
+            y = flash_attention_qkv(qkv, causal=True)
+        else:
+            q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))   # (B,H,T,Dh)
+            y = Fn.scaled_dot_product_attention(q, k, v, is_causal=True)
+            y = y.transpose(1, 2)
+        x = x + self.proj(y.reshape(B, T, D))
+        h = self._norm(x, self.ln2_w)
+        if self.mlp_impl == "fused":
+            u = fused_linear(h, self.fc.weight, None, "gelu_tanh")
+        else:
+            u = Fn.gelu(self.fc(h), approximate="tanh")
+        return x + self.fc2(u)
+
+
+class GPT(nn.Module):
+    def __init__(self, cfg: GPTConfig):
+        super().__init__()
+        if cfg.d_model % cfg.n_head:
+            raise ValueError("d_model must be a multiple of n_head")
+        self.cfg = cfg
+        D = cfg.d_model
+        self.tok_emb = nn.Embedding(cfg.vocab_size, D)
+        self.pos_emb = nn.Parameter(torch.zeros(cfg.seq_len, D))
+        self.blocks = nn.ModuleList(Block(cfg) for _ in range(cfg.n_layer))
+        self.lnf_w = nn.Parameter(torch.ones(D))
+        if not cfg.tie_embeddings:
+            self.head = nn.Linear(D, cfg.vocab_size, bias=False)
+        self.apply(self._init)
+        # small init for the residual projections (depth scaling)
+        s = 0.02 / math.sqrt(2 * cfg.n_layer)
+        for b in self.blocks:
+            nn.init.normal_(b.proj.weight, std=s)
+            nn.init.normal_(b.fc2.weight, std=s)
+
+    @staticmethod
+    def _init(m):
+        if isinstance(m, (nn.Linear, nn.Embedding)):
+            nn.init.normal_(m.weight, std=0.02)
+
+    def _norm_f(self, x):
+        if self.cfg.norm_impl == "fused":
+            return rms_norm(x, self.lnf_w, self.cfg.eps)
+        return Fn.rms_norm(x, (x.shape[-1],), self.lnf_w, self.cfg.eps)
+
+    def _head_w(self):
+        return self.tok_emb.weight if self.cfg.tie_embeddings else self.head.weight
+
+    def num_params(self):
+        return sum(p.numel() for p in self.parameters())
+
+    def forward(self, idx, targets=None, grad_scale=1.0):
+        B, T = idx.shape
+        if T > self.cfg.seq_len:
+            raise ValueError(f"T={T} > seq_len={self.cfg.seq_len}")
+        x = self.tok_emb(idx) + self.pos_emb[:T]
+        for blk in self.blocks:
+            x = blk(x)
+        x = self._norm_f(x)
+        if targets is None:
+            return Fn.linear(x, self._head_w())
+        if self.cfg.ce_impl == "fused":
+            return linear_cross_entropy(x.reshape(-1, x.shape[-1]), self._head_w(),
+                                        targets.reshape(-1), grad_scale=grad_scale)
+        logits = Fn.linear(x, self._head_w())
+        return Fn.cross_entropy(logits.float().view(-1, logits.shape[-1]), targets.reshape(-1))

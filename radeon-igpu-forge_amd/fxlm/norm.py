@@ -1,0 +1,88 @@
+"""fxlm.norm: fused RMSNorm (bf16 I/O, fp32 math) on gfx950.
+
+y = x * rsqrt(mean(x^2) + eps) * w.  The forward stores rstd (fp32, one per
+row); the backward produces dx and dw from a single pass over x and dy
+(fx_rms_norm_bwd).  Surface and checks follow ml/fxlm/norm.py:30-90.
+"""
+import torch
+
+from fxgpu.abi import call, lib, ptr, stream_of
+
+
+def _check(x, w):
+    if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
+        raise TypeError(f"x and weight must be bfloat16 ({x.dtype}, {w.dtype})")
+    if not (x.is_cuda and w.is_cuda):
+        raise TypeError("x and weight must be cuda tensors")
+    D = x.shape[-1]
+    if w.shape != (D,):
+        raise ValueError(f"weight must have shape ({D},), got {tuple(w.shape)}")
+    if D % 8 != 0 or D > 8192:
+        raise ValueError(f"D={D}: needs D % 8 == 0 and D <= 8192")
+    if not x.is_contiguous() or not w.is_contiguous():
+        raise ValueError("x and weight must be contiguous")
+    return D
+
+
+class _RMSNorm(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, w, eps):
+        D = _check(x, w)
+        N = x.numel() // D
+        x2 = x.view(N, D)
+        y = torch.empty_like(x2)
+        rstd = torch.empty(N, device=x.device, dtype=torch.float32)
+        call("fx_rms_norm_fwd", ptr(x2), ptr(w), ptr(y), ptr(rstd), N, D, float(eps),
+             stream_of(x))
+        ctx.save_for_backward(x2, w, rstd)
+        ctx.eps = eps
+        ctx.oshape = x.shape
+        return y.view(x.shape)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, w, rstd = ctx.saved_tensors
+        N, D = x2.shape
+        dy2 = dy.contiguous().view(N, D)
+        if dy2.dtype != torch.bfloat16:
+            dy2 = dy2.to(torch.bfloat16)
+        dx = torch.empty_like(x2)
+        dw32 = torch.empty(D, device=x2.device, dtype=torch.float32)
+        dw = torch.empty(D, device=x2.device, dtype=w.dtype)
+        nbytes = lib().fx_rms_norm_bwd_workspace(N, D)
+        work = torch.empty(max(1, nbytes // 4), device=x2.device, dtype=torch.float32)
+        call("fx_rms_norm_bwd", ptr(x2), ptr(dy2), ptr(w), ptr(rstd), ptr(dx), ptr(dw32),
+             ptr(dw), ptr(work), N, D, stream_of(x2))
+        return dx.view(ctx.oshape), dw, None
+
+
+def rms_norm(x, weight, eps=1e-6):
+    """x (..., D) bf16, weight (D,) bf16 -> y (..., D) bf16."""
+    return _RMSNorm.apply(x, weight, float(eps))
+
+
+def rms_norm_fwd_stats(x, weight, eps=1e-6):
+    """Forward only, returning (y, rstd): the fp32 per-row rstd for parity checks."""
+    D = _check(x, weight)
+    N = x.numel() // D
+    x2 = x.view(N, D)
+    y = torch.empty_like(x2)
+    rstd = torch.empty(N, device=x.device, dtype=torch.float32)
+    call("fx_rms_norm_fwd", ptr(x2), ptr(weight), ptr(y), ptr(rstd), N, D, float(eps),
+         stream_of(x))
+    return y.view(x.shape), rstd
+
+
+def rms_norm_bwd_raw(x, dy, weight, rstd):
+    """Backward only, returning (dx, dw_f32, dw_bf16) for parity checks."""
+    D = _check(x, weight)
+    N = x.numel() // D
+    x2, dy2 = x.view(N, D), dy.contiguous().view(N, D)
+    dx = torch.empty_like(x2)
+    dw32 = torch.empty(D, device=x.device, dtype=torch.float32)
+    dw = torch.empty(D, device=x.device, dtype=torch.bfloat16)
+    work = torch.empty(max(1, lib().fx_rms_norm_bwd_workspace(N, D) // 4), device=x.device,
+                       dtype=torch.float32)
+    call("fx_rms_norm_bwd", ptr(x2), ptr(dy2), ptr(weight), ptr(rstd), ptr(dx), ptr(dw32),
+         ptr(dw), ptr(work), N, D, stream_of(x))
+    return dx.view(x.shape), dw32, dw

@@ -1,0 +1,97 @@
+"""The C-ABI library: it loads, exports every function of include/fx_abi.h, its
+struct layouts match the ctypes mirrors, and argument checks reject bad input
+before anything reaches the GPU (CPU only)."""
+import ctypes
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "fx_abi.h")
+
+
+@pytest.fixture(scope="module")
+def abi():
+    from fxgpu import abi as _abi
+    srcs = os.path.join(ROOT, "radeon-igpu-forge_amd", "csrc")
+    newest = max(os.path.getmtime(os.path.join(srcs, f)) for f in os.listdir(srcs)
+                 if f.endswith((".hip", ".h")))
+    newest = max(newest, os.path.getmtime(HEADER))
+    if not os.path.exists(_abi.LIB_PATH) or os.path.getmtime(_abi.LIB_PATH) < newest:
+        subprocess.run(["python", os.path.join(srcs, "build.py")], check=True)
+    return _abi
+
+
+def header_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?(?:int|int64_t|char\s*\*|void)\s*\*?\s*(fx_\w+)\s*\(",
+                                 text, re.M)))
+
+
+def test_header_and_ctypes_agree(abi):
+    assert header_functions() == sorted(abi.SIGNATURES)
+
+
+def test_library_exports_every_symbol(abi):
+    lib = abi.lib()
+    for name in header_functions():
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", abi.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r" T (fx_\w+)", out))
+    assert set(header_functions()) <= exported
+    assert lib.fx_abi_version() == abi.FX_ABI_VERSION
+
+
+STRUCTS = ["fxCEArgs", "fxTensorList", "fxAdamWState", "fxAttnArgs"]
+
+
+def test_struct_layout_matches_c(abi, tmp_path):
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
+    for s in STRUCTS:
+        cls = getattr(abi, s)
+        lines.append(f'printf("{s} %zu\\n", sizeof({s}));')
+        for f, _t in cls._fields_:
+            lines.append(f'printf("{s}.{f} %zu\\n", offsetof({s}, {f}));')
+    lines += ["return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-o", str(exe), str(src)], check=True)
+    got = dict(l.rsplit(" ", 1) for l in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                         check=True).stdout.split("\n") if l)
+    for s in STRUCTS:
+        cls = getattr(abi, s)
+        assert int(got[s]) == ctypes.sizeof(cls), s
+        for f, _t in cls._fields_:
+            assert int(got[f"{s}.{f}"]) == getattr(cls, f).offset, f"{s}.{f}"
+
+
+def test_argument_checks_reject_before_launch(abi):
+    lib = abi.lib()
+    fake = ctypes.c_void_p(4096)     # never dereferenced: the checks fail first
+    rc = lib.fx_rms_norm_fwd(fake, fake, fake, fake, 4, 7, 1e-6, None)
+    assert rc == abi.FX_EINVAL and b"D=7" in lib.fx_last_error()
+    assert lib.fx_ce_fwd_grad(None, None) == abi.FX_EINVAL
+    a = abi.fxAttnArgs()
+    a.D, a.B, a.T, a.H = 96, 1, 1, 1
+    assert lib.fx_attn_fwd(ctypes.byref(a), None) == abi.FX_EINVAL
+    assert b"head_dim 96" in lib.fx_last_error()
+    tl = abi.fxTensorList()
+    tl.count = 65
+    st = abi.fxAdamWState()
+    assert lib.fx_adamw_step(ctypes.byref(st), ctypes.byref(tl), 1, None) == abi.FX_EINVAL
+    assert lib.fx_rms_norm_bwd_workspace(65536, 768) == 1024 * 768 * 4
+
+
+def test_adamw_workspace_counts_chunks(abi):
+    tl = abi.fxTensorList()
+    tl.count = 3
+    for i, n in enumerate((8192, 8193, 1)):
+        tl.n[i] = n
+    # 1 + 2 + 1 chunks of 8192 elements, plus the 4-float header
+    assert abi.lib().fx_adamw_workspace(ctypes.byref(tl), 1) == (4 + 4) * 4

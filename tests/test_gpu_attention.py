@@ -1,0 +1,109 @@
+"""Flash attention on the GPU (fx_attn_fwd / fx_attn_bwd) against the oracle and fixtures.
+
+Tolerance: outputs and gradients within 2e-2 max-abs of the fp64 oracle
+(bf16 inputs), lse within 1e-3 relative.
+"""
+import math
+
+import pytest
+import torch
+
+from golden_util import bf16, f32, load
+from oracle import attention as oatt
+from tolerances import ATOL_BF16, max_abs
+
+pytestmark = pytest.mark.gpu
+
+
+def _fwd_bwd(q, k, v, do, causal, scale):
+    from fxlm.attention import attention_fwd_raw, flash_attention
+    qq, kk, vv = (t.clone().requires_grad_() for t in (q, k, v))
+    o = flash_attention(qq, kk, vv, causal=causal, scale=scale)
+    o.backward(do)
+    _, lse = attention_fwd_raw(q, k, v, causal, scale)
+    torch.cuda.synchronize()
+    return o, lse, qq.grad, kk.grad, vv.grad
+
+
+def _check(got, ref):
+    o, lse, dq, dk, dv = got
+    ro, rl, rdq, rdk, rdv = ref
+    assert max_abs(o, ro) <= ATOL_BF16
+    fin = torch.isfinite(rl)
+    assert float((lse.cpu().double() - rl.double()).abs()[fin].max()) <= 1e-3 * max(1.0, float(rl[fin].abs().max()))
+    for a, b in ((dq, rdq), (dk, rdk), (dv, rdv)):
+        assert max_abs(a, b) <= ATOL_BF16
+
+
+@pytest.mark.parametrize("name", ["attn_t37_d64_causal", "attn_t33_d128_full", "attn_t130_d64_causal"])
+def test_golden(dev, name):
+    d = load(name)
+    q, k, v, do = (bf16(d[x], dev) for x in ("q", "k", "v", "do"))
+    got = _fwd_bwd(q, k, v, do, bool(d["causal"]), float(d["scale"]))
+    _check(got, [f32(d[x]) for x in ("o", "lse", "dq", "dk", "dv")])
+
+
+CASES = [(1, 1, 1, 64), (1, 17, 1, 64), (2, 64, 2, 64), (1, 100, 8, 64), (3, 256, 8, 64),
+         (2, 513, 2, 64), (1, 130, 4, 128), (2, 200, 8, 128), (1, 33, 1, 128)]
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("B,T,H,Dh", CASES)
+def test_against_oracle(dev, causal, B, T, H, Dh):
+    # ml/fxlm/selftest.py:286-318: q/k/v are strided views of one (B,T,3,H,Dh) buffer
+    torch.manual_seed(B * 7 + T * 13 + Dh)
+    scale = 1.0 / math.sqrt(Dh)
+    qkv = torch.randn(B, T, 3, H, Dh).bfloat16()
+    do = torch.randn(B, T, H, Dh).bfloat16()
+    qg = qkv.to(dev)
+    got = _fwd_bwd(qg[:, :, 0], qg[:, :, 1], qg[:, :, 2], do.to(dev), causal, scale)
+    q, k, v = qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2]
+    ro, rl = oatt.attn_fwd(q, k, v, causal, scale)
+    rdq, rdk, rdv = oatt.attn_bwd(q, k, v, got[0].cpu(), rl, do, causal, scale)
+    _check(got, (ro, rl, rdq, rdk, rdv))
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_qkv_variant(dev, causal):
+    from fxlm.attention import flash_attention_qkv
+    torch.manual_seed(5)
+    B, T, H, Dh = 2, 100, 4, 64
+    qkv = torch.randn(B, T, 3, H, Dh).bfloat16()
+    x = qkv.to(dev).requires_grad_()
+    o = flash_attention_qkv(x, causal=causal)
+    do = torch.randn(B, T, H, Dh).bfloat16()
+    o.backward(do.to(dev))
+    q, k, v = qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2]
+    ro, rl = oatt.attn_fwd(q, k, v, causal)
+    rdq, rdk, rdv = oatt.attn_bwd(q, k, v, o.detach().cpu(), rl, do, causal)
+    assert max_abs(o, ro) <= ATOL_BF16
+    for i, r in enumerate((rdq, rdk, rdv)):
+        assert max_abs(x.grad[:, :, i], r) <= ATOL_BF16
+
+
+def test_single_key_closed_form(dev):
+    from fxlm.attention import flash_attention
+    torch.manual_seed(2)
+    q, k, v = (torch.randn(3, 1, 2, 64, device=dev).bfloat16().requires_grad_() for _ in range(3))
+    o = flash_attention(q, k, v)
+    o.backward(torch.ones_like(o))
+    assert torch.equal(o, v.detach())                     # one key: O = V exactly
+    assert float(q.grad.abs().max()) == 0.0 and float(k.grad.abs().max()) == 0.0
+
+
+def test_cfg2_full_size(dev):
+    # cfg2: [16, 12, 1024, 64] causal bf16 ~ N(0,1); fp32 oracle math on two batch entries
+    from fxlm.attention import attention_fwd_raw, flash_attention
+    g = torch.Generator(device=dev).manual_seed(2)
+    B, T, H, Dh = 16, 1024, 12, 64
+    q, k, v, do = (torch.randn(B, T, H, Dh, device=dev, generator=g).bfloat16() for _ in range(4))
+    qq, kk, vv = (t.clone().requires_grad_() for t in (q, k, v))
+    o = flash_attention(qq, kk, vv, causal=True)
+    o.backward(do)
+    _, lse = attention_fwd_raw(q, k, v, True)
+    for b in (0, B - 1):
+        sl = slice(b, b + 1)
+        ro, rl = oatt.attn_fwd(q[sl], k[sl], v[sl], True, dtype=torch.float32)
+        rdq, rdk, rdv = oatt.attn_bwd(q[sl], k[sl], v[sl], o[sl].detach(), rl, do[sl], True,
+                                      dtype=torch.float32)
+        _check((o[sl], lse[sl], qq.grad[sl], kk.grad[sl], vv.grad[sl]), (ro, rl, rdq, rdk, rdv))

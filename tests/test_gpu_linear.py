@@ -1,0 +1,115 @@
+"""Fused (gather) linear layers on the GPU (fx_linear_fwd / fx_gelu_bwd) against the oracle.
+
+Tolerance: outputs and gradients within 2e-2 max-abs of the fp64 oracle, or
+2e-2 of the largest |value| for sums over many rows (dW, db).
+"""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from golden_util import bf16, f32, load
+from oracle import linear as olin
+from tolerances import ATOL_BF16, max_abs
+
+pytestmark = pytest.mark.gpu
+
+
+def _rel_tol(ref):
+    return max(ATOL_BF16, 2e-2 * float(ref.abs().max()))
+
+
+def test_golden_gather(dev):
+    from fxgpu.fused_linear import FusedGatherLinear
+    d = load("gather_linear")
+    X, W, b = bf16(d["X"], dev), bf16(d["W"], dev).requires_grad_(), bf16(d["bias"], dev).requires_grad_()
+    idx = torch.from_numpy(d["idx"]).to(dev)
+    out = FusedGatherLinear.apply(X, idx, W, b)
+    out.backward(bf16(d["gout"], dev))
+    assert max_abs(out, f32(d["out"])) <= ATOL_BF16
+    assert max_abs(W.grad, f32(d["dW"])) <= _rel_tol(f32(d["dW"]))
+    assert max_abs(b.grad, f32(d["db"])) <= _rel_tol(f32(d["db"]))
+
+
+def test_golden_linear_gelu(dev):
+    from fxgpu.fused_linear import fused_linear
+    d = load("linear_gelu")
+    x, W = bf16(d["x"], dev).requires_grad_(), bf16(d["W"], dev).requires_grad_()
+    y = fused_linear(x, W, None, "gelu_tanh")
+    y.backward(bf16(d["dy"], dev))
+    assert max_abs(y, f32(d["y"])) <= ATOL_BF16
+    assert max_abs(x.grad, f32(d["dx"])) <= ATOL_BF16
+    assert max_abs(W.grad, f32(d["dW"])) <= _rel_tol(f32(d["dW"]))
+
+
+def test_reference_selftest_gather(dev):
+    # ml/fxgpu/selftest.py:22-69: R=100k, F=40, W=30, HID=256, B=8192
+    from fxgpu.fused_linear import FusedGatherLinear, fused_gather_linear
+    torch.manual_seed(0)
+    R, Fe, Wn, HID, B = 100_000, 40, 30, 256, 8192
+    K = Wn * Fe
+    X = torch.randn(R, Fe, device=dev).bfloat16()
+    weight = (torch.randn(HID, K, device=dev) * 0.03).bfloat16()
+    bias = (torch.randn(HID, device=dev) * 0.01).bfloat16()
+    idx = torch.randint(0, R - Wn + 1, (B,), device=dev, dtype=torch.int32)
+    xb = X.unfold(0, Wn, 1)[idx.long()].transpose(1, 2).reshape(B, K)
+    w_r, b_r = weight.clone().requires_grad_(), bias.clone().requires_grad_()
+    out_r = F.linear(xb.float(), w_r.float(), b_r.float())
+    w_f, b_f = weight.clone().requires_grad_(), bias.clone().requires_grad_()
+    out_f = fused_gather_linear(X, idx, w_f, b_f)
+    assert float((out_f.double() - out_r.double()).abs().max()) < 0.05
+    g = torch.randn(B, HID, device=dev).bfloat16()
+    out_f.backward(g)
+    dW_r = torch.mm(g.t(), xb)           # the reference's backward on the unfolded rows
+    assert float((w_f.grad.double() - dW_r.double()).abs().max()) < 1e-3
+    assert float((b_f.grad.double() - g.sum(0).double()).abs().max()) < 1e-3
+    bad = torch.randn(1000, 37, device=dev).bfloat16()
+    with pytest.raises(ValueError, match="multiple of 8"):
+        FusedGatherLinear.apply(bad, idx[:8].clamp(max=1000 - Wn),
+                                torch.randn(HID, 37 * Wn, device=dev).bfloat16(), bias)
+    with torch.no_grad():                # no grad: no Xg write-out, same result
+        out_i = fused_gather_linear(X, idx, weight, bias)
+    assert torch.equal(out_i, out_f.detach())
+
+
+def test_gather_window_outside_reads_zero(dev):
+    from fxgpu.fused_linear import fused_gather_linear
+    X = torch.randn(20, 8, device=dev).bfloat16()
+    W = torch.randn(4, 24, device=dev).bfloat16()
+    b = torch.zeros(4, device=dev).bfloat16()
+    idx = torch.tensor([0, 17, -1, 18], device=dev, dtype=torch.int32)   # windows of 3 rows
+    out = fused_gather_linear(X, idx, W, b)
+    assert float(out[2].abs().max()) == 0.0 and float(out[3].abs().max()) == 0.0
+    assert float(out[1].abs().max()) > 0.0
+
+
+@pytest.mark.parametrize("M,K,N,bias", [(300, 768, 3072, False), (77, 40, 100, True), (1, 8, 1, True),
+                                        (513, 256, 129, False)])
+def test_linear_gelu_against_oracle(dev, M, K, N, bias):
+    from fxgpu.fused_linear import fused_linear
+    torch.manual_seed(M + K + N)
+    x = torch.randn(M, K).bfloat16()
+    W = (torch.randn(N, K) * K ** -0.5).bfloat16()
+    b = (torch.randn(N) * 0.1).bfloat16() if bias else None
+    dy = torch.randn(M, N).bfloat16()
+    xg, Wg = x.to(dev).requires_grad_(), W.to(dev).requires_grad_()
+    bg = b.to(dev).requires_grad_() if bias else None
+    y = fused_linear(xg, Wg, bg, "gelu_tanh")
+    y.backward(dy.to(dev))
+    ry, rh = olin.linear_act_fwd(x, W, b)
+    rdx, rdW, rdb = olin.linear_act_bwd(x, W, rh, dy)
+    assert max_abs(y, ry) <= ATOL_BF16
+    assert max_abs(xg.grad, rdx) <= _rel_tol(rdx)
+    assert max_abs(Wg.grad, rdW) <= _rel_tol(rdW)
+    if bias:
+        assert max_abs(bg.grad, rdb) <= _rel_tol(rdb)
+
+
+def test_cfg5_mlp_shape(dev):
+    # the GPT MLP fc at cfg5: (16384 x 768) . (3072 x 768)^T -> GELU, vs fp32 torch math
+    from fxgpu.fused_linear import fused_linear
+    g = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn(16384, 768, device=dev, generator=g).bfloat16()
+    W = (torch.randn(3072, 768, device=dev, generator=g) * 0.02).bfloat16()
+    y = fused_linear(x, W, None, "gelu_tanh")
+    ref = F.gelu(x.float() @ W.float().t(), approximate="tanh")
+    assert float((y.float() - ref).abs().max()) <= ATOL_BF16

@@ -1,0 +1,80 @@
+"""RMSNorm on the GPU (fx_rms_norm_fwd / fx_rms_norm_bwd) against the oracle and fixtures."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from golden_util import bf16, f32, load
+from oracle import norm as onorm
+from tolerances import RTOL_NORM, bf16_close, rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(x, w, dy, eps=1e-6):
+    from fxlm.norm import rms_norm_bwd_raw, rms_norm_fwd_stats
+    y, rstd = rms_norm_fwd_stats(x, w, eps)
+    dx, dw32, dw = rms_norm_bwd_raw(x, dy, w, rstd)
+    torch.cuda.synchronize()
+    return y, rstd, dx, dw32, dw
+
+
+def test_golden(dev):
+    d = load("rms_n7_d768")
+    y, rstd, dx, dw32, dw = _run(bf16(d["x"], dev), bf16(d["w"], dev), bf16(d["dy"], dev))
+    assert bf16_close(y, f32(d["y"])) and bf16_close(dx, f32(d["dx"]))
+    assert rel_err(rstd, f32(d["rstd"])) < RTOL_NORM
+    assert rel_err(dw32, f32(d["dw"])) < RTOL_NORM
+    assert torch.equal(dw.cpu(), dw32.cpu().bfloat16())
+
+
+@pytest.mark.parametrize("N,D", [(4, 8), (37, 64), (129, 768), (1000, 512), (300, 8192),
+                                 (5, 1032), (3, 96)])
+def test_against_oracle(dev, N, D):
+    # the reference selftest's cases (ml/fxlm/selftest.py:186-204) plus odd row shapes
+    torch.manual_seed(N * 1000 + D)
+    x = (torch.randn(N, D) * 3).bfloat16()
+    w = (torch.randn(D) * 0.5 + 1).bfloat16()
+    dy = torch.randn(N, D).bfloat16()
+    y, rstd, dx, dw32, _dw = _run(x.to(dev), w.to(dev), dy.to(dev))
+    yr, rr = onorm.rms_norm_fwd(x, w, 1e-6)
+    dxr, dwr = onorm.rms_norm_bwd(x, dy, w, rr)
+    assert bf16_close(y, yr) and bf16_close(dx, dxr)
+    assert rel_err(rstd, rr) < RTOL_NORM and rel_err(dw32, dwr) < RTOL_NORM
+
+
+def test_autograd_path(dev):
+    from fxlm.norm import rms_norm
+    torch.manual_seed(1)
+    x = torch.randn(2, 9, 768, device=dev).bfloat16().requires_grad_()
+    w = (torch.randn(768, device=dev) * 0.1 + 1).bfloat16().requires_grad_()
+    y = rms_norm(x, w)
+    g = torch.randn_like(y)
+    y.backward(g)
+    xr, wr = x.detach().float().requires_grad_(), w.detach().float().requires_grad_()
+    F.rms_norm(xr, (768,), wr, 1e-6).backward(g.float())
+    assert y.shape == x.shape and x.grad.dtype == torch.bfloat16 and w.grad.dtype == torch.bfloat16
+    assert bf16_close(x.grad, xr.grad) and bf16_close(w.grad, wr.grad)
+
+
+def test_empty_batch(dev):
+    x = torch.empty(0, 64, device=dev, dtype=torch.bfloat16)
+    w = torch.ones(64, device=dev, dtype=torch.bfloat16)
+    y, rstd, dx, dw32, dw = _run(x, w, x)
+    assert y.shape == (0, 64) and float(dw32.abs().max()) == 0.0
+
+
+def test_cfg4_full_size(dev):
+    # cfg4: x (65536, 768) ~ N(0,1), w ~ N(1, 0.1); checked against fp32 torch math
+    g = torch.Generator(device=dev).manual_seed(4)
+    N, D = 65536, 768
+    x = torch.randn(N, D, device=dev, generator=g).bfloat16()
+    w = (torch.randn(D, device=dev, generator=g) * 0.1 + 1).bfloat16()
+    dy = torch.randn(N, D, device=dev, generator=g).bfloat16()
+    y, rstd, dx, dw32, _ = _run(x, w, dy)
+    xr, wr = x.float().requires_grad_(), w.float().requires_grad_()
+    yr = F.rms_norm(xr, (D,), wr, 1e-6)
+    yr.backward(dy.float())
+    rr = torch.rsqrt(x.float().pow(2).mean(-1) + 1e-6)
+    assert float((y.float() - yr).abs().max()) <= 2e-2
+    assert float((dx.float() - xr.grad).abs().max()) <= 2e-2
+    assert rel_err(rstd, rr) < RTOL_NORM and rel_err(dw32, wr.grad) < RTOL_NORM
