@@ -1,0 +1,280 @@
+"""Benchmark: the fxlm GPT 12L-d768 training step on one MI355X, plus the hot-path kernels.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+Workload: GPT with 12 layers, d_model 768, 12 heads of
+64, RMSNorm (fused), fused-linear GELU MLP 3072, vocab 50304, causal S=1024,
+batch 16, tied head; all bf16 with FlatAdamW (fp32 master, lr 6e-4, betas
+(0.9, 0.95), eps 1e-8, wd 0.1, clip 1.0).  Tokens are uniform random from a
+seed, weights N(0, 0.02): synthetic data, random init.  One step = forward +
+backward + optimiser step over 16,384 tokens; K steps are timed after W
+warm-up steps, bracketed by torch.cuda.synchronize().
+
+Also measured in the same run, each with HIP events on the stream the kernels
+are launched on (torch's current stream):
+  attention cfg2 [16,12,1024,64] causal: fx_attn_fwd and fx_attn_bwd
+  cross-entropy cfg3 [16384, 50304]: fused forward + backward
+  RMSNorm cfg4 [65536, 768]: forward and backward
+  FlatAdamW cfg4: one step over 124,373,760 parameters
+  fused linear + GELU: the cfg5 MLP fc (16384 x 768 x 3072)
+and, on the host CPU, the reference's naive-PyTorch fp32 training step
+(oracle/gpt.py) on a bounded sample.  Prints ONE JSON line.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "radeon-igpu-forge_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2516.6      # MI355X dense bf16 MFMA, TFLOP/s
+
+CFG5 = dict(vocab_size=50304, seq_len=1024, n_layer=12, n_head=12, d_model=768, batch=16)
+
+
+def _events(torch):
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def time_us(torch, fn, iters=20, warm=5):
+    """Average duration (us) of fn() over `iters` runs, HIP events on the current stream."""
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    s, e = _events(torch)
+    s.record()
+    for _ in range(iters):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / iters * 1e3
+
+
+def bench_attention(torch):
+    from fxlm.attention import _bwd, _fwd
+    B, T, H, D = 16, 1024, 12, 64
+    g = torch.Generator(device="cuda").manual_seed(2)
+    q, k, v, do = (torch.randn(B, T, H, D, device="cuda", generator=g).bfloat16() for _ in range(4))
+    scale = 1.0 / math.sqrt(D)
+    o, lse = _fwd(q, k, v, True, scale)
+    dq, dk, dv = (torch.empty_like(q) for _ in range(3))
+    t_fwd = time_us(torch, lambda: _fwd(q, k, v, True, scale))
+    t_bwd = time_us(torch, lambda: _bwd(q, k, v, o, lse, do, True, scale, dq, dk, dv))
+    f_fwd = 4.0 * B * H * T * T * D * 0.5          # causal half of QK^T and PV
+    f_bwd = 2.5 * f_fwd                            # dV, dP, dK, dQ (+ recomputed S)
+    return {
+        "shape": [B, T, H, D], "causal": True,
+        "fwd_us": round(t_fwd, 2), "bwd_us": round(t_bwd, 2),
+        "fwd_tflops": round(f_fwd / t_fwd / 1e6, 1), "bwd_tflops": round(f_bwd / t_bwd / 1e6, 1),
+        "fwdbwd_tflops": round((f_fwd + f_bwd) / (t_fwd + t_bwd) / 1e6, 1),
+        "fwdbwd_frac_of_bf16_peak": round((f_fwd + f_bwd) / (t_fwd + t_bwd) / 1e6 / BF16_PEAK_TFLOPS, 4),
+        "flop_fwd": f_fwd, "flop_bwd": f_bwd,
+    }
+
+
+def bench_ce(torch):
+    from fxlm.cross_entropy import fused_cross_entropy
+    N, V = 16384, 50304
+    g = torch.Generator(device="cuda").manual_seed(3)
+    lg = (torch.randn(N, V, device="cuda", generator=g) * 2).bfloat16().requires_grad_()
+    tg = torch.randint(0, V, (N,), device="cuda", generator=g)
+    tg[torch.rand(N, device="cuda", generator=g) < 0.05] = -100
+
+    def fb():
+        fused_cross_entropy(lg, tg).backward()
+        lg.grad = None
+    t = time_us(torch, fb, iters=10, warm=3)
+    nbytes = 2 * N * V * 2 + N * 8                 # read logits once, write dlogits once, targets
+    del lg
+    return {"shape": [N, V], "fwdbwd_us": round(t, 2), "gbs": round(nbytes / t / 1e3, 1),
+            "frac_of_hbm": round(nbytes / t / 1e3 / HBM_PEAK_GBS, 4), "bytes": nbytes}
+
+
+def bench_norm(torch):
+    from fxlm.norm import rms_norm_bwd_raw, rms_norm_fwd_stats
+    N, D = 65536, 768
+    g = torch.Generator(device="cuda").manual_seed(4)
+    x = torch.randn(N, D, device="cuda", generator=g).bfloat16()
+    w = (torch.randn(D, device="cuda", generator=g) * 0.1 + 1).bfloat16()
+    dy = torch.randn(N, D, device="cuda", generator=g).bfloat16()
+    _, rstd = rms_norm_fwd_stats(x, w)
+    tf = time_us(torch, lambda: rms_norm_fwd_stats(x, w))
+    tb = time_us(torch, lambda: rms_norm_bwd_raw(x, dy, w, rstd))
+    bf = N * D * 2 * 2 + N * 4 + D * 2             # x read, y write, rstd, w
+    bb = N * D * 2 * 3 + N * 4 + D * 2 + D * 4     # x, dy read, dx write, rstd, w, dw
+    return {"shape": [N, D], "fwd_us": round(tf, 2), "bwd_us": round(tb, 2),
+            "fwd_gbs": round(bf / tf / 1e3, 1), "bwd_gbs": round(bb / tb / 1e3, 1),
+            "fwd_frac_of_hbm": round(bf / tf / 1e3 / HBM_PEAK_GBS, 4),
+            "bwd_frac_of_hbm": round(bb / tb / 1e3 / HBM_PEAK_GBS, 4)}
+
+
+def bench_adamw(torch):
+    from torch import nn
+
+    from fxlm.optim import FlatAdamW
+    n = 124373760
+
+    class Flat(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.w = nn.Parameter(torch.empty(n // 768, 768, device="cuda").normal_(0, 0.02))
+
+    m = Flat()
+    opt = FlatAdamW(m, lr=6e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0,
+                    init_scale=1.0)
+    g = torch.Generator(device="cuda").manual_seed(5)
+    opt.m.normal_(0, 1e-4, generator=g)
+    opt.v.normal_(0, 1e-6, generator=g).abs_()
+    opt._step_ctr.fill_(99)
+    m.w.grad = (torch.randn(n // 768, 768, device="cuda", generator=g) * 1e-3).bfloat16()
+    t = time_us(torch, lambda: opt.step(lr=6e-4), iters=10, warm=3)
+    nbytes = 30 * n
+    del opt, m
+    return {"params": n, "step_us": round(t, 2), "gbs": round(nbytes / t / 1e3, 1),
+            "frac_of_hbm": round(nbytes / t / 1e3 / HBM_PEAK_GBS, 4), "bytes": nbytes}
+
+
+def bench_linear(torch):
+    from fxgpu.fused_linear import fused_linear
+    M, K, N = 16384, 768, 3072
+    g = torch.Generator(device="cuda").manual_seed(6)
+    x = torch.randn(M, K, device="cuda", generator=g).bfloat16()
+    W = (torch.randn(N, K, device="cuda", generator=g) * 0.02).bfloat16()
+    with torch.no_grad():
+        t = time_us(torch, lambda: fused_linear(x, W, None, "gelu_tanh"))
+        t_ref = time_us(torch, lambda: torch.nn.functional.gelu(x @ W.t(), approximate="tanh"))
+    f = 2.0 * M * K * N
+    return {"shape": [M, K, N], "fwd_us": round(t, 2), "tflops": round(f / t / 1e6, 1),
+            "frac_of_bf16_peak": round(f / t / 1e6 / BF16_PEAK_TFLOPS, 4),
+            "hipblaslt_mm_plus_gelu_us": round(t_ref, 2)}
+
+
+def gpu_step_bench(torch, steps, warmup):
+    from fxlm.model import GPT, GPTConfig
+    from fxlm.optim import FlatAdamW
+    c = CFG5
+    torch.manual_seed(0)
+    cfg = GPTConfig(vocab_size=c["vocab_size"], seq_len=c["seq_len"], n_layer=c["n_layer"],
+                    n_head=c["n_head"], d_model=c["d_model"])
+    model = GPT(cfg).cuda()
+    opt = FlatAdamW(model, lr=6e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_grad_norm=1.0)
+    B, T = c["batch"], c["seq_len"]
+    g = torch.Generator(device="cuda").manual_seed(1234)
+    data = torch.randint(0, c["vocab_size"], (4 * B, T + 1), device="cuda", generator=g)
+
+    def step(i):
+        s = data[(i % 4) * B:(i % 4 + 1) * B]
+        loss = model(s[:, :-1], s[:, 1:], grad_scale=opt.scale)
+        opt.backward(loss)
+        opt.step(lr=6e-4)
+        opt.zero_grad()
+        return loss
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        loss = step(i)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    return {"ms_per_step": dt * 1e3, "tok_s": B * T / dt, "loss": float(loss),
+            "params": model.num_params(), "found_inf": float(opt._found_inf)}
+
+
+def cpu_baseline(torch):
+    """The reference's naive-PyTorch fp32 step (oracle/gpt.py) on the host cores."""
+    from oracle import gpt as ogpt
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    c = CFG5
+    torch.manual_seed(0)
+    m = ogpt.GPT(c["vocab_size"], c["seq_len"], c["n_layer"], c["n_head"], c["d_model"])
+    opt = ogpt.make_optimizer(m, lr=6e-4)
+    Bc, T = 1, c["seq_len"]
+    gen = torch.Generator().manual_seed(1234)
+    data = torch.randint(0, c["vocab_size"], (Bc, T + 1), generator=gen)
+    x, y = data[:, :-1], data[:, 1:]
+    ogpt.cpu_train_step(m, opt, x, y)          # warm-up
+    n, t0 = 0, time.perf_counter()
+    while n < 2 or (time.perf_counter() - t0 < 10.0 and n < 6):
+        ogpt.cpu_train_step(m, opt, x, y)
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(Bc * T / dt, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": (f"oracle/gpt.py naive-PyTorch fp32 GPT 12L-d768 V50304 (SDPA, F.rms_norm, "
+                       f"F.cross_entropy, AdamW + clip 1.0) at batch {Bc} x {T} tokens, "
+                       f"1 warm-up + {n} timed steps ({dt:.2f} s/step) on {cores} threads, {cpu_model}")}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): the fxlm hot path is "
+              "single-GPU; see DESIGN.md for how it would shard.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from fxgpu.abi import lib
+    lib()
+
+    attn = bench_attention(torch)
+    ce = bench_ce(torch)
+    norm = bench_norm(torch)
+    adamw = bench_adamw(torch)
+    lin = bench_linear(torch)
+    torch.cuda.empty_cache()
+    step = gpu_step_bench(torch, args.steps, args.warmup)
+    torch.cuda.empty_cache()
+
+    roofline = {
+        "kernel": "fx_attn_bwd (attn_bwd_dq + attn_bwd_dkv), cfg2 [16,12,1024,64] causal",
+        "bound": "mfma", "achieved": round(attn["flop_bwd"] / attn["bwd_us"] / 1e6, 1),
+        "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+        "frac": round(attn["flop_bwd"] / attn["bwd_us"] / 1e6 / BF16_PEAK_TFLOPS, 4),
+        "traffic": None,
+    }
+    cpu = None if args.no_cpu else cpu_baseline(torch)
+    out = {
+        "metric": "train tokens/sec (GPT 12L-d768, S=1024) + attn fwd/bwd TFLOPS, % roofline",
+        "value": round(step["tok_s"], 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(step["ms_per_step"], 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (uniform random tokens, seed 1234; random-init weights N(0,0.02))",
+        "config": {"workload": "GPT 12L-d768 H12 V50304 S1024 B16 bf16 train step "
+                               "(fwd+bwd+FlatAdamW), fused attention/RMSNorm/linear-CE/MLP/AdamW",
+                   "global_batch": 16, "seq_len": 1024, "tokens_per_step": 16384,
+                   "params": step["params"], "parallelism": "single GPU"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "gpu_over_cpu": (round(step["tok_s"] / cpu["value"], 1) if cpu else None),
+        "kernels": {"attention_cfg2": {k: v for k, v in attn.items() if not k.startswith("flop")},
+                    "cross_entropy_cfg3": ce, "rmsnorm_cfg4": norm, "flat_adamw_cfg4": adamw,
+                    "fused_linear_gelu_cfg5_fc": lin},
+        "final_loss": round(step["loss"], 4),
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

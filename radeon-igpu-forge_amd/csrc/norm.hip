@@ -221,7 +221,7 @@ static int64_t bwd_blocks(int64_t N) {
 using namespace fx;
 
 static int norm_check(const void* x, const void* w, int64_t N, int32_t D, const char* who) {
-    FX_REQUIRE(x != nullptr && w != nullptr, "%s: null pointer", who);
+    FX_REQUIRE((N == 0 || x != nullptr) && w != nullptr, "%s: null pointer", who);
     FX_REQUIRE(N >= 0, "%s: N=%lld < 0", who, (long long)N);
     FX_REQUIRE(D >= 8 && D <= 8192 && D % 8 == 0, "%s: D=%d needs D%%8==0 and 8<=D<=8192", who, D);
     return 0;
@@ -230,8 +230,8 @@ static int norm_check(const void* x, const void* w, int64_t N, int32_t D, const 
 extern "C" int fx_rms_norm_fwd(const uint16_t* x, const uint16_t* w, uint16_t* y, float* rstd,
                                int64_t N, int32_t D, float eps, void* stream) {
     if (int e = norm_check(x, w, N, D, "fx_rms_norm_fwd")) return e;
-    FX_REQUIRE(y != nullptr && rstd != nullptr, "fx_rms_norm_fwd: null output");
     if (N == 0) return 0;
+    FX_REQUIRE(y != nullptr && rstd != nullptr, "fx_rms_norm_fwd: null output");
     const RowShape s = pick_shape(D);
     const int G = 256 / s.lpr;
     const int64_t blocks = (N + G - 1) / G;
@@ -253,7 +253,8 @@ extern "C" int fx_rms_norm_bwd(const uint16_t* x, const uint16_t* dy, const uint
                                const float* rstd, uint16_t* dx, float* dw_f32, uint16_t* dw,
                                float* work, int64_t N, int32_t D, void* stream) {
     if (int e = norm_check(x, w, N, D, "fx_rms_norm_bwd")) return e;
-    FX_REQUIRE(dy != nullptr && rstd != nullptr && dx != nullptr && dw_f32 != nullptr,
+    FX_REQUIRE(dw_f32 != nullptr, "fx_rms_norm_bwd: null dw");
+    FX_REQUIRE(N == 0 || (dy != nullptr && rstd != nullptr && dx != nullptr),
                "fx_rms_norm_bwd: null pointer");
     if (N == 0) {
         // dw of an empty batch is zero

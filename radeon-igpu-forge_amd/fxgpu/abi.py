@@ -133,7 +133,7 @@ def call(name, *args):
     if rc != 0:
         msg = lib().fx_last_error().decode(errors="replace")
         if rc == FX_EINVAL:
-            raise ValueError(f"{name}: {msg}")
+            raise ValueError(msg)
         raise RuntimeError(f"{name} failed: hipError={rc} ({msg})")
 
 

@@ -28,11 +28,13 @@ from oracle import norm as onorm  # noqa: E402
 
 
 def bf16_bits(t):
-    return t.detach().cpu().to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    return t.detach().cpu().to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16).copy()
 
 
 def f32(t):
-    return t.detach().cpu().to(torch.float32).numpy()
+    # copy: .numpy() of a float32 CPU tensor shares its storage (the optimiser
+    # state is updated in place by later steps)
+    return t.detach().cpu().to(torch.float32).numpy().copy()
 
 
 def attention_cases():
