@@ -17,8 +17,14 @@
 // row softmax is 15 in-lane steps plus one exchange with lane l^32.
 // Backward: per query tile, S^T, dP^T and dQ^T = K^T dS^T (Delta computed in the same
 // kernel); per key tile, S = Q K^T, dP = dO V^T, dV^T += dO^T P, dK^T += Q^T dS.
+// The softmax scale of dS is applied once to dQ / dK at the end.
 // Semantics follow ml/fxlm/kernels/attention.hip:103-534 (mask key <= query, lse =
 // m + log l or -inf, Delta from the bf16 output, dS = P (dP - Delta) scale).
+//
+// Each tile's MFMA operands are read from LDS up front and the independent
+// accumulator chains are interleaved, so LDS latency and MFMA dependencies overlap;
+// K/V (Q/dO) tiles are double-buffered in LDS with the next tile's global loads in
+// flight during the current tile's math (one barrier per tile).
 #include <math.h>
 
 #include "fx_device.h"
@@ -32,6 +38,10 @@ constexpr int kBN = 64;              // keys per streamed tile (forward, dQ)
 constexpr int kBK = 32 * kAttWaves;  // keys per workgroup (dK/dV)
 constexpr int kBQ = 64;              // queries per streamed tile (dK/dV)
 constexpr float kNegInfA = -__builtin_huge_valf();
+
+// Lazy rescaling (forward): the running max only moves when a row's new max exceeds
+// it by more than this (log2 units), so P stays <= 2^8 and most tiles skip the O rescale.
+constexpr float kLazyRescale = 8.f;
 
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
 
@@ -48,18 +58,13 @@ __device__ __forceinline__ bf16x8 cat8(const bf16x4& lo, const bf16x4& hi) {
     return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-__device__ __forceinline__ bf16x8 as_bf16x8(const uint4& v) {
-    return __builtin_bit_cast(bf16x8, v);
-}
+__device__ __forceinline__ bf16x8 as_bf16x8(const uint4& v) { return __builtin_bit_cast(bf16x8, v); }
 
-// 8 fp32 accumulator values -> bf16x8 operand
-__device__ __forceinline__ bf16x8 pack_op(const f32x16& c, int base) {
-    uint4 u;
-    u.x = pack_bf16x2(c[base + 0], c[base + 1]);
-    u.y = pack_bf16x2(c[base + 2], c[base + 3]);
-    u.z = pack_bf16x2(c[base + 4], c[base + 5]);
-    u.w = pack_bf16x2(c[base + 6], c[base + 7]);
-    return as_bf16x8(u);
+// 8 fp32 accumulator values (elements 8h..8h+7) -> bf16x8 operand
+__device__ __forceinline__ bf16x8 pack_op(const f32x16& c, int h) {
+    const f32x8 v = h == 0 ? __builtin_shufflevector(c, c, 0, 1, 2, 3, 4, 5, 6, 7)
+                           : __builtin_shufflevector(c, c, 8, 9, 10, 11, 12, 13, 14, 15);
+    return __builtin_convertvector(v, bf16x8);
 }
 
 // A operand whose K dimension runs down the rows of a row-major LDS tile with row
@@ -82,23 +87,43 @@ __device__ __forceinline__ bf16x8 lds_op_row(const uint16_t* tile, int ld, int r
 // row index (within a 32-row accumulator tile) of accumulator element i of lane l
 __device__ __forceinline__ int acc_row(int i, int lane) { return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3); }
 
-// Stage rows [r0, r0+R) of a (rows, D) bf16 matrix with row stride `rs` into an LDS
-// tile of row stride D+8; rows >= nrows are zero.
+// Register staging of a tile for software pipelining.  init() fixes this thread's
+// vectors of a tile (row, element offset row*rs + col); load() issues the global
+// reads of one tile given its first row's address (rows past `valid_rows` read row 0
+// and are zeroed, so there is no divergent branch); store() writes them to an LDS
+// tile of row stride D+8 once its previous contents are no longer read.
 template <int D, int R>
-__device__ __forceinline__ void stage_tile(uint16_t* tile, const uint16_t* src, int64_t rs, int r0, int nrows) {
-    constexpr int VPR = D / 8;  // 16-byte vectors per row
-    constexpr int LD = D + 8;
+struct TileRegs {
+    static constexpr int VPR = D / 8;
+    static constexpr int NV = R * VPR / kAttThreads;
+    static_assert(R * VPR % kAttThreads == 0, "tile must split evenly over the workgroup");
+    uint4 v[NV];
+    int row[NV];
+    int off[NV];
+    __device__ __forceinline__ void init(int64_t rs) {
 #pragma unroll
-    for (int it = 0; it < (R * VPR + kAttThreads - 1) / kAttThreads; ++it) {
-        const int idx = it * kAttThreads + threadIdx.x;
-        if (idx < R * VPR) {
-            const int r = idx / VPR, cv = idx % VPR;
-            uint4 v = make_uint4(0u, 0u, 0u, 0u);
-            if (r0 + r < nrows) v = ld16(src + (int64_t)(r0 + r) * rs + cv * 8);
-            *reinterpret_cast<uint4*>(tile + r * LD + cv * 8) = v;
+        for (int it = 0; it < NV; ++it) {
+            const int idx = it * kAttThreads + threadIdx.x;
+            row[it] = idx / VPR;
+            off[it] = (int)(row[it] * rs) + (idx % VPR) * 8;
         }
     }
-}
+    __device__ __forceinline__ void load(const uint16_t* first_row, int valid_rows) {
+#pragma unroll
+        for (int it = 0; it < NV; ++it) {
+            const bool ok = row[it] < valid_rows;
+            const uint4 x = ld16(first_row + (ok ? off[it] : 0));
+            v[it] = ok ? x : make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+    __device__ __forceinline__ void store(uint16_t* tile) const {
+#pragma unroll
+        for (int it = 0; it < NV; ++it) {
+            const int idx = it * kAttThreads + threadIdx.x;
+            *reinterpret_cast<uint4*>(tile + (idx / VPR) * (D + 8) + (idx % VPR) * 8) = v[it];
+        }
+    }
+};
 
 // 1-D grid over (bh, tile): consecutive tiles of one (b, h) land on one XCD
 // (workgroups are dealt round-robin to the 8 XCDs), so they share its L2.
@@ -110,6 +135,14 @@ __device__ __forceinline__ void grid_map(int ntiles, int nbh, int& bh, int& tile
     tile = x - bh * ntiles;
 }
 
+// 4 consecutive fp32 accumulator values (elements 4r..4r+3) * mul -> 4 bf16 (8-byte store)
+__device__ __forceinline__ void store4(uint16_t* p, const f32x16& c, int r, float mul) {
+    uint2 u;
+    u.x = pack_bf16x2(c[4 * r + 0] * mul, c[4 * r + 1] * mul);
+    u.y = pack_bf16x2(c[4 * r + 2] * mul, c[4 * r + 3] * mul);
+    *reinterpret_cast<uint2*>(p) = u;
+}
+
 // ---------------------------------------------------------------------------
 // forward
 
@@ -118,8 +151,8 @@ __global__ void __launch_bounds__(kAttThreads) attn_fwd_kernel(fxAttnArgs a) {
     constexpr int LD = D + 8;
     constexpr int DC = D / 16;  // K chunks of Q.K
     constexpr int DT = D / 32;  // 32-row tiles of O^T
-    __shared__ __attribute__((aligned(16))) uint16_t sk[kBN * LD];
-    __shared__ __attribute__((aligned(16))) uint16_t sv[kBN * LD];
+    __shared__ __attribute__((aligned(16))) uint16_t sk[2][kBN * LD];
+    __shared__ __attribute__((aligned(16))) uint16_t sv[2][kBN * LD];
 
     const int T = a.T;
     const int nqt = (T + kBM - 1) / kBM;
@@ -135,6 +168,14 @@ __global__ void __launch_bounds__(kAttThreads) attn_fwd_kernel(fxAttnArgs a) {
 
     const uint16_t* kbase = a.k + b * a.ksb + h * a.ksh;
     const uint16_t* vbase = a.v + b * a.vsb + h * a.vsh;
+    const int kend = a.causal ? min(T, q0 + kBM) : T;
+    const int nblk = (kend + kBN - 1) / kBN;
+
+    TileRegs<D, kBN> rk, rv;
+    rk.init(a.kst);
+    rv.init(a.vst);
+    rk.load(kbase, T);
+    rv.load(vbase, T);
 
     bf16x8 qop[DC];
     {
@@ -146,70 +187,92 @@ __global__ void __launch_bounds__(kAttThreads) attn_fwd_kernel(fxAttnArgs a) {
             qop[c] = as_bf16x8(v);
         }
     }
+    rk.store(sk[0]);
+    rv.store(sv[0]);
+    __syncthreads();
+
     const float sl2 = a.scale * kLog2e;
     float m_run = kNegInfA, l_run = 0.f;
     f32x16 acc[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16{};
 
-    const int kend = a.causal ? min(T, q0 + kBM) : T;
-    for (int kb = 0; kb < kend; kb += kBN) {
-        __syncthreads();
-        stage_tile<D, kBN>(sk, kbase, a.kst, kb, T);
-        stage_tile<D, kBN>(sv, vbase, a.vst, kb, T);
-        __syncthreads();
-        if (a.causal && kb > q0w + 31) continue;  // every key of the tile is masked for this wave
-
-        f32x16 s[2];
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            s[t] = f32x16{};
-#pragma unroll
-            for (int c = 0; c < DC; ++c)
-                s[t] = mfma32(lds_op_row(sk, LD, 32 * t, 16 * c, lane), qop[c], s[t]);
+    for (int j = 0; j < nblk; ++j) {
+        const int kb = j * kBN;
+        const int buf = j & 1;
+        const bool more = j + 1 < nblk;
+        if (more) {
+            rk.load(kbase + (int64_t)(kb + kBN) * a.kst, T - kb - kBN);
+            rv.load(vbase + (int64_t)(kb + kBN) * a.vst, T - kb - kBN);
         }
-        const bool need_mask = (kb + kBN > T) || (a.causal && kb + kBN - 1 > q0w);
-        float mloc = kNegInfA;
+        const uint16_t* K = sk[buf];
+        const uint16_t* V = sv[buf];
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int hh = 0; hh < 2; ++hh) {
+            const int kh = kb + 32 * hh;  // first key of this half
+            if (a.causal && kh > q0w + 31) continue;  // every key of the half is masked for this wave
+            bf16x8 kop[DC];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                float v = s[t][i] * sl2;
-                if (need_mask) {
-                    const int key = kb + 32 * t + acc_row(i, lane);
-                    if (key >= T || (a.causal && key > qi)) v = kNegInfA;
-                }
-                s[t][i] = v;
-                mloc = fmaxf(mloc, v);
+            for (int c = 0; c < DC; ++c) kop[c] = lds_op_row(K, LD, 32 * hh, 16 * c, lane);
+            f32x16 s0 = f32x16{}, s1 = f32x16{};  // two chains over the halves of D
+#pragma unroll
+            for (int c = 0; c < DC / 2; ++c) {
+                s0 = mfma32(kop[c], qop[c], s0);
+                s1 = mfma32(kop[c + DC / 2], qop[c + DC / 2], s1);
             }
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-        const float m_new = fmaxf(m_run, mloc);
-        const float m_use = (m_new == kNegInfA) ? 0.f : m_new;
-        const float alpha = exp2_fast(m_run - m_use);
-        float rs = 0.f;
+            bf16x8 vop[DT][2];
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int kc = 0; kc < 2; ++kc) vop[dt][kc] = lds_op_t(V, LD, 32 * hh + 16 * kc, 32 * dt, lane);
+            f32x16 sc;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sc[i] = s0[i] + s1[i];
+            if ((kh + 32 > T) || (a.causal && kh + 31 > q0w)) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int key = kh + acc_row(i, lane);
+                    if (key >= T || (a.causal && key > qi)) sc[i] = kNegInfA;
+                }
+            }
+            float mloc = sc[0];
+#pragma unroll
+            for (int i = 1; i < 16; ++i) mloc = fmaxf(mloc, sc[i]);
+            mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+            const float m_new = fmaxf(m_run, mloc * sl2);
+            const bool need = m_new > m_run + kLazyRescale;
+            float alpha = 1.f;
+            if (need) {
+                alpha = exp2_fast(m_run - m_new);
+                m_run = m_new;
+            }
+            const float mu = (m_run == kNegInfA) ? 0.f : m_run;
+            float rs = 0.f;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const float p = exp2_fast(s[t][i] - m_use);
-                s[t][i] = p;
+                const float p = exp2_fast(fmaf(sc[i], sl2, -mu));
+                sc[i] = p;
                 rs += p;
             }
-        l_run = l_run * alpha + rs;
-        m_run = m_new;
+            l_run = l_run * alpha + rs;
+            if (__ballot(need)) {
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
+                for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
-
-        bf16x8 pop[4];
+                    for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
+            }
+            const bf16x8 p0 = pack_op(sc, 0), p1 = pack_op(sc, 1);
 #pragma unroll
-        for (int kc = 0; kc < 4; ++kc) pop[kc] = pack_op(s[kc >> 1], 8 * (kc & 1));
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-            for (int kc = 0; kc < 4; ++kc)
-                acc[dt] = mfma32(lds_op_t(sv, LD, 16 * kc, 32 * dt, lane), pop[kc], acc[dt]);
+            for (int dt = 0; dt < DT; ++dt) {
+                acc[dt] = mfma32(vop[dt][0], p0, acc[dt]);
+                acc[dt] = mfma32(vop[dt][1], p1, acc[dt]);
+            }
+        }
+        if (more) {
+            rk.store(sk[buf ^ 1]);
+            rv.store(sv[buf ^ 1]);
+        }
+        __syncthreads();
     }
 
     const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
@@ -219,13 +282,7 @@ __global__ void __launch_bounds__(kAttThreads) attn_fwd_kernel(fxAttnArgs a) {
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int d = 32 * dt + 8 * r + 4 * g;
-                uint2 u;
-                u.x = pack_bf16x2(acc[dt][4 * r + 0] * inv, acc[dt][4 * r + 1] * inv);
-                u.y = pack_bf16x2(acc[dt][4 * r + 2] * inv, acc[dt][4 * r + 3] * inv);
-                *reinterpret_cast<uint2*>(orow + d) = u;
-            }
+            for (int r = 0; r < 4; ++r) store4(orow + 32 * dt + 8 * r + 4 * g, acc[dt], r, inv);
         if (g == 0)
             a.lse_out[(int64_t)bh * T + qi] = l_tot > 0.f ? (m_run + log2_fast(l_tot)) * kLn2 : kNegInfA;
     }
@@ -235,12 +292,12 @@ __global__ void __launch_bounds__(kAttThreads) attn_fwd_kernel(fxAttnArgs a) {
 // backward, query side: Delta and dQ
 
 template <int D>
-__global__ void __launch_bounds__(kAttThreads) attn_bwd_dq_kernel(fxAttnArgs a) {
+__global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dq_kernel(fxAttnArgs a) {
     constexpr int LD = D + 8;
     constexpr int DC = D / 16;
     constexpr int DT = D / 32;
-    __shared__ __attribute__((aligned(16))) uint16_t sk[kBN * LD];
-    __shared__ __attribute__((aligned(16))) uint16_t sv[kBN * LD];
+    __shared__ __attribute__((aligned(16))) uint16_t sk[2][kBN * LD];
+    __shared__ __attribute__((aligned(16))) uint16_t sv[2][kBN * LD];
 
     const int T = a.T;
     const int nqt = (T + kBM - 1) / kBM;
@@ -254,6 +311,16 @@ __global__ void __launch_bounds__(kAttThreads) attn_bwd_dq_kernel(fxAttnArgs a) 
     const int q0w = q0 + 32 * wave;
     const int qi = q0w + ln;
     const bool qok = qi < T;
+
+    const uint16_t* kbase = a.k + b * a.ksb + h * a.ksh;
+    const uint16_t* vbase = a.v + b * a.vsb + h * a.vsh;
+    const int kend = a.causal ? min(T, q0 + kBM) : T;
+    const int nblk = (kend + kBN - 1) / kBN;
+    TileRegs<D, kBN> rk, rv;
+    rk.init(a.kst);
+    rv.init(a.vst);
+    rk.load(kbase, T);
+    rv.load(vbase, T);
 
     // Q^T and dO^T operands, Delta = rowsum(dO * O) for this lane's query
     bf16x8 qop[DC], dop[DC];
@@ -282,52 +349,67 @@ __global__ void __launch_bounds__(kAttThreads) attn_bwd_dq_kernel(fxAttnArgs a) 
     }
     const float lse2 = qok ? a.lse[(int64_t)bh * T + qi] * kLog2e : 0.f;
     const float sl2 = a.scale * kLog2e;
-    const uint16_t* kbase = a.k + b * a.ksb + h * a.ksh;
-    const uint16_t* vbase = a.v + b * a.vsb + h * a.vsh;
+    rk.store(sk[0]);
+    rv.store(sv[0]);
+    __syncthreads();
 
     f32x16 acc[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16{};
 
-    const int kend = a.causal ? min(T, q0 + kBM) : T;
-    for (int kb = 0; kb < kend; kb += kBN) {
-        __syncthreads();
-        stage_tile<D, kBN>(sk, kbase, a.kst, kb, T);
-        stage_tile<D, kBN>(sv, vbase, a.vst, kb, T);
-        __syncthreads();
-        if (a.causal && kb > q0w + 31) continue;
-
-        f32x16 s[2], dp[2];
+    for (int j = 0; j < nblk; ++j) {
+        const int kb = j * kBN;
+        const int buf = j & 1;
+        const bool more = j + 1 < nblk;
+        if (more) {
+            rk.load(kbase + (int64_t)(kb + kBN) * a.kst, T - kb - kBN);
+            rv.load(vbase + (int64_t)(kb + kBN) * a.vst, T - kb - kBN);
+        }
+        const uint16_t* K = sk[buf];
+        const uint16_t* V = sv[buf];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            s[t] = f32x16{};
-            dp[t] = f32x16{};
+        for (int hh = 0; hh < 2; ++hh) {
+            const int kh = kb + 32 * hh;
+            if (a.causal && kh > q0w + 31) continue;
+            bf16x8 kop[DC], vop[DC];
 #pragma unroll
             for (int c = 0; c < DC; ++c) {
-                s[t] = mfma32(lds_op_row(sk, LD, 32 * t, 16 * c, lane), qop[c], s[t]);
-                dp[t] = mfma32(lds_op_row(sv, LD, 32 * t, 16 * c, lane), dop[c], dp[t]);
+                kop[c] = lds_op_row(K, LD, 32 * hh, 16 * c, lane);
+                vop[c] = lds_op_row(V, LD, 32 * hh, 16 * c, lane);
             }
-        }
-        const bool need_mask = (kb + kBN > T) || (a.causal && kb + kBN - 1 > q0w);
+            f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+            for (int c = 0; c < DC; ++c) {
+                s = mfma32(kop[c], qop[c], s);
+                dp = mfma32(vop[c], dop[c], dp);
+            }
+            bf16x8 ktop[DT][2];
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int kc = 0; kc < 2; ++kc) ktop[dt][kc] = lds_op_t(K, LD, 32 * hh + 16 * kc, 32 * dt, lane);
+            const bool need_mask = (kh + 32 > T) || (a.causal && kh + 31 > q0w);
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                float p = exp2_fast(s[t][i] * sl2 - lse2);
+                float p = exp2_fast(fmaf(s[i], sl2, -lse2));
                 if (need_mask) {
-                    const int key = kb + 32 * t + acc_row(i, lane);
+                    const int key = kh + acc_row(i, lane);
                     if (key >= T || (a.causal && key > qi)) p = 0.f;
                 }
-                s[t][i] = p * (dp[t][i] - delta) * a.scale;  // dS^T
+                s[i] = p * (dp[i] - delta);  // dS^T / scale
             }
-        bf16x8 dsop[4];
+            const bf16x8 d0 = pack_op(s, 0), d1 = pack_op(s, 1);
 #pragma unroll
-        for (int kc = 0; kc < 4; ++kc) dsop[kc] = pack_op(s[kc >> 1], 8 * (kc & 1));
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-            for (int kc = 0; kc < 4; ++kc)
-                acc[dt] = mfma32(lds_op_t(sk, LD, 16 * kc, 32 * dt, lane), dsop[kc], acc[dt]);
+            for (int dt = 0; dt < DT; ++dt) {
+                acc[dt] = mfma32(ktop[dt][0], d0, acc[dt]);
+                acc[dt] = mfma32(ktop[dt][1], d1, acc[dt]);
+            }
+        }
+        if (more) {
+            rk.store(sk[buf ^ 1]);
+            rv.store(sv[buf ^ 1]);
+        }
+        __syncthreads();
     }
 
     if (qok) {
@@ -335,13 +417,7 @@ __global__ void __launch_bounds__(kAttThreads) attn_bwd_dq_kernel(fxAttnArgs a) 
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int d = 32 * dt + 8 * r + 4 * g;
-                uint2 u;
-                u.x = pack_bf16x2(acc[dt][4 * r + 0], acc[dt][4 * r + 1]);
-                u.y = pack_bf16x2(acc[dt][4 * r + 2], acc[dt][4 * r + 3]);
-                *reinterpret_cast<uint2*>(dqrow + d) = u;
-            }
+            for (int r = 0; r < 4; ++r) store4(dqrow + 32 * dt + 8 * r + 4 * g, acc[dt], r, a.scale);
     }
 }
 
@@ -349,14 +425,14 @@ __global__ void __launch_bounds__(kAttThreads) attn_bwd_dq_kernel(fxAttnArgs a) 
 // backward, key side: dK and dV
 
 template <int D>
-__global__ void __launch_bounds__(kAttThreads) attn_bwd_dkv_kernel(fxAttnArgs a) {
+__global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dkv_kernel(fxAttnArgs a) {
     constexpr int LD = D + 8;
     constexpr int DC = D / 16;
     constexpr int DT = D / 32;
-    __shared__ __attribute__((aligned(16))) uint16_t sq[kBQ * LD];
-    __shared__ __attribute__((aligned(16))) uint16_t sdo[kBQ * LD];
-    __shared__ __attribute__((aligned(16))) float slse[kBQ];
-    __shared__ __attribute__((aligned(16))) float sdelta[kBQ];
+    __shared__ __attribute__((aligned(16))) uint16_t sq[2][kBQ * LD];
+    __shared__ __attribute__((aligned(16))) uint16_t sdo[2][kBQ * LD];
+    __shared__ __attribute__((aligned(16))) float slse[2][kBQ];
+    __shared__ __attribute__((aligned(16))) float sdelta[2][kBQ];
 
     const int T = a.T;
     const int nkt = (T + kBK - 1) / kBK;
@@ -369,6 +445,37 @@ __global__ void __launch_bounds__(kAttThreads) attn_bwd_dkv_kernel(fxAttnArgs a)
     const int k0w = k0 + 32 * wave;
     const int ki = k0w + ln;
     const bool kok = ki < T;
+
+    const uint16_t* qbase = a.q + b * a.qsb + h * a.qsh;
+    const uint16_t* dobase = a.dout + (int64_t)b * T * a.H * D + (int64_t)h * D;
+    const int64_t dors = (int64_t)a.H * D;
+    const float* lse_bh = a.lse + (int64_t)bh * T;
+    const float* del_bh = a.delta + (int64_t)bh * T;
+    const int qstart = a.causal ? k0 : 0;  // k0 is a multiple of kBQ
+    const int nblk = (T - qstart + kBQ - 1) / kBQ;
+
+    TileRegs<D, kBQ> rq, rd;
+    rq.init(a.qst);
+    rd.init(dors);
+    float rl = 0.f, rdl = 0.f;
+    auto load_rows = [&](int qb) {
+        rq.load(qbase + (int64_t)qb * a.qst, T - qb);
+        rd.load(dobase + (int64_t)qb * dors, T - qb);
+        if (threadIdx.x < kBQ) {
+            const int q = qb + threadIdx.x;
+            rl = q < T ? lse_bh[q] * kLog2e : 0.f;
+            rdl = q < T ? del_bh[q] : 0.f;
+        }
+    };
+    auto store_rows = [&](int buf) {
+        rq.store(sq[buf]);
+        rd.store(sdo[buf]);
+        if (threadIdx.x < kBQ) {
+            slse[buf][threadIdx.x] = rl;
+            sdelta[buf][threadIdx.x] = rdl;
+        }
+    };
+    if (nblk > 0) load_rows(qstart);
 
     bf16x8 kop[DC], vop[DC];
     {
@@ -386,9 +493,8 @@ __global__ void __launch_bounds__(kAttThreads) attn_bwd_dkv_kernel(fxAttnArgs a)
         }
     }
     const float sl2 = a.scale * kLog2e;
-    const uint16_t* qbase = a.q + b * a.qsb + h * a.qsh;
-    const uint16_t* dobase = a.dout + (int64_t)b * T * a.H * D + (int64_t)h * D;
-    const int64_t dors = (int64_t)a.H * D;
+    if (nblk > 0) store_rows(0);
+    __syncthreads();
 
     f32x16 adv[DT], adk[DT];
 #pragma unroll
@@ -397,65 +503,73 @@ __global__ void __launch_bounds__(kAttThreads) attn_bwd_dkv_kernel(fxAttnArgs a)
         adk[dt] = f32x16{};
     }
 
-    const int qstart = a.causal ? k0 : 0;  // k0 is a multiple of kBQ
-    for (int qb = qstart; qb < T; qb += kBQ) {
-        __syncthreads();
-        stage_tile<D, kBQ>(sq, qbase, a.qst, qb, T);
-        stage_tile<D, kBQ>(sdo, dobase, dors, qb, T);
-        if (threadIdx.x < kBQ) {
-            const int q = qb + threadIdx.x;
-            slse[threadIdx.x] = q < T ? a.lse[(int64_t)bh * T + q] * kLog2e : 0.f;
-            sdelta[threadIdx.x] = q < T ? a.delta[(int64_t)bh * T + q] : 0.f;
-        }
-        __syncthreads();
-        if (a.causal && qb + kBQ - 1 < k0w) continue;  // all of this wave's keys are after these queries
-
-        f32x16 s[2], dp[2];
+    for (int j = 0; j < nblk; ++j) {
+        const int qb = qstart + j * kBQ;
+        const int buf = j & 1;
+        const bool more = j + 1 < nblk;
+        if (more) load_rows(qb + kBQ);
+        const uint16_t* Q = sq[buf];
+        const uint16_t* DO = sdo[buf];
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            s[t] = f32x16{};
-            dp[t] = f32x16{};
+        for (int hh = 0; hh < 2; ++hh) {
+            const int qh = qb + 32 * hh;  // first query of this half
+            if (a.causal && qh + 31 < k0w) continue;  // all of this wave's keys follow these queries
+            bf16x8 qa[DC], da[DC];
 #pragma unroll
             for (int c = 0; c < DC; ++c) {
-                s[t] = mfma32(lds_op_row(sq, LD, 32 * t, 16 * c, lane), kop[c], s[t]);
-                dp[t] = mfma32(lds_op_row(sdo, LD, 32 * t, 16 * c, lane), vop[c], dp[t]);
+                qa[c] = lds_op_row(Q, LD, 32 * hh, 16 * c, lane);
+                da[c] = lds_op_row(DO, LD, 32 * hh, 16 * c, lane);
             }
-        }
-        const bool need_mask = (qb + kBQ > T) || (a.causal && qb < k0w + 31);
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
+            float4 l4[4], d4[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int qr = 32 * t + 8 * r + 4 * g;  // 4 consecutive queries of this lane
-                const float4 l4 = *reinterpret_cast<const float4*>(slse + qr);
-                const float4 d4 = *reinterpret_cast<const float4*>(sdelta + qr);
-                const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-                const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
+                const int qr = 32 * hh + 8 * r + 4 * g;  // 4 consecutive queries of this lane
+                l4[r] = *reinterpret_cast<const float4*>(&slse[buf][qr]);
+                d4[r] = *reinterpret_cast<const float4*>(&sdelta[buf][qr]);
+            }
+            f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+            for (int c = 0; c < DC; ++c) {
+                s = mfma32(qa[c], kop[c], s);
+                dp = mfma32(da[c], vop[c], dp);
+            }
+            bf16x8 dot[DT][2], qtr[DT][2];
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+                for (int kc = 0; kc < 2; ++kc) {
+                    dot[dt][kc] = lds_op_t(DO, LD, 32 * hh + 16 * kc, 32 * dt, lane);
+                    qtr[dt][kc] = lds_op_t(Q, LD, 32 * hh + 16 * kc, 32 * dt, lane);
+                }
+            const bool need_mask = (qh + 32 > T) || (a.causal && qh < k0w + 31);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float lv[4] = {l4[r].x, l4[r].y, l4[r].z, l4[r].w};
+                const float dv[4] = {d4[r].x, d4[r].y, d4[r].z, d4[r].w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int i = 4 * r + e;
-                    float p = exp2_fast(s[t][i] * sl2 - lv[e]);
+                    float p = exp2_fast(fmaf(s[i], sl2, -lv[e]));
                     if (need_mask) {
-                        const int q = qb + qr + e;
+                        const int q = qh + 8 * r + 4 * g + e;
                         if (q >= T || (a.causal && ki > q)) p = 0.f;
                     }
-                    s[t][i] = p;                                      // P
-                    dp[t][i] = p * (dp[t][i] - dv[e]) * a.scale;      // dS
+                    s[i] = p;                          // P
+                    dp[i] = p * (dp[i] - dv[e]);       // dS / scale
                 }
             }
-        bf16x8 pop[4], dsop[4];
+            const bf16x8 p0 = pack_op(s, 0), p1 = pack_op(s, 1);
+            const bf16x8 d0 = pack_op(dp, 0), d1 = pack_op(dp, 1);
 #pragma unroll
-        for (int kc = 0; kc < 4; ++kc) {
-            pop[kc] = pack_op(s[kc >> 1], 8 * (kc & 1));
-            dsop[kc] = pack_op(dp[kc >> 1], 8 * (kc & 1));
-        }
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-            for (int kc = 0; kc < 4; ++kc) {
-                adv[dt] = mfma32(lds_op_t(sdo, LD, 16 * kc, 32 * dt, lane), pop[kc], adv[dt]);
-                adk[dt] = mfma32(lds_op_t(sq, LD, 16 * kc, 32 * dt, lane), dsop[kc], adk[dt]);
+            for (int dt = 0; dt < DT; ++dt) {
+                adv[dt] = mfma32(dot[dt][0], p0, adv[dt]);
+                adk[dt] = mfma32(qtr[dt][0], d0, adk[dt]);
+                adv[dt] = mfma32(dot[dt][1], p1, adv[dt]);
+                adk[dt] = mfma32(qtr[dt][1], d1, adk[dt]);
             }
+        }
+        if (more) store_rows(buf ^ 1);
+        __syncthreads();
     }
 
     if (kok) {
@@ -465,14 +579,8 @@ __global__ void __launch_bounds__(kAttThreads) attn_bwd_dkv_kernel(fxAttnArgs a)
         for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int d = 32 * dt + 8 * r + 4 * g;
-                uint2 u;
-                u.x = pack_bf16x2(adk[dt][4 * r + 0], adk[dt][4 * r + 1]);
-                u.y = pack_bf16x2(adk[dt][4 * r + 2], adk[dt][4 * r + 3]);
-                *reinterpret_cast<uint2*>(dkrow + d) = u;
-                u.x = pack_bf16x2(adv[dt][4 * r + 0], adv[dt][4 * r + 1]);
-                u.y = pack_bf16x2(adv[dt][4 * r + 2], adv[dt][4 * r + 3]);
-                *reinterpret_cast<uint2*>(dvrow + d) = u;
+                store4(dkrow + 32 * dt + 8 * r + 4 * g, adk[dt], r, a.scale);
+                store4(dvrow + 32 * dt + 8 * r + 4 * g, adv[dt], r, 1.f);
             }
     }
 }
@@ -492,6 +600,10 @@ static int attn_check(const fxAttnArgs* p, bool bwd) {
     for (int64_t x : s) FX_REQUIRE(x % 8 == 0, "fx_attn: q/k/v strides must be multiples of 8 elements");
     FX_REQUIRE((((uintptr_t)a.q | (uintptr_t)a.k | (uintptr_t)a.v) & 15) == 0,
                "fx_attn: q/k/v must be 16-byte aligned");
+    // tile offsets row * stride are 32-bit inside the kernels
+    const int64_t mx = (int64_t)64 * (a.qst > a.kst ? (a.qst > a.vst ? a.qst : a.vst) : (a.kst > a.vst ? a.kst : a.vst));
+    FX_REQUIRE(mx < ((int64_t)1 << 30) && (int64_t)64 * a.H * a.D < ((int64_t)1 << 30),
+               "fx_attn: row strides too large");
     if (!bwd) {
         FX_REQUIRE(a.o_out && a.lse_out, "fx_attn_fwd: null output");
         FX_REQUIRE(((uintptr_t)a.o_out & 15) == 0, "fx_attn_fwd: o must be 16-byte aligned");

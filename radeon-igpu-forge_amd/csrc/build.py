@@ -26,6 +26,9 @@ FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-munsafe-fp-atomics", "-Wall", "-Wno-unused-function",
+    # keep MFMA accumulators in VGPRs: the softmax works on them directly, without
+    # v_accvgpr_read/write copies each tile
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
 
