@@ -91,7 +91,10 @@ def bench_ce(torch):
         fused_cross_entropy(lg, tg).backward()
         lg.grad = None
     t = time_us(torch, fb, iters=10, warm=3)
-    nbytes = 2 * N * V * 2 + N * 8                 # read logits once, write dlogits once, targets
+    n_valid = int((tg != -100).sum())
+    # logits of rows with a valid target read once, dlogits of every row written once
+    # (ignored rows get a zero gradient row without being read), targets
+    nbytes = (n_valid + N) * V * 2 + N * 8
     del lg
     return {"shape": [N, V], "fwdbwd_us": round(t, 2), "gbs": round(nbytes / t / 1e3, 1),
             "frac_of_hbm": round(nbytes / t / 1e3 / HBM_PEAK_GBS, 4), "bytes": nbytes}

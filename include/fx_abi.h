@@ -53,9 +53,9 @@ int64_t fx_rms_norm_bwd_workspace(int64_t N, int32_t D);
 
 /* dx = rstd*w*dy - x*(rstd^3 * sum_d(x*w*dy) / D)   (bf16, (N, D))
  * dw = sum_rows x*rstd*dy                             (fp32 dw_f32 and bf16 dw, (D,))
- * One pass over x and dy: dx and per-strip dw partials in one kernel, then a column
+ * One pass over x and dy: dx and per-block dw partials in one kernel, then a column
  * reduction of the partials.  `work` holds fx_rms_norm_bwd_workspace(N, D) bytes.
- * dw (bf16) may be NULL.
+ * dw (bf16) may be NULL.  dw_f32 and work are 16-byte aligned, dw 8-byte aligned.
  * Replaces _RMSNorm.backward + rms_norm_bwd_dx + rms_norm_bwd_dw + part.sum(0)
  * (ml/fxlm/norm.py:64-85, ml/fxlm/kernels/norm.hip:63-127). */
 int fx_rms_norm_bwd(const uint16_t* x, const uint16_t* dy, const uint16_t* w,
@@ -133,7 +133,7 @@ typedef struct fxAdamWState {
     float* grad_norm;         /* () sqrt(sum g^2) / scale */
     float* scale;             /* () dynamic loss scale, updated in place */
     int32_t* growth;          /* () clean steps since the last scale change */
-    float* work;              /* fx_adamw_workspace(...) bytes */
+    float* work;              /* fx_adamw_workspace(...) bytes, 16-byte aligned */
     float lr, beta1, beta2, eps, weight_decay, max_grad_norm;
     float growth_factor;      /* 2.0 in the reference */
     float backoff_factor;     /* 0.5 in the reference */

@@ -17,69 +17,99 @@ namespace fx {
 
 constexpr float kNegInf = -__builtin_huge_valf();
 
-template <int NT>
-__device__ __forceinline__ float block_max(float v, float* sh) {
-    constexpr int NW = NT / 64;
-    v = group_max<64>(v);
-    if (NW == 1) return v;
-    const int wid = threadIdx.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) sh[wid] = v;
-    __syncthreads();
-    float r = sh[0];
-#pragma unroll
-    for (int i = 1; i < NW; ++i) r = fmaxf(r, sh[i]);
-    return r;
-}
-
-template <int NT>
-__device__ __forceinline__ float block_sum(float v, float* sh) {
-    constexpr int NW = NT / 64;
-    v = group_sum<64>(v);
-    if (NW == 1) return v;
-    const int wid = threadIdx.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) sh[wid] = v;
-    __syncthreads();
-    float r = sh[0];
-#pragma unroll
-    for (int i = 1; i < NW; ++i) r += sh[i];
-    return r;
+// (max, sum of exp(x - max)) pairs: merge b into a
+__device__ __forceinline__ void ms_merge(float& m, float& s, float m2, float s2) {
+    const float mn = fmaxf(m, m2);
+    // a side whose max equals the new max keeps its sum; -inf sides carry s == 0
+    const float ea = (m == mn) ? 1.f : exp2_fast((m - mn) * kLog2e);
+    const float eb = (m2 == mn) ? 1.f : exp2_fast((m2 - mn) * kLog2e);
+    s = s * ea + s2 * eb;
+    m = mn;
 }
 
 // Register-resident row: needs V % 8 == 0, ld % 8 == 0, ldg % 8 == 0 and 16-byte
 // aligned bases (checked by the host); V <= 8 * NT * NV.
+// Each thread reduces its own vectors to (max, sum exp(x - max)) without any
+// barrier; one block-wide merge of those pairs gives (M, Z); the gradient pass
+// then rereads the registers.  The target's gradient element is fixed up by the one
+// thread that holds it.
 template <int NT, int NV>
 __global__ void __launch_bounds__(NT) ce_row_kernel(fxCEArgs a) {
-    __shared__ float sh[NT / 64];
+    constexpr int NW = NT / 64;
+    __shared__ float shm[NW], shs[NW];
     const int64_t row = blockIdx.x;
     const uint16_t* lr = a.logits + row * a.ld;
     const int64_t t = a.target[row];
     const bool valid = (t != a.ignore_index) && (t >= 0) && (t < a.V);
     const int V8 = (int)(a.V >> 3);
     const int tid = threadIdx.x;
-    // x_t is read before any barrier: with grad == logits (in place) other threads
-    // overwrite the row once the reductions are done.
+    // x_t is read before the barrier: with grad == logits (in place) other threads
+    // overwrite the row once the reduction is done.
     const float xt = (tid == 0 && valid) ? bf16_to_f32(lr[t]) : 0.f;
+    uint16_t* gr = a.grad != nullptr ? a.grad + row * a.ldg : nullptr;
+    if (!valid) {  // no loss and a zero gradient row: the logits are not read
+        if (tid == 0) a.row_loss[row] = 0.f;
+        if (gr != nullptr) {
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                const int c = i * NT + tid;
+                if (c < V8) st16_nt(gr + (int64_t)c * 8, make_uint4(0u, 0u, 0u, 0u));
+            }
+        }
+        return;
+    }
 
     uint4 xv[NV];
-    float mx = kNegInf;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const int c = i * NT + tid;
         xv[i] = make_uint4(0u, 0u, 0u, 0u);
-        if (c < V8) {
-            xv[i] = ld16_nt(lr + (int64_t)c * 8);
+        if (c < V8) xv[i] = ld16_nt(lr + (int64_t)c * 8);
+    }
+    float m = kNegInf;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        if (i * NT + tid < V8) {
             float f[8];
             unpack8(xv[i], f);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) mx = fmaxf(mx, f[j]);
+            for (int j = 0; j < 8; ++j) m = fmaxf(m, f[j]);
         }
     }
-    mx = block_max<NT>(mx, sh);
-    const float mxl = mx * kLog2e;
-
     float s = 0.f;
+    {
+        const float ml = (m == kNegInf) ? 0.f : m * kLog2e;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            if (i * NT + tid < V8) {
+                float f[8];
+                unpack8(xv[i], f);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) s += exp2_fast(fmaf(f[j], kLog2e, -ml));
+            }
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ms_merge(m, s, __shfl_xor(m, off, 64), __shfl_xor(s, off, 64));
+    if (NW > 1) {
+        if ((tid & 63) == 0) {
+            shm[tid >> 6] = m;
+            shs[tid >> 6] = s;
+        }
+        __syncthreads();
+        m = shm[0];
+        s = shs[0];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) ms_merge(m, s, shm[w], shs[w]);
+    }
+
+    if (tid == 0) a.row_loss[row] = m + logf(s) - xt;
+    if (gr == nullptr) return;
+
+    const float gmul = *a.mul;
+    const float scale = gmul / s;  // softmax * mul = exp(x - M) * (mul / Z)
+    const float ml = m * kLog2e;
+    const int tc = (int)(t >> 3);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const int c = i * NT + tid;
@@ -87,34 +117,14 @@ __global__ void __launch_bounds__(NT) ce_row_kernel(fxCEArgs a) {
             float f[8];
             unpack8(xv[i], f);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) s += exp2_fast(fmaf(f[j], kLog2e, -mxl));
-        }
-    }
-    s = block_sum<NT>(s, sh);
-
-    if (tid == 0) {
-        float l = 0.f;
-        if (valid) l = mx + logf(s) - xt;
-        a.row_loss[row] = l;
-    }
-    if (a.grad == nullptr) return;
-
-    const float gmul = valid ? *a.mul : 0.f;
-    const float scale = gmul / s;  // softmax * mul = exp(x - m) * (mul / Z)
-    uint16_t* gr = a.grad + row * a.ldg;
+            for (int j = 0; j < 8; ++j) f[j] = exp2_fast(fmaf(f[j], kLog2e, -ml)) * scale;
+            if (c == tc) {
+                const int tj = (int)(t & 7);
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int c = i * NT + tid;
-        if (c < V8) {
-            float f[8], o[8];
-            unpack8(xv[i], f);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                float p = exp2_fast(fmaf(f[j], kLog2e, -mxl)) * scale;
-                if ((int64_t)c * 8 + j == t) p -= gmul;
-                o[j] = valid ? p : 0.f;
+                for (int j = 0; j < 8; ++j)
+                    if (j == tj) f[j] -= gmul;
             }
-            st16_nt(gr + (int64_t)c * 8, pack8(o));
+            st16_nt(gr + (int64_t)c * 8, pack8(f));
         }
     }
 }
@@ -174,6 +184,7 @@ ce_inv_nvalid_kernel(const int64_t* __restrict__ target, int64_t N, int64_t igno
                      float* __restrict__ mul) {
     __shared__ int sh[16];
     int cnt = 0;
+#pragma unroll 8
     for (int64_t i = threadIdx.x; i < N; i += 1024) cnt += (target[i] != ignore) ? 1 : 0;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
@@ -194,6 +205,7 @@ ce_loss_finalize_kernel(const float* __restrict__ row_loss, int64_t N,
                         const float* __restrict__ inv_n, float* __restrict__ loss) {
     __shared__ float sh[16];
     float s = 0.f;
+#pragma unroll 8
     for (int64_t i = threadIdx.x; i < N; i += 1024) s += row_loss[i];
     s = group_sum<64>(s);
     if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = s;
@@ -308,7 +320,7 @@ extern "C" int fx_ce_scale_grad(uint16_t* grad, int64_t numel, const float* g, f
     hipStream_t s = (hipStream_t)stream;
     if (numel > 0) {
         int64_t blocks = (numel / 8 + 255) / 256;
-        if (blocks > 8192) blocks = 8192;
+        if (blocks > 2048) blocks = 2048;  // grid-stride; small, since usually every block exits at once
         if (blocks < 1) blocks = 1;
         hipLaunchKernelGGL(ce_scale_grad_kernel, dim3((unsigned)blocks), dim3(256), 0, s, grad, numel, g,
                            (const float*)applied);

@@ -56,37 +56,25 @@ rms_fwd_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
     }
 }
 
-// dx for every row of a strip of `rows_per_block` rows, plus the strip's partial dw
-// (fp32, one row of `part` per block).
+// dx for the rows dealt to this block, plus the block's partial dw (fp32, one row of
+// `part` per block).  Rows are dealt round-robin over the whole grid, so all blocks
+// stream one window of consecutive rows at a time (DRAM pages stay open, as in a
+// plain copy); per-block strips of consecutive rows measured about 10% slower.
+// The row groups of a wave fold their dw partials with lane exchanges and the waves
+// then fold through LDS in a fixed order (deterministic).
+constexpr int kNormBwdThreads = 512;
+
 template <int LPR, int NV>
-__global__ void __launch_bounds__(256)
-rms_bwd_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ dy,
-               const uint16_t* __restrict__ w, const float* __restrict__ rstd,
-               uint16_t* __restrict__ dx, float* __restrict__ part, int64_t N, int D,
-               int64_t rows_per_block) {
-    constexpr int G = 256 / LPR;
-    extern __shared__ float red[];  // D floats
-    const int lane = threadIdx.x % LPR;
-    const int grp = threadIdx.x / LPR;
-    const int V8 = D >> 3;
-    const float invD = 1.f / (float)D;
-
-    uint4 wv[NV];
-    float acc[NV][8];
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int c = i * LPR + lane;
-        wv[i] = (c < V8) ? ld16(w + c * 8) : make_uint4(0u, 0u, 0u, 0u);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = 0.f;
-    }
-
-    const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
-    const int64_t r1 = (r0 + rows_per_block < N) ? r0 + rows_per_block : N;
-    for (int64_t row = r0 + grp; row < r1; row += G) {
+struct NormBwdRow {
+    uint4 xv[NV], dv[NV];
+    float r;
+    __device__ __forceinline__ void load(const uint16_t* __restrict__ x, const uint16_t* __restrict__ dy,
+                                         const float* __restrict__ rstd, int64_t row, int64_t n,
+                                         int D, int lane) {
+        if (row >= n) return;  // past the last row: nothing is read (uniform per row group)
         const uint16_t* xr = x + row * D;
         const uint16_t* dr = dy + row * D;
-        uint4 xv[NV], dv[NV];
+        const int V8 = D >> 3;
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int c = i * LPR + lane;
@@ -97,74 +85,150 @@ rms_bwd_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ dy,
                 dv[i] = ld16_nt(dr + (int64_t)c * 8);
             }
         }
-        const float r = rstd[row];
-        float t = 0.f;
+        r = rstd[row];
+    }
+};
+
+template <int LPR, int NV>
+__device__ __forceinline__ void norm_bwd_row(const NormBwdRow<LPR, NV>& b, const uint16_t* __restrict__ w,
+                                             uint16_t* __restrict__ dxr, float (&acc)[NV][8], int D,
+                                             float invD, int lane) {
+    const int V8 = D >> 3;
+    float t = 0.f;
 #pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            float fx_[8], fd[8], fw[8];
-            unpack8(xv[i], fx_);
-            unpack8(dv[i], fd);
-            unpack8(wv[i], fw);
+    for (int i = 0; i < NV; ++i) {
+        const int c = i * LPR + lane;
+        float fx_[8], fd[8], fw[8];
+        unpack8(b.xv[i], fx_);
+        unpack8(b.dv[i], fd);
+        unpack8((c < V8) ? ld16(w + c * 8) : make_uint4(0u, 0u, 0u, 0u), fw);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                t += fx_[j] * fw[j] * fd[j];
-                acc[i][j] += fx_[j] * r * fd[j];
-            }
-        }
-        t = group_sum<LPR>(t);
-        const float corr = r * r * r * t * invD;
-        uint16_t* dxr = dx + row * D;
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            const int c = i * LPR + lane;
-            if (c < V8) {
-                float fx_[8], fd[8], fw[8], o[8];
-                unpack8(xv[i], fx_);
-                unpack8(dv[i], fd);
-                unpack8(wv[i], fw);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) o[j] = r * fw[j] * fd[j] - fx_[j] * corr;
-                st16_nt(dxr + (int64_t)c * 8, pack8(o));
-            }
+        for (int j = 0; j < 8; ++j) {
+            t = fmaf(fx_[j] * fw[j], fd[j], t);
+            acc[i][j] = fmaf(fx_[j] * b.r, fd[j], acc[i][j]);
         }
     }
+    t = group_sum<LPR>(t);
+    const float corr = b.r * b.r * b.r * t * invD;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = i * LPR + lane;
+        if (c < V8) {
+            float fx_[8], fd[8], fw[8], o[8];
+            unpack8(b.xv[i], fx_);
+            unpack8(b.dv[i], fd);
+            unpack8(ld16(w + c * 8), fw);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = fmaf(b.r * fw[j], fd[j], -fx_[j] * corr);
+            st16_nt(dxr + (int64_t)c * 8, pack8(o));
+        }
+    }
+}
 
-    // fold the G row groups' partials in a fixed order (deterministic)
-    for (int g = 0; g < G; ++g) {
-        if (grp == g) {
+// waves per SIMD to budget registers for (two 512-thread blocks per CU up to 3
+// vectors per lane)
+template <int NV>
+constexpr int norm_bwd_min_waves() { return NV <= 3 ? 4 : 2; }
+
+template <int LPR, int NV, int NT = kNormBwdThreads, int MW = norm_bwd_min_waves<NV>()>
+__global__ void __launch_bounds__(NT, MW)
+rms_bwd_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ dy,
+               const uint16_t* __restrict__ w, const float* __restrict__ rstd,
+               uint16_t* __restrict__ dx, float* __restrict__ part, int64_t N, int D) {
+    constexpr int G = NT / LPR;
+    constexpr int NW = NT / 64;
+    extern __shared__ float red[];  // D floats
+    const int lane = threadIdx.x % LPR;
+    const int grp = threadIdx.x / LPR;
+    const int V8 = D >> 3;
+    const float invD = 1.f / (float)D;
+
+    float acc[NV][8];
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = 0.f;
+
+    // rows are dealt to the blocks' row groups round-robin (row = (k * P + block) * G +
+    // group), so at any moment the whole grid streams one window of consecutive rows
+    const int64_t stride = (int64_t)gridDim.x * G;
+    const int64_t first = (int64_t)blockIdx.x * G + grp;
+    NormBwdRow<LPR, NV> b;
+    for (int64_t row = first; row < N; row += stride) {
+        b.load(x, dy, rstd, row, N, D, lane);
+        norm_bwd_row<LPR, NV>(b, w, dx + row * D, acc, D, invD, lane);
+    }
+
+    // row groups sharing a wave: butterfly over the group index
+#pragma unroll
+    for (int off = LPR; off < 64; off <<= 1)
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[i][j] += __shfl_xor(acc[i][j], off, 64);
+    // waves: fixed-order fold through LDS
+    const int wave = threadIdx.x >> 6;
+    for (int wv = 0; wv < NW; ++wv) {
+        if (wave == wv && (threadIdx.x & 63) < LPR) {
 #pragma unroll
             for (int i = 0; i < NV; ++i) {
                 const int c = i * LPR + lane;
                 if (c < V8) {
 #pragma unroll
                     for (int j = 0; j < 8; ++j)
-                        red[c * 8 + j] = (g == 0) ? acc[i][j] : red[c * 8 + j] + acc[i][j];
+                        red[c * 8 + j] = (wv == 0) ? acc[i][j] : red[c * 8 + j] + acc[i][j];
                 }
             }
         }
         __syncthreads();
     }
     float* pr = part + (int64_t)blockIdx.x * D;
-    for (int c = threadIdx.x; c < D; c += 256) pr[c] = red[c];
+    for (int c = threadIdx.x; c < D; c += NT) pr[c] = red[c];
 }
 
-// dw[c] = sum_p part[p][c]: 8 columns x 32 partial-row lanes per block, fixed order.
+// dw[c] = sum_p part[p][c] in a fixed order.  A block owns 16 columns (4 float4
+// lanes) and 64 partial-row lanes (16 per wave); each thread sums every 64th partial
+// row of its 4 columns with all its loads in flight, the row lanes of a wave fold
+// with a butterfly (every lane ends with the same bits) and the 4 waves through LDS.
+// D % 8 == 0, so a column quad never straddles D.
 __global__ void __launch_bounds__(256)
 rms_dw_reduce_kernel(const float* __restrict__ part, int64_t P, int D, float* __restrict__ dw_f32,
                      uint16_t* __restrict__ dw) {
-    __shared__ float red[32][9];
-    const int cl = threadIdx.x & 7, rl = threadIdx.x >> 3;
-    const int col = blockIdx.x * 8 + cl;
-    float s = 0.f;
-    if (col < D)
-        for (int64_t p = rl; p < P; p += 32) s += part[p * D + col];
-    red[rl][cl] = s;
+    __shared__ float4 red[4][4];
+    const int ql = threadIdx.x & 3, rl = threadIdx.x >> 2;
+    const int col = blockIdx.x * 16 + ql * 4;
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (col < D) {
+#pragma unroll 16
+        for (int64_t p = rl; p < P; p += 64) {
+            const float4 v = *reinterpret_cast<const float4*>(part + p * D + col);
+            s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
+        }
+    }
+#pragma unroll
+    for (int off = 4; off < 64; off <<= 1) {
+        s.x += __shfl_xor(s.x, off, 64);
+        s.y += __shfl_xor(s.y, off, 64);
+        s.z += __shfl_xor(s.z, off, 64);
+        s.w += __shfl_xor(s.w, off, 64);
+    }
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) < 4) red[wave][ql] = s;
     __syncthreads();
-    if (rl == 0 && col < D) {
-        float t = 0.f;
-        for (int k = 0; k < 32; ++k) t += red[k][cl];
-        dw_f32[col] = t;
-        if (dw) dw[col] = f32_to_bf16(t);
+    if (threadIdx.x < 4 && col < D) {
+        float4 t = red[0][ql];
+#pragma unroll
+        for (int k = 1; k < 4; ++k) {
+            const float4 v = red[k][ql];
+            t.x += v.x; t.y += v.y; t.z += v.z; t.w += v.w;
+        }
+        *reinterpret_cast<float4*>(dw_f32 + col) = t;
+        if (dw) {
+            uint2 u;
+            u.x = pack_bf16x2(t.x, t.y);
+            u.y = pack_bf16x2(t.z, t.w);
+            *reinterpret_cast<uint2*>(dw + col) = u;
+        }
     }
 }
 
@@ -210,10 +274,11 @@ static RowShape pick_shape(int D) {
         case 8: switch (shape.nv) { FX_NORM_NV_CASES(8, CALL) } break;          \
     }
 
-static int64_t bwd_blocks(int64_t N) {
-    // about four strips per CU on a 256-CU part; never more strips than rows
-    const int64_t target = 1024;
-    return N < target ? (N > 0 ? N : 1) : target;
+// blocks of the backward (one dw partial each) for `ngroups` row groups of work:
+// two per CU on a 256-CU part, never more than there are row groups
+static int64_t bwd_blocks(int64_t ngroups) {
+    const int64_t target = 512;
+    return ngroups < target ? (ngroups > 0 ? ngroups : 1) : target;
 }
 
 }  // namespace fx
@@ -246,7 +311,7 @@ extern "C" int fx_rms_norm_fwd(const uint16_t* x, const uint16_t* w, uint16_t* y
 
 extern "C" int64_t fx_rms_norm_bwd_workspace(int64_t N, int32_t D) {
     if (N <= 0 || D <= 0) return 0;
-    return bwd_blocks(N) * (int64_t)D * (int64_t)sizeof(float);
+    return bwd_blocks(N) * (int64_t)D * (int64_t)sizeof(float);  // >= the blocks any D uses
 }
 
 extern "C" int fx_rms_norm_bwd(const uint16_t* x, const uint16_t* dy, const uint16_t* w,
@@ -254,29 +319,28 @@ extern "C" int fx_rms_norm_bwd(const uint16_t* x, const uint16_t* dy, const uint
                                float* work, int64_t N, int32_t D, void* stream) {
     if (int e = norm_check(x, w, N, D, "fx_rms_norm_bwd")) return e;
     FX_REQUIRE(dw_f32 != nullptr, "fx_rms_norm_bwd: null dw");
+    FX_REQUIRE(((uintptr_t)dw_f32 & 15) == 0 && ((uintptr_t)dw & 7) == 0 && ((uintptr_t)work & 15) == 0,
+               "fx_rms_norm_bwd: dw_f32 and work must be 16-byte aligned, dw 8-byte aligned");
     FX_REQUIRE(N == 0 || (dy != nullptr && rstd != nullptr && dx != nullptr),
                "fx_rms_norm_bwd: null pointer");
     if (N == 0) {
         // dw of an empty batch is zero
-        hipLaunchKernelGGL(rms_dw_reduce_kernel, dim3((D + 7) / 8), dim3(256), 0,
+        hipLaunchKernelGGL(rms_dw_reduce_kernel, dim3((D + 15) / 16), dim3(256), 0,
                            (hipStream_t)stream, (const float*)nullptr, (int64_t)0, (int)D, dw_f32, dw);
         return check_launch("rms_dw_reduce");
     }
     FX_REQUIRE(work != nullptr, "fx_rms_norm_bwd: null workspace");
     const RowShape s = pick_shape(D);
-    const int G = 256 / s.lpr;
-    const int64_t P0 = bwd_blocks(N);
-    int64_t rows = (N + P0 - 1) / P0;
-    rows = (rows + G - 1) / G * G;
-    const int64_t P = (N + rows - 1) / rows;  // <= P0, so `work` is large enough
+    const int G = kNormBwdThreads / s.lpr;
+    const int64_t P = bwd_blocks((N + G - 1) / G);  // every block gets a row group's worth
     const size_t lds = (size_t)D * sizeof(float);
 #define FX_CALL(L, V)                                                                          \
-    hipLaunchKernelGGL((rms_bwd_kernel<L, V>), dim3((unsigned)P), dim3(256), lds,              \
-                       (hipStream_t)stream, x, dy, w, rstd, dx, work, N, (int)D, rows)
+    hipLaunchKernelGGL((rms_bwd_kernel<L, V>), dim3((unsigned)P), dim3(kNormBwdThreads), lds,  \
+                       (hipStream_t)stream, x, dy, w, rstd, dx, work, N, (int)D)
     FX_NORM_DISPATCH(s, FX_CALL)
 #undef FX_CALL
     if (int e = check_launch("rms_norm_bwd")) return e;
-    hipLaunchKernelGGL(rms_dw_reduce_kernel, dim3((D + 7) / 8), dim3(256), 0, (hipStream_t)stream,
+    hipLaunchKernelGGL(rms_dw_reduce_kernel, dim3((D + 15) / 16), dim3(256), 0, (hipStream_t)stream,
                        (const float*)work, P, (int)D, dw_f32, dw);
     return check_launch("rms_dw_reduce");
 }

@@ -85,7 +85,12 @@ def test_argument_checks_reject_before_launch(abi):
     tl.count = 65
     st = abi.fxAdamWState()
     assert lib.fx_adamw_step(ctypes.byref(st), ctypes.byref(tl), 1, None) == abi.FX_EINVAL
-    assert lib.fx_rms_norm_bwd_workspace(65536, 768) == 1024 * 768 * 4
+    # one fp32 dw partial row per backward block: a whole number of rows, far fewer
+    # than the batch, and none for an empty batch
+    ws = lib.fx_rms_norm_bwd_workspace(65536, 768)
+    assert ws > 0 and ws % (768 * 4) == 0 and ws // (768 * 4) <= 65536 // 16
+    assert lib.fx_rms_norm_bwd_workspace(3, 768) == 3 * 768 * 4
+    assert lib.fx_rms_norm_bwd_workspace(0, 768) == 0
 
 
 def test_adamw_workspace_counts_chunks(abi):
