@@ -144,15 +144,118 @@ __device__ __forceinline__ void store4(uint16_t* p, const f32x16& c, int r, floa
 }
 
 // ---------------------------------------------------------------------------
+// Tile staging by direct global -> LDS loads (global_load_lds_dwordx4).
+//
+// A tile of R rows x D columns lives in LDS with row stride D + 8 elements (the pad
+// keeps the MFMA operand reads free of bank conflicts), i.e. SPR = D/8 + 1 16-byte
+// slots per row.  A wave-wide global_load_lds writes 64 consecutive slots (lane i ->
+// slot base + i), so a tile is covered slot by slot: slot s holds row s / SPR, chunk
+// s % SPR; the pad slot re-reads the row's last chunk and rows past the end of the
+// sequence read a zero line.  The loads need no registers and no LDS stores; they are
+// complete once the issuing wave's vmcnt drains, and visible to the other waves after
+// the following barrier.
+
+// 16 zero bytes in global memory: the source of tile rows past the sequence end
+__device__ __attribute__((aligned(16))) uint32_t g_zero_line[4];
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// global_load_lds_dwordx4 from per-lane address `src` to LDS slots lds + 16 * lane.
+// Issued as inline asm so that the compiler's wait-count pass does not treat every
+// later LDS read as possibly depending on it (it would insert vmcnt(0) before the
+// reads of the other stage and serialise the prefetch); the protocol waits for the
+// loads itself (tile_arrive).  vmcnt completes in order, so loads the compiler does
+// not know about only make its own waits stricter.  `lds` must be wave-uniform.
+// M0 (which the instruction reads as the LDS base) is saved and restored inside the
+// statement, so whatever the compiler keeps in it survives.
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, off\n\t"
+        "s_nop 0\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(src), "s"(lds)
+        : "memory");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(lds_void*)p;
+}
+
+// Two R x D tiles (K and V, or Q and dO) staged together: 2 * R * SPR / 64 wave
+// instructions dealt round-robin to the workgroup's waves.
+template <int D, int R>
+struct TileDma2 {
+    static constexpr int SPR = D / 8 + 1;
+    static constexpr int NI = R * SPR / 64;  // wave instructions per tile
+    static_assert(R * SPR % 64 == 0, "tile must be a whole number of wave loads");
+    static constexpr int PW = (2 * NI + kAttWaves - 1) / kAttWaves;  // per wave, at most
+    int off[PW];  // element offset of this lane's chunk from the tile's first row
+    int row[PW];  // tile row of this lane's chunk
+    int wave;
+    __device__ __forceinline__ void init(int64_t rs0, int64_t rs1) {
+        wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+        const int lane = threadIdx.x & 63;
+#pragma unroll
+        for (int k = 0; k < PW; ++k) {
+            const int i = wave + k * kAttWaves;
+            const int s = (i % NI) * 64 + lane;
+            const int r = s / SPR;
+            int c = s - r * SPR;
+            if (c == SPR - 1) c = SPR - 2;  // pad slot: any in-row chunk
+            row[k] = r;
+            off[k] = (int)(r * (i < NI ? rs0 : rs1)) + c * 8;
+        }
+    }
+    // first0/first1: the tiles' first rows in global memory; rows >= valid read zeros
+    __device__ __forceinline__ void issue(const uint16_t* first0, const uint16_t* first1, int valid,
+                                          const uint16_t* lds0, const uint16_t* lds1) const {
+#pragma unroll
+        for (int k = 0; k < PW; ++k) {
+            const int i = wave + k * kAttWaves;
+            if (i < 2 * NI) {
+                const bool second = i >= NI;
+                const uint16_t* src = (second ? first1 : first0) + off[k];
+                const void* p = row[k] < valid ? (const void*)src : (const void*)g_zero_line;
+                const uint16_t* dst = (second ? lds1 : lds0) + (i - (second ? NI : 0)) * 64 * 8;
+                dma16(p, __builtin_amdgcn_readfirstlane(lds_addr(dst)));
+            }
+        }
+    }
+};
+
+// Wait for this wave's outstanding vector-memory operations (including its tile
+// loads), then barrier: afterwards every wave's loads of the tile are visible.
+__device__ __forceinline__ void tile_arrive() {
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
+    __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
 // forward
+
+// max / sum over the two lanes l and l ^ 32 that hold the same query column: one
+// v_permlane32_swap hands every lane both values (same operand order in both lanes,
+// so both end with the same bits)
+__device__ __forceinline__ float pair_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 template <int D>
 __global__ void __launch_bounds__(kAttThreads) attn_fwd_kernel(fxAttnArgs a) {
     constexpr int LD = D + 8;
     constexpr int DC = D / 16;  // K chunks of Q.K
     constexpr int DT = D / 32;  // 32-row tiles of O^T
-    __shared__ __attribute__((aligned(16))) uint16_t sk[2][kBN * LD];
-    __shared__ __attribute__((aligned(16))) uint16_t sv[2][kBN * LD];
+    __shared__ __attribute__((aligned(16))) uint16_t sk0[kBN * LD], sk1[kBN * LD];
+    __shared__ __attribute__((aligned(16))) uint16_t sv0[kBN * LD], sv1[kBN * LD];
 
     const int T = a.T;
     const int nqt = (T + kBM - 1) / kBM;
@@ -171,11 +274,9 @@ __global__ void __launch_bounds__(kAttThreads) attn_fwd_kernel(fxAttnArgs a) {
     const int kend = a.causal ? min(T, q0 + kBM) : T;
     const int nblk = (kend + kBN - 1) / kBN;
 
-    TileRegs<D, kBN> rk, rv;
-    rk.init(a.kst);
-    rv.init(a.vst);
-    rk.load(kbase, T);
-    rv.load(vbase, T);
+    TileDma2<D, kBN> dma;
+    dma.init(a.kst, a.vst);
+    dma.issue(kbase, vbase, T, sk0, sv0);
 
     bf16x8 qop[DC];
     {
@@ -187,9 +288,6 @@ __global__ void __launch_bounds__(kAttThreads) attn_fwd_kernel(fxAttnArgs a) {
             qop[c] = as_bf16x8(v);
         }
     }
-    rk.store(sk[0]);
-    rv.store(sv[0]);
-    __syncthreads();
 
     const float sl2 = a.scale * kLog2e;
     float m_run = kNegInfA, l_run = 0.f;
@@ -197,37 +295,28 @@ __global__ void __launch_bounds__(kAttThreads) attn_fwd_kernel(fxAttnArgs a) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16{};
 
-    for (int j = 0; j < nblk; ++j) {
+    // one 64-key tile: K/V in (K, V); the next tile's loads go to (nK, nV)
+    auto step = [&](int j, const uint16_t* K, const uint16_t* V, uint16_t* nK, uint16_t* nV) {
         const int kb = j * kBN;
-        const int buf = j & 1;
-        const bool more = j + 1 < nblk;
-        if (more) {
-            rk.load(kbase + (int64_t)(kb + kBN) * a.kst, T - kb - kBN);
-            rv.load(vbase + (int64_t)(kb + kBN) * a.vst, T - kb - kBN);
-        }
-        const uint16_t* K = sk[buf];
-        const uint16_t* V = sv[buf];
+        tile_arrive();
+        if (j + 1 < nblk)
+            dma.issue(kbase + (int64_t)(kb + kBN) * a.kst, vbase + (int64_t)(kb + kBN) * a.vst,
+                      T - kb - kBN, nK, nV);
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             const int kh = kb + 32 * hh;  // first key of this half
-            if (a.causal && kh > q0w + 31) continue;  // every key of the half is masked for this wave
+            if (kh >= T || (a.causal && kh > q0w + 31)) continue;  // every key masked for this wave
             bf16x8 kop[DC];
 #pragma unroll
             for (int c = 0; c < DC; ++c) kop[c] = lds_op_row(K, LD, 32 * hh, 16 * c, lane);
-            f32x16 s0 = f32x16{}, s1 = f32x16{};  // two chains over the halves of D
+            f32x16 sc = f32x16{};
 #pragma unroll
-            for (int c = 0; c < DC / 2; ++c) {
-                s0 = mfma32(kop[c], qop[c], s0);
-                s1 = mfma32(kop[c + DC / 2], qop[c + DC / 2], s1);
-            }
+            for (int c = 0; c < DC; ++c) sc = mfma32(kop[c], qop[c], sc);
             bf16x8 vop[DT][2];
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
                 for (int kc = 0; kc < 2; ++kc) vop[dt][kc] = lds_op_t(V, LD, 32 * hh + 16 * kc, 32 * dt, lane);
-            f32x16 sc;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) sc[i] = s0[i] + s1[i];
             if ((kh + 32 > T) || (a.causal && kh + 31 > q0w)) {
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
@@ -238,7 +327,7 @@ __global__ void __launch_bounds__(kAttThreads) attn_fwd_kernel(fxAttnArgs a) {
             float mloc = sc[0];
 #pragma unroll
             for (int i = 1; i < 16; ++i) mloc = fmaxf(mloc, sc[i]);
-            mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+            mloc = pair_max(mloc);
             const float m_new = fmaxf(m_run, mloc * sl2);
             const bool need = m_new > m_run + kLazyRescale;
             float alpha = 1.f;
@@ -247,14 +336,14 @@ __global__ void __launch_bounds__(kAttThreads) attn_fwd_kernel(fxAttnArgs a) {
                 m_run = m_new;
             }
             const float mu = (m_run == kNegInfA) ? 0.f : m_run;
-            float rs = 0.f;
+            float r4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const float p = exp2_fast(fmaf(sc[i], sl2, -mu));
                 sc[i] = p;
-                rs += p;
+                r4[i & 3] += p;
             }
-            l_run = l_run * alpha + rs;
+            l_run = l_run * alpha + ((r4[0] + r4[1]) + (r4[2] + r4[3]));
             if (__ballot(need)) {
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt)
@@ -268,14 +357,15 @@ __global__ void __launch_bounds__(kAttThreads) attn_fwd_kernel(fxAttnArgs a) {
                 acc[dt] = mfma32(vop[dt][1], p1, acc[dt]);
             }
         }
-        if (more) {
-            rk.store(sk[buf ^ 1]);
-            rv.store(sv[buf ^ 1]);
-        }
-        __syncthreads();
+    };
+    // stages alternate with the tile parity; unrolled by two so that each LDS access
+    // names its stage array
+    for (int j = 0; j < nblk; j += 2) {
+        step(j, sk0, sv0, sk1, sv1);
+        if (j + 1 < nblk) step(j + 1, sk1, sv1, sk0, sv0);
     }
 
-    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    const float l_tot = pair_sum(l_run);
     if (qi < T) {
         const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
         uint16_t* orow = a.o_out + (((int64_t)b * T + qi) * a.H + h) * D;
