@@ -22,9 +22,9 @@
 // m + log l or -inf, Delta from the bf16 output, dS = P (dP - Delta) scale).
 //
 // Each tile's MFMA operands are read from LDS up front and the independent
-// accumulator chains are interleaved, so LDS latency and MFMA dependencies overlap;
-// K/V (Q/dO) tiles are double-buffered in LDS with the next tile's global loads in
-// flight during the current tile's math (one barrier per tile).
+// accumulator chains are interleaved, so LDS latency and MFMA dependencies overlap.
+// K/V (Q/dO) tiles are double-buffered in LDS and filled by direct global -> LDS
+// loads that are in flight during the previous tile's math (one barrier per tile).
 #include <math.h>
 
 #include "fx_device.h"
@@ -87,52 +87,17 @@ __device__ __forceinline__ bf16x8 lds_op_row(const uint16_t* tile, int ld, int r
 // row index (within a 32-row accumulator tile) of accumulator element i of lane l
 __device__ __forceinline__ int acc_row(int i, int lane) { return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3); }
 
-// Register staging of a tile for software pipelining.  init() fixes this thread's
-// vectors of a tile (row, element offset row*rs + col); load() issues the global
-// reads of one tile given its first row's address (rows past `valid_rows` read row 0
-// and are zeroed, so there is no divergent branch); store() writes them to an LDS
-// tile of row stride D+8 once its previous contents are no longer read.
-template <int D, int R>
-struct TileRegs {
-    static constexpr int VPR = D / 8;
-    static constexpr int NV = R * VPR / kAttThreads;
-    static_assert(R * VPR % kAttThreads == 0, "tile must split evenly over the workgroup");
-    uint4 v[NV];
-    int row[NV];
-    int off[NV];
-    __device__ __forceinline__ void init(int64_t rs) {
-#pragma unroll
-        for (int it = 0; it < NV; ++it) {
-            const int idx = it * kAttThreads + threadIdx.x;
-            row[it] = idx / VPR;
-            off[it] = (int)(row[it] * rs) + (idx % VPR) * 8;
-        }
-    }
-    __device__ __forceinline__ void load(const uint16_t* first_row, int valid_rows) {
-#pragma unroll
-        for (int it = 0; it < NV; ++it) {
-            const bool ok = row[it] < valid_rows;
-            const uint4 x = ld16(first_row + (ok ? off[it] : 0));
-            v[it] = ok ? x : make_uint4(0u, 0u, 0u, 0u);
-        }
-    }
-    __device__ __forceinline__ void store(uint16_t* tile) const {
-#pragma unroll
-        for (int it = 0; it < NV; ++it) {
-            const int idx = it * kAttThreads + threadIdx.x;
-            *reinterpret_cast<uint4*>(tile + (idx / VPR) * (D + 8) + (idx % VPR) * 8) = v[it];
-        }
-    }
-};
-
-// 1-D grid over (bh, tile): consecutive tiles of one (b, h) land on one XCD
-// (workgroups are dealt round-robin to the 8 XCDs), so they share its L2.
+// 1-D grid over (tile rank, bh), rank-major: all heads' rank-0 tiles are dispatched
+// first, so with ranks ordered by decreasing causal work the longest workgroups start
+// first and the short ones fill the tail (bh-major order left heavy tiles of the last
+// heads for the end: 63 -> 50 us at [16,12,1024,64] causal forward).  Workgroups are
+// dealt round-robin to the 8 XCDs, so with nbh % 8 == 0 every tile of one head runs
+// on the same XCD and shares its L2.
 __device__ __forceinline__ void grid_map(int ntiles, int nbh, int& bh, int& tile) {
-    const int G = ntiles * nbh;
-    int x = blockIdx.x;
-    if ((G & 7) == 0) x = (x & 7) * (G >> 3) + (x >> 3);
-    bh = x / ntiles;
-    tile = x - bh * ntiles;
+    (void)ntiles;
+    const int x = blockIdx.x;
+    tile = x / nbh;
+    bh = x - tile * nbh;
 }
 
 // 4 consecutive fp32 accumulator values (elements 4r..4r+3) * mul -> 4 bf16 (8-byte store)
@@ -386,8 +351,8 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dq_kern
     constexpr int LD = D + 8;
     constexpr int DC = D / 16;
     constexpr int DT = D / 32;
-    __shared__ __attribute__((aligned(16))) uint16_t sk[2][kBN * LD];
-    __shared__ __attribute__((aligned(16))) uint16_t sv[2][kBN * LD];
+    __shared__ __attribute__((aligned(16))) uint16_t sk0[kBN * LD], sk1[kBN * LD];
+    __shared__ __attribute__((aligned(16))) uint16_t sv0[kBN * LD], sv1[kBN * LD];
 
     const int T = a.T;
     const int nqt = (T + kBM - 1) / kBM;
@@ -406,11 +371,9 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dq_kern
     const uint16_t* vbase = a.v + b * a.vsb + h * a.vsh;
     const int kend = a.causal ? min(T, q0 + kBM) : T;
     const int nblk = (kend + kBN - 1) / kBN;
-    TileRegs<D, kBN> rk, rv;
-    rk.init(a.kst);
-    rv.init(a.vst);
-    rk.load(kbase, T);
-    rv.load(vbase, T);
+    TileDma2<D, kBN> dma;
+    dma.init(a.kst, a.vst);
+    dma.issue(kbase, vbase, T, sk0, sv0);
 
     // Q^T and dO^T operands, Delta = rowsum(dO * O) for this lane's query
     bf16x8 qop[DC], dop[DC];
@@ -434,33 +397,26 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dq_kern
 #pragma unroll
             for (int j = 0; j < 8; ++j) delta += fd[j] * fo[j];
         }
-        delta += __shfl_xor(delta, 32, 64);
+        delta = pair_sum(delta);
         if (qok && g == 0) a.delta[(int64_t)bh * T + qi] = delta;
     }
     const float lse2 = qok ? a.lse[(int64_t)bh * T + qi] * kLog2e : 0.f;
     const float sl2 = a.scale * kLog2e;
-    rk.store(sk[0]);
-    rv.store(sv[0]);
-    __syncthreads();
 
     f32x16 acc[DT];
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16{};
 
-    for (int j = 0; j < nblk; ++j) {
+    auto step = [&](int j, const uint16_t* K, const uint16_t* V, uint16_t* nK, uint16_t* nV) {
         const int kb = j * kBN;
-        const int buf = j & 1;
-        const bool more = j + 1 < nblk;
-        if (more) {
-            rk.load(kbase + (int64_t)(kb + kBN) * a.kst, T - kb - kBN);
-            rv.load(vbase + (int64_t)(kb + kBN) * a.vst, T - kb - kBN);
-        }
-        const uint16_t* K = sk[buf];
-        const uint16_t* V = sv[buf];
+        tile_arrive();
+        if (j + 1 < nblk)
+            dma.issue(kbase + (int64_t)(kb + kBN) * a.kst, vbase + (int64_t)(kb + kBN) * a.vst,
+                      T - kb - kBN, nK, nV);
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             const int kh = kb + 32 * hh;
-            if (a.causal && kh > q0w + 31) continue;
+            if (kh >= T || (a.causal && kh > q0w + 31)) continue;
             bf16x8 kop[DC], vop[DC];
 #pragma unroll
             for (int c = 0; c < DC; ++c) {
@@ -495,11 +451,10 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dq_kern
                 acc[dt] = mfma32(ktop[dt][1], d1, acc[dt]);
             }
         }
-        if (more) {
-            rk.store(sk[buf ^ 1]);
-            rv.store(sv[buf ^ 1]);
-        }
-        __syncthreads();
+    };
+    for (int j = 0; j < nblk; j += 2) {
+        step(j, sk0, sv0, sk1, sv1);
+        if (j + 1 < nblk) step(j + 1, sk1, sv1, sk0, sv0);
     }
 
     if (qok) {
@@ -519,8 +474,8 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dkv_ker
     constexpr int LD = D + 8;
     constexpr int DC = D / 16;
     constexpr int DT = D / 32;
-    __shared__ __attribute__((aligned(16))) uint16_t sq[2][kBQ * LD];
-    __shared__ __attribute__((aligned(16))) uint16_t sdo[2][kBQ * LD];
+    __shared__ __attribute__((aligned(16))) uint16_t sq0[kBQ * LD], sq1[kBQ * LD];
+    __shared__ __attribute__((aligned(16))) uint16_t sdo0[kBQ * LD], sdo1[kBQ * LD];
     __shared__ __attribute__((aligned(16))) float slse[2][kBQ];
     __shared__ __attribute__((aligned(16))) float sdelta[2][kBQ];
 
@@ -544,28 +499,20 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dkv_ker
     const int qstart = a.causal ? k0 : 0;  // k0 is a multiple of kBQ
     const int nblk = (T - qstart + kBQ - 1) / kBQ;
 
-    TileRegs<D, kBQ> rq, rd;
-    rq.init(a.qst);
-    rd.init(dors);
+    // Q / dO tiles by DMA; the tile's lse and Delta through one register each
+    // (threads 0..63), stored to LDS once they have arrived
+    TileDma2<D, kBQ> dma;
+    dma.init(a.qst, dors);
     float rl = 0.f, rdl = 0.f;
-    auto load_rows = [&](int qb) {
-        rq.load(qbase + (int64_t)qb * a.qst, T - qb);
-        rd.load(dobase + (int64_t)qb * dors, T - qb);
+    auto issue = [&](int qb, const uint16_t* nQ, const uint16_t* nDO) {
+        dma.issue(qbase + (int64_t)qb * a.qst, dobase + (int64_t)qb * dors, T - qb, nQ, nDO);
         if (threadIdx.x < kBQ) {
             const int q = qb + threadIdx.x;
             rl = q < T ? lse_bh[q] * kLog2e : 0.f;
             rdl = q < T ? del_bh[q] : 0.f;
         }
     };
-    auto store_rows = [&](int buf) {
-        rq.store(sq[buf]);
-        rd.store(sdo[buf]);
-        if (threadIdx.x < kBQ) {
-            slse[buf][threadIdx.x] = rl;
-            sdelta[buf][threadIdx.x] = rdl;
-        }
-    };
-    if (nblk > 0) load_rows(qstart);
+    if (nblk > 0) issue(qstart, sq0, sdo0);
 
     bf16x8 kop[DC], vop[DC];
     {
@@ -583,8 +530,6 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dkv_ker
         }
     }
     const float sl2 = a.scale * kLog2e;
-    if (nblk > 0) store_rows(0);
-    __syncthreads();
 
     f32x16 adv[DT], adk[DT];
 #pragma unroll
@@ -593,17 +538,20 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dkv_ker
         adk[dt] = f32x16{};
     }
 
-    for (int j = 0; j < nblk; ++j) {
+    auto step = [&](int j, const uint16_t* Q, const uint16_t* DO, uint16_t* nQ, uint16_t* nDO) {
         const int qb = qstart + j * kBQ;
-        const int buf = j & 1;
-        const bool more = j + 1 < nblk;
-        if (more) load_rows(qb + kBQ);
-        const uint16_t* Q = sq[buf];
-        const uint16_t* DO = sdo[buf];
+        const int st = j & 1;
+        __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's tile loads and rl / rdl
+        if (threadIdx.x < kBQ) {
+            slse[st][threadIdx.x] = rl;
+            sdelta[st][threadIdx.x] = rdl;
+        }
+        __syncthreads();
+        if (j + 1 < nblk) issue(qb + kBQ, nQ, nDO);
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             const int qh = qb + 32 * hh;  // first query of this half
-            if (a.causal && qh + 31 < k0w) continue;  // all of this wave's keys follow these queries
+            if (qh >= T || (a.causal && qh + 31 < k0w)) continue;  // all of this wave's keys follow these queries
             bf16x8 qa[DC], da[DC];
 #pragma unroll
             for (int c = 0; c < DC; ++c) {
@@ -614,8 +562,8 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dkv_ker
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int qr = 32 * hh + 8 * r + 4 * g;  // 4 consecutive queries of this lane
-                l4[r] = *reinterpret_cast<const float4*>(&slse[buf][qr]);
-                d4[r] = *reinterpret_cast<const float4*>(&sdelta[buf][qr]);
+                l4[r] = *reinterpret_cast<const float4*>(&slse[st][qr]);
+                d4[r] = *reinterpret_cast<const float4*>(&sdelta[st][qr]);
             }
             f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
@@ -658,8 +606,10 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dkv_ker
                 adk[dt] = mfma32(qtr[dt][1], d1, adk[dt]);
             }
         }
-        if (more) store_rows(buf ^ 1);
-        __syncthreads();
+    };
+    for (int j = 0; j < nblk; j += 2) {
+        step(j, sq0, sdo0, sq1, sdo1);
+        if (j + 1 < nblk) step(j + 1, sq1, sdo1, sq0, sdo0);
     }
 
     if (kok) {
