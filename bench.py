@@ -1,6 +1,8 @@
 """Benchmark: the fxlm GPT 12L-d768 training step on one MI355X, plus the hot-path kernels.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+    python bench.py --only {attention,ce,norm,adamw,linear,step,copy}   (profiling runs)
+    python bench.py --pmc-summary FETCH.csv WRITE.csv COPY_FETCH.csv COPY_WRITE.csv
 
 Workload: GPT with 12 layers, d_model 768, 12 heads of
 64, RMSNorm (fused), fused-linear GELU MLP 3072, vocab 50304, causal S=1024,
@@ -226,13 +228,81 @@ def cpu_baseline(torch):
                        f"1 warm-up + {n} timed steps ({dt:.2f} s/step) on {cores} threads, {cpu_model}")}
 
 
+def bench_copy(torch):
+    """Calibration workload for the HBM byte counters: torch's copy of 1 GiB."""
+    n = 1 << 29
+    a = torch.empty(n, device="cuda", dtype=torch.bfloat16).fill_(1.0)
+    b = torch.empty_like(a)
+    t = time_us(torch, lambda: b.copy_(a), iters=5, warm=2)
+    return {"bytes_read": n * 2, "bytes_written": n * 2, "us": round(t, 2)}
+
+
+TRAFFIC_JSON = os.path.join(ROOT, "profiles", "attn_bwd_cfg2_traffic.json")
+_TRAFFIC_KERNELS = ("attn_bwd_dq_kernel", "attn_bwd_dkv_kernel")
+
+
+def _pmc_per_dispatch(csv_path, counter, name_filter):
+    """Average of `counter` (KiB) per dispatch of kernels whose name contains name_filter,
+    from a rocprofv3 --pmc counter_collection.csv."""
+    import csv
+    vals = {}
+    with open(csv_path) as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] != counter or name_filter not in r["Kernel_Name"]:
+                continue
+            vals.setdefault(r["Dispatch_Id"], 0.0)
+            vals[r["Dispatch_Id"]] += float(r["Counter_Value"])
+    if not vals:
+        raise SystemExit(f"{csv_path}: no {counter} rows for kernels matching {name_filter!r}")
+    return sum(vals.values()) / len(vals), len(vals)
+
+
+def pmc_summary(fetch_csv, write_csv, copy_fetch_csv, copy_write_csv):
+    """HBM bytes per fx_attn_bwd launch from FETCH_SIZE / WRITE_SIZE (KiB per dispatch),
+    each scaled by what the counter reads for torch's 1 GiB copy (known bytes)."""
+    known = 1 << 30
+    cf, _ = _pmc_per_dispatch(copy_fetch_csv, "FETCH_SIZE", "copy")
+    cw, _ = _pmc_per_dispatch(copy_write_csv, "WRITE_SIZE", "copy")
+    sf, sw = known / (cf * 1024.0), known / (cw * 1024.0)
+    out = {"scale_fetch": sf, "scale_write": sw, "kernels": {}}
+    tot = 0.0
+    for k in _TRAFFIC_KERNELS:
+        f, nf = _pmc_per_dispatch(fetch_csv, "FETCH_SIZE", k)
+        w, nw = _pmc_per_dispatch(write_csv, "WRITE_SIZE", k)
+        fb, wb = f * 1024.0 * sf, w * 1024.0 * sw
+        out["kernels"][k] = {"fetch_kib": f, "write_kib": w, "dispatches": [nf, nw],
+                             "fetch_bytes": fb, "write_bytes": wb}
+        tot += fb + wb
+    out["traffic_bytes_per_launch"] = tot
+    return out
+
+
+def _traffic():
+    try:
+        with open(TRAFFIC_JSON) as f:
+            return round(json.load(f)["traffic_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU baseline")
+    ap.add_argument("--only", choices=["attention", "ce", "norm", "adamw", "linear", "step", "copy"],
+                    help="run one workload and print its figures (for profiling runs)")
+    ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV",
+                                                       "COPY_WRITE_CSV"),
+                    help="write the fx_attn_bwd HBM traffic from rocprofv3 --pmc csv files")
     args = ap.parse_args()
+    if args.pmc_summary:
+        res = pmc_summary(*args.pmc_summary)
+        with open(TRAFFIC_JSON, "w") as f:
+            json.dump(res, f, indent=1)
+        print(json.dumps(res))
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): the fxlm hot path is "
               "single-GPU; see DESIGN.md for how it would shard.", file=sys.stderr)
@@ -240,6 +310,13 @@ def main():
     import torch
     from fxgpu.abi import lib
     lib()
+    if args.only:
+        fn = {"attention": bench_attention, "ce": bench_ce, "norm": bench_norm, "adamw": bench_adamw,
+              "linear": bench_linear, "copy": bench_copy,
+              "step": lambda t: gpu_step_bench(t, args.steps, args.warmup)}[args.only]
+        r = fn(torch)
+        print(json.dumps({k: v for k, v in r.items() if not k.startswith("flop")}))
+        return
 
     attn = bench_attention(torch)
     ce = bench_ce(torch)
@@ -255,7 +332,9 @@ def main():
         "bound": "mfma", "achieved": round(attn["flop_bwd"] / attn["bwd_us"] / 1e6, 1),
         "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
         "frac": round(attn["flop_bwd"] / attn["bwd_us"] / 1e6 / BF16_PEAK_TFLOPS, 4),
-        "traffic": None,
+        # HBM bytes per fx_attn_bwd launch: rocprofv3 FETCH_SIZE + WRITE_SIZE of the two
+        # kernels, calibrated on a copy of known size (profiles/attn_bwd_cfg2_traffic.*)
+        "traffic": _traffic(),
     }
     cpu = None if args.no_cpu else cpu_baseline(torch)
     out = {
