@@ -181,7 +181,7 @@ typedef struct fxAttnArgs {
     int64_t qsb, qst, qsh, ksb, kst, ksh, vsb, vst, vsh;
     int64_t dqb, dqt, dqh, dkb, dkt, dkh, dvb, dvt, dvh;
     int32_t B, T, H, D;       /* D in {64, 128} */
-    float scale;
+    float scale;              /* > 0 and finite (1/sqrt(D) in fxlm) */
     int32_t causal;
 } fxAttnArgs;
 

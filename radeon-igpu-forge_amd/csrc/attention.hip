@@ -84,8 +84,17 @@ __device__ __forceinline__ bf16x8 lds_op_row(const uint16_t* tile, int ld, int r
     return *reinterpret_cast<const bf16x8*>(tile + (r0 + (lane & 31)) * ld + c0 + 8 * (lane >> 5));
 }
 
-// row index (within a 32-row accumulator tile) of accumulator element i of lane l
-__device__ __forceinline__ int acc_row(int i, int lane) { return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3); }
+// row index (within a 32-row accumulator tile) of accumulator element i of lane l is
+// acc_c(i) + 4 * (l / 32), acc_c(i) a compile-time constant once i is unrolled
+__device__ __forceinline__ constexpr int acc_c(int i) { return 8 * (i >> 2) + (i & 3); }
+
+// -inf into the elements whose row offset acc_c(i) lies outside [lo, hi] (one compare
+// pair and one select per element; lo / hi already hold the lane's 4 * (l / 32) shift)
+__device__ __forceinline__ void mask_rows(f32x16& x, int lo, int hi) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        if (acc_c(i) < lo || acc_c(i) > hi) x[i] = kNegInfA;
+}
 
 // 1-D grid over (tile rank, bh), rank-major: all heads' rank-0 tiles are dispatched
 // first, so with ranks ordered by decreasing causal work the longest workgroups start
@@ -125,14 +134,16 @@ __device__ __attribute__((aligned(16))) uint32_t g_zero_line[4];
 
 typedef __attribute__((address_space(3))) void lds_void;
 
-// global_load_lds_dwordx4 from per-lane address `src` to LDS slots lds + 16 * lane.
-// Issued as inline asm so that the compiler's wait-count pass does not treat every
-// later LDS read as possibly depending on it (it would insert vmcnt(0) before the
-// reads of the other stage and serialise the prefetch); the protocol waits for the
-// loads itself (tile_arrive).  vmcnt completes in order, so loads the compiler does
-// not know about only make its own waits stricter.  `lds` must be wave-uniform.
-// M0 (which the instruction reads as the LDS base) is saved and restored inside the
-// statement, so whatever the compiler keeps in it survives.
+// global_load_lds_dwordx4 to LDS slots lds + 16 * lane, from per-lane address `src`
+// (dma16) or from the wave-uniform base `sbase` plus a per-lane 32-bit byte offset
+// (dma16_so: no 64-bit address arithmetic per lane).  Issued as inline asm so that the
+// compiler's wait-count pass does not treat every later LDS read as possibly
+// depending on it (it would insert vmcnt(0) before the reads of the other stage and
+// serialise the prefetch); the protocol waits for the loads itself (tile_arrive).
+// vmcnt completes in order, so loads the compiler does not know about only make its
+// own waits stricter.  `lds` must be wave-uniform.  M0 (the LDS base the instruction
+// reads) is saved and restored inside the statement, so whatever the compiler keeps
+// in it survives.
 __device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
     uint32_t saved;
     asm volatile(
@@ -144,6 +155,19 @@ __device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
         "s_mov_b32 m0, %0"
         : "=&s"(saved)
         : "v"(src), "s"(lds)
+        : "memory");
+}
+__device__ __forceinline__ void dma16_so(const void* sbase, uint32_t voff, uint32_t lds) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %3\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %2\n\t"
+        "s_nop 0\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(voff), "s"(sbase), "s"(lds)
         : "memory");
 }
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
@@ -158,8 +182,8 @@ struct TileDma2 {
     static constexpr int NI = R * SPR / 64;  // wave instructions per tile
     static_assert(R * SPR % 64 == 0, "tile must be a whole number of wave loads");
     static constexpr int PW = (2 * NI + kAttWaves - 1) / kAttWaves;  // per wave, at most
-    int off[PW];  // element offset of this lane's chunk from the tile's first row
-    int row[PW];  // tile row of this lane's chunk
+    uint32_t off[PW];  // byte offset of this lane's chunk from the tile's first row
+    int row[PW];       // tile row of this lane's chunk
     int wave;
     __device__ __forceinline__ void init(int64_t rs0, int64_t rs1) {
         wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -172,21 +196,27 @@ struct TileDma2 {
             int c = s - r * SPR;
             if (c == SPR - 1) c = SPR - 2;  // pad slot: any in-row chunk
             row[k] = r;
-            off[k] = (int)(r * (i < NI ? rs0 : rs1)) + c * 8;
+            off[k] = (uint32_t)(r * (i < NI ? rs0 : rs1) + c * 8) * 2u;
         }
     }
     // first0/first1: the tiles' first rows in global memory; rows >= valid read zeros
     __device__ __forceinline__ void issue(const uint16_t* first0, const uint16_t* first1, int valid,
                                           const uint16_t* lds0, const uint16_t* lds1) const {
+        const bool full = valid >= R;  // wave-uniform: every row of the tile exists
 #pragma unroll
         for (int k = 0; k < PW; ++k) {
             const int i = wave + k * kAttWaves;
             if (i < 2 * NI) {
                 const bool second = i >= NI;
-                const uint16_t* src = (second ? first1 : first0) + off[k];
-                const void* p = row[k] < valid ? (const void*)src : (const void*)g_zero_line;
-                const uint16_t* dst = (second ? lds1 : lds0) + (i - (second ? NI : 0)) * 64 * 8;
-                dma16(p, __builtin_amdgcn_readfirstlane(lds_addr(dst)));
+                const uint16_t* base = second ? first1 : first0;
+                const uint32_t dst = lds_addr((second ? lds1 : lds0) + (i - (second ? NI : 0)) * 64 * 8);
+                if (full) {
+                    dma16_so(base, off[k], dst);
+                } else {
+                    const void* p = row[k] < valid ? (const void*)((const char*)base + off[k])
+                                                   : (const void*)g_zero_line;
+                    dma16(p, dst);
+                }
             }
         }
     }
@@ -282,13 +312,8 @@ __global__ void __launch_bounds__(kAttThreads) attn_fwd_kernel(fxAttnArgs a) {
             for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
                 for (int kc = 0; kc < 2; ++kc) vop[dt][kc] = lds_op_t(V, LD, 32 * hh + 16 * kc, 32 * dt, lane);
-            if ((kh + 32 > T) || (a.causal && kh + 31 > q0w)) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int key = kh + acc_row(i, lane);
-                    if (key >= T || (a.causal && key > qi)) sc[i] = kNegInfA;
-                }
-            }
+            if ((kh + 32 > T) || (a.causal && kh + 31 > q0w))  // keys past T or after the query
+                mask_rows(sc, 0, (a.causal ? min(qi, T - 1) : T - 1) - kh - 4 * g);
             float mloc = sc[0];
 #pragma unroll
             for (int i = 1; i < 16; ++i) mloc = fmaxf(mloc, sc[i]);
@@ -434,14 +459,11 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dq_kern
             for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
                 for (int kc = 0; kc < 2; ++kc) ktop[dt][kc] = lds_op_t(K, LD, 32 * hh + 16 * kc, 32 * dt, lane);
-            const bool need_mask = (kh + 32 > T) || (a.causal && kh + 31 > q0w);
+            if ((kh + 32 > T) || (a.causal && kh + 31 > q0w))  // masked scores give P = 0
+                mask_rows(s, 0, (a.causal ? min(qi, T - 1) : T - 1) - kh - 4 * g);
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                float p = exp2_fast(fmaf(s[i], sl2, -lse2));
-                if (need_mask) {
-                    const int key = kh + acc_row(i, lane);
-                    if (key >= T || (a.causal && key > qi)) p = 0.f;
-                }
+                const float p = exp2_fast(fmaf(s[i], sl2, -lse2));
                 s[i] = p * (dp[i] - delta);  // dS^T / scale
             }
             const bf16x8 d0 = pack_op(s, 0), d1 = pack_op(s, 1);
@@ -579,7 +601,8 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dkv_ker
                     dot[dt][kc] = lds_op_t(DO, LD, 32 * hh + 16 * kc, 32 * dt, lane);
                     qtr[dt][kc] = lds_op_t(Q, LD, 32 * hh + 16 * kc, 32 * dt, lane);
                 }
-            const bool need_mask = (qh + 32 > T) || (a.causal && qh < k0w + 31);
+            if ((qh + 32 > T) || (a.causal && qh < k0w + 31))  // queries past T or before the key
+                mask_rows(s, a.causal ? ki - qh - 4 * g : INT32_MIN, T - 1 - qh - 4 * g);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const float lv[4] = {l4[r].x, l4[r].y, l4[r].z, l4[r].w};
@@ -587,11 +610,7 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dkv_ker
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int i = 4 * r + e;
-                    float p = exp2_fast(fmaf(s[i], sl2, -lv[e]));
-                    if (need_mask) {
-                        const int q = qh + 8 * r + 4 * g + e;
-                        if (q >= T || (a.causal && ki > q)) p = 0.f;
-                    }
+                    const float p = exp2_fast(fmaf(s[i], sl2, -lv[e]));
                     s[i] = p;                          // P
                     dp[i] = p * (dp[i] - dv[e]);       // dS / scale
                 }
@@ -636,6 +655,9 @@ static int attn_check(const fxAttnArgs* p, bool bwd) {
     FX_REQUIRE(a.B >= 1 && a.T >= 1 && a.H >= 1, "fx_attn: bad shape B=%d T=%d H=%d", a.B, a.T, a.H);
     FX_REQUIRE((int64_t)a.B * a.H * ((a.T + kBM - 1) / kBM) < 0x7fffffff, "fx_attn: grid too large");
     FX_REQUIRE(a.q && a.k && a.v, "fx_attn: null q/k/v");
+    // masked scores are -inf before the scale is applied: the scale must be positive
+    FX_REQUIRE(a.scale > 0.f && a.scale < __builtin_huge_valf(), "fx_attn: scale %g must be positive and finite",
+               (double)a.scale);
     const int64_t s[] = {a.qsb, a.qst, a.qsh, a.ksb, a.kst, a.ksh, a.vsb, a.vst, a.vsh};
     for (int64_t x : s) FX_REQUIRE(x % 8 == 0, "fx_attn: q/k/v strides must be multiples of 8 elements");
     FX_REQUIRE((((uintptr_t)a.q | (uintptr_t)a.k | (uintptr_t)a.v) & 15) == 0,

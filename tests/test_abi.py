@@ -81,6 +81,13 @@ def test_argument_checks_reject_before_launch(abi):
     a.D, a.B, a.T, a.H = 96, 1, 1, 1
     assert lib.fx_attn_fwd(ctypes.byref(a), None) == abi.FX_EINVAL
     assert b"head_dim 96" in lib.fx_last_error()
+    # masked scores are -inf before scaling: zero, negative or inf scales are rejected
+    for bad_scale in (0.0, -0.125, float("inf")):
+        a = abi.fxAttnArgs()
+        a.D, a.B, a.T, a.H, a.scale = 64, 1, 1, 1, bad_scale
+        a.q = a.k = a.v = 0x1000  # never dereferenced: the check fails first
+        assert lib.fx_attn_fwd(ctypes.byref(a), None) == abi.FX_EINVAL
+        assert b"scale" in lib.fx_last_error()
     tl = abi.fxTensorList()
     tl.count = 65
     st = abi.fxAdamWState()
