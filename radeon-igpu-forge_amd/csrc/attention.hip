@@ -129,51 +129,6 @@ __device__ __forceinline__ void store4(uint16_t* p, const f32x16& c, int r, floa
 // complete once the issuing wave's vmcnt drains, and visible to the other waves after
 // the following barrier.
 
-// 16 zero bytes in global memory: the source of tile rows past the sequence end
-__device__ __attribute__((aligned(16))) uint32_t g_zero_line[4];
-
-typedef __attribute__((address_space(3))) void lds_void;
-
-// global_load_lds_dwordx4 to LDS slots lds + 16 * lane, from per-lane address `src`
-// (dma16) or from the wave-uniform base `sbase` plus a per-lane 32-bit byte offset
-// (dma16_so: no 64-bit address arithmetic per lane).  Issued as inline asm so that the
-// compiler's wait-count pass does not treat every later LDS read as possibly
-// depending on it (it would insert vmcnt(0) before the reads of the other stage and
-// serialise the prefetch); the protocol waits for the loads itself (tile_arrive).
-// vmcnt completes in order, so loads the compiler does not know about only make its
-// own waits stricter.  `lds` must be wave-uniform.  M0 (the LDS base the instruction
-// reads) is saved and restored inside the statement, so whatever the compiler keeps
-// in it survives.
-__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
-    uint32_t saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %2\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %1, off\n\t"
-        "s_nop 0\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "v"(src), "s"(lds)
-        : "memory");
-}
-__device__ __forceinline__ void dma16_so(const void* sbase, uint32_t voff, uint32_t lds) {
-    uint32_t saved;
-    asm volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %3\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %1, %2\n\t"
-        "s_nop 0\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "v"(voff), "s"(sbase), "s"(lds)
-        : "memory");
-}
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return (uint32_t)(uintptr_t)(lds_void*)p;
-}
-
 // Two R x D tiles (K and V, or Q and dO) staged together: 2 * R * SPR / 64 wave
 // instructions dealt round-robin to the workgroup's waves.
 template <int D, int R>
@@ -221,13 +176,6 @@ struct TileDma2 {
         }
     }
 };
-
-// Wait for this wave's outstanding vector-memory operations (including its tile
-// loads), then barrier: afterwards every wave's loads of the tile are visible.
-__device__ __forceinline__ void tile_arrive() {
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-    __syncthreads();
-}
 
 // ---------------------------------------------------------------------------
 // forward

@@ -7,20 +7,35 @@
 // So gathering costs nothing beyond a per-row base pointer, and the gathered
 // rows can be written out (Xg) by the first column of tiles for the backward.
 //
-// Tiling: 128 x 128 output tile per workgroup, 4 waves in 2 x 2, each wave
-// 64 x 64 = 2 x 2 tiles of v_mfma_f32_32x32x16_bf16; K advances 32 per stage
-// through double-buffered LDS (row stride 40 elements) with the next stage's
-// global loads in flight during the MFMAs.  Epilogue: + bias, optional
-// GELU-tanh, optional pre-activation output.
+// Tiling: 256 x 256 output tile per workgroup (128 FLOP per byte of tile loads: a
+// 128 x 128 tile measured L2-bandwidth bound), 16 waves in 4 x 4, each wave
+// 64 x 64 = 2 x 2 tiles of v_mfma_f32_32x32x16_bf16 (128 VGPRs: 4 waves per SIMD,
+// which hide the LDS operand latency that left 8 waves of 128 x 64 at half speed).
+// K advances 64 per stage through two LDS stages (row stride 72 elements,
+// conflict-free row reads) filled by direct global -> LDS loads that are in flight
+// during the previous stage's MFMAs (147 KB of LDS: one persistent workgroup per CU
+// walking tiles, with the stage pipeline running on from one tile into the next).
+// Epilogue: + bias, optional GELU-tanh, optional pre-activation output, stored
+// from the MFMA layout so each half-wave writes 64 contiguous bytes of a row (a
+// transposed layout with 8-byte stores scattered over 32 rows measured 1.6x slower).
+// Tiles sharing an A row panel are dealt to one XCD (shared L2).
 #include <math.h>
 
 #include "fx_device.h"
 
 namespace fx {
 
-constexpr int kGBM = 128, kGBN = 128, kGBK = 32;
-constexpr int kGLD = kGBK + 8;  // LDS row stride (elements)
-constexpr int kGThreads = 256;
+constexpr int kGBM = 256, kGBN = 256, kGBK = 64;
+constexpr int kGLD = kGBK + 8;              // LDS row stride (elements)
+constexpr int kGSPR = kGBK / 8 + 1;         // 16-byte LDS slots per row (the last is padding)
+constexpr int kGNI = kGBM * kGSPR / 64;     // wave loads per 256-row tile
+constexpr int kGThreads = 1024;
+constexpr int kGWaves = kGThreads / 64;
+constexpr int kGPW = (2 * kGNI + kGWaves - 1) / kGWaves;  // wave loads per wave per stage (A and W)
+constexpr int kGWM = 64, kGWN = 64;         // wave tile: 16 waves in 4 (M) x 4 (N)
+constexpr int kGTI = kGWM / 32, kGTJ = kGWN / 32;  // 32 x 32 MFMA tiles per wave
+static_assert(kGBM == kGBN && kGBM * kGSPR % 64 == 0, "tile shape");
+static_assert((kGBM / kGWM) * (kGBN / kGWN) == kGWaves, "wave layout");
 
 struct GemmArgs {
     const uint16_t* A;
@@ -38,134 +53,188 @@ struct GemmArgs {
     uint16_t* Xg;
     int64_t ldxg;
     int M, N, K;
-    int act;  // 0: identity, 1: GELU (tanh approximation)
+    int act;   // 0: identity, 1: GELU (tanh approximation)
 };
 
 __device__ __forceinline__ f32x16 mfma32g(const bf16x8& a, const bf16x8& b, const f32x16& c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// GELU, tanh approximation: 0.5 h (1 + tanh(u)), u = sqrt(2/pi) (h + 0.044715 h^3),
+// evaluated as h - h / (e + 1) with e = exp(2u) (= h * sigmoid(2u)); the reciprocal is
+// v_rcp_f32 (1 ulp), not a correctly rounded division (a ten-instruction sequence).
+// e = inf gives h, e = 0 gives 0.
 __device__ __forceinline__ float gelu_tanh(float h) {
-    // 0.5 h (1 + tanh(u)), u = sqrt(2/pi) (h + 0.044715 h^3); tanh(u) = 1 - 2 / (e^{2u} + 1)
-    const float u = 0.7978845608028654f * (h + 0.044715f * h * h * h);
+    const float u = 0.7978845608028654f * fmaf(0.044715f * h, h * h, h);
     const float e = exp2_fast(2.f * kLog2e * u);
-    const float th = 1.f - 2.f / (e + 1.f);
-    return 0.5f * h * (1.f + th);
+    return h - h * __builtin_amdgcn_rcpf(e + 1.f);
 }
 
+// d/dh of the above: 0.5 (1 + t) + 0.5 h (1 - t^2) u'(h), t = tanh(u) = 1 - 2 / (e + 1)
 __device__ __forceinline__ float gelu_tanh_grad(float h) {
-    const float u = 0.7978845608028654f * (h + 0.044715f * h * h * h);
+    const float u = 0.7978845608028654f * fmaf(0.044715f * h, h * h, h);
     const float e = exp2_fast(2.f * kLog2e * u);
-    const float th = 1.f - 2.f / (e + 1.f);
+    const float th = 1.f - 2.f * __builtin_amdgcn_rcpf(e + 1.f);
     return 0.5f * (1.f + th) +
            0.5f * h * (1.f - th * th) * 0.7978845608028654f * (1.f + 3.f * 0.044715f * h * h);
 }
 
-// Grid: x over N tiles, y over M tiles (a row of tiles shares its A rows in L2).
-__global__ void __launch_bounds__(kGThreads) gemm_bias_act_kernel(GemmArgs a) {
+// tile t -> (row panel, column tile): with a multiple of 8 row panels, tiles with
+// t % 8 == c (run by the workgroups on XCD c) cover panels c, c+8, ... and walk all
+// column tiles of one panel in a row, so a panel's A rows are shared in that XCD's L2
+__device__ __forceinline__ void gemm_tile(int t, int nm, int nn, int& m0, int& n0, int& nt) {
+    int mt;
+    if ((nm & 7) == 0) {
+        const int c = t & 7, s = t >> 3;
+        mt = (s / nn) * 8 + c;
+        nt = s - (s / nn) * nn;
+    } else {
+        mt = t / nn;
+        nt = t - mt * nn;
+    }
+    m0 = mt * kGBM;
+    n0 = nt * kGBN;
+}
+
+// Persistent: each workgroup walks tiles blockIdx.x, blockIdx.x + gridDim.x, ...; the
+// stage pipeline runs on across tiles, so the next tile's first K stage loads during
+// the current tile's last MFMAs and epilogue.
+__global__ void __launch_bounds__(kGThreads, 1) gemm_bias_act_kernel(GemmArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t sa[2][kGBM * kGLD];
     __shared__ __attribute__((aligned(16))) uint16_t sb[2][kGBN * kGLD];
 
-    const int n0 = blockIdx.x * kGBN, m0 = blockIdx.y * kGBM;
+    const int nm = (a.M + kGBM - 1) / kGBM, nn = (a.N + kGBN - 1) / kGBN;
+    const int ntiles = nm * nn;
+    int t = blockIdx.x;
+    if (t >= ntiles) return;
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = (wave / (kGBN / kGWN)) * kGWM, wn = (wave % (kGBN / kGWN)) * kGWN;
     const int g = lane >> 5;
-    const bool write_xg = (a.Xg != nullptr) && blockIdx.x == 0;
-
-    // each thread moves 2 x 16 B of A and 2 x 16 B of B per stage:
-    // vector v = tid + 256*r (r = 0, 1) -> row v / 4, k-vector v % 4
-    const uint16_t* arow[2];
-    const uint16_t* brow[2];
-    int vrow[2], vk[2];
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-        const int v = tid + kGThreads * r;
-        vrow[r] = v >> 2;
-        vk[r] = (v & 3) * 8;
-        const int m = m0 + vrow[r];
-        const int n = n0 + vrow[r];
-        arow[r] = nullptr;
-        if (m < a.M) {
-            if (a.idx) {
-                // a window that leaves X reads as zeros instead of faulting
-                const int64_t s = a.idx[m];
-                if (s >= 0 && s * a.F + a.K <= a.R * a.F) arow[r] = a.A + s * a.F;
-            } else {
-                arow[r] = a.A + (int64_t)m * a.lda;
-            }
-        }
-        brow[r] = (n < a.N) ? a.B + (int64_t)n * a.ldb : nullptr;
-    }
     const int nk = (a.K + kGBK - 1) / kGBK;
-    uint4 ra[2], rb[2];
-    auto gload = [&](int kt) {
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const int k = kt * kGBK + vk[r];
-            ra[r] = make_uint4(0u, 0u, 0u, 0u);
-            rb[r] = make_uint4(0u, 0u, 0u, 0u);
-            if (arow[r] && k < a.K) ra[r] = ld16(arow[r] + k);
-            if (brow[r] && k < a.K) rb[r] = ld16(brow[r] + k);
-            if (write_xg && m0 + vrow[r] < a.M && k < a.K)
-                st16(a.Xg + (int64_t)(m0 + vrow[r]) * a.ldxg + k, ra[r]);
-        }
-    };
-    auto sstore = [&](int buf) {
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            *reinterpret_cast<uint4*>(&sa[buf][vrow[r] * kGLD + vk[r]]) = ra[r];
-            *reinterpret_cast<uint4*>(&sb[buf][vrow[r] * kGLD + vk[r]]) = rb[r];
-        }
-    };
 
-    f32x16 acc[2][2];
+    // this wave's slot loads: instruction i = wave + 16k covers 64 slots of the A tile
+    // (i < kGNI) or the W tile; per lane a row pointer (null: row past M / N, or a
+    // gathered window that leaves X, read as zeros) and the slot's column
+    const uint16_t* src[kGPW];
+    int kcol[kGPW], trow[kGPW];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
-
-    gload(0);
-    sstore(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < nk) gload(kt + 1);
-#pragma unroll
-        for (int c = 0; c < kGBK / 16; ++c) {
-            bf16x8 av[2], bv[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-                av[i] = *reinterpret_cast<const bf16x8*>(&sa[buf][(wm + 32 * i + (lane & 31)) * kGLD + 16 * c + 8 * g]);
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-                bv[j] = *reinterpret_cast<const bf16x8*>(&sb[buf][(wn + 32 * j + (lane & 31)) * kGLD + 16 * c + 8 * g]);
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] = mfma32g(av[i], bv[j], acc[i][j]);
-        }
-        if (kt + 1 < nk) sstore(buf ^ 1);
-        __syncthreads();
+    for (int k = 0; k < kGPW; ++k) {
+        const int i = wave + kGWaves * k;
+        const int sl = (i % kGNI) * 64 + lane;
+        const int r = sl / kGSPR;
+        int c = sl - r * kGSPR;
+        if (c == kGSPR - 1) c = kGSPR - 2;  // pad slot: any in-row chunk
+        kcol[k] = c * 8;
+        trow[k] = r;
     }
-
-    // epilogue: lane holds column n = n0 + wn + 32 j + lane%32, rows 8*(e/4) + 4 g + e%4
+    auto set_rows = [&](int m0, int n0) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int n = n0 + wn + 32 * j + (lane & 31);
-        if (n >= a.N) continue;
-        const float bn = a.bias ? bf16_to_f32(a.bias[n]) : 0.f;
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int m = m0 + wm + 32 * i + 8 * (e >> 2) + 4 * g + (e & 3);
+        for (int k = 0; k < kGPW; ++k) {
+            const int i = wave + kGWaves * k;
+            const uint16_t* row = nullptr;
+            if (i < kGNI) {
+                const int m = m0 + trow[k];
                 if (m < a.M) {
-                    const float h = acc[i][j][e] + bn;
-                    if (a.H) a.H[(int64_t)m * a.ldh + n] = f32_to_bf16(h);
-                    a.C[(int64_t)m * a.ldc + n] = f32_to_bf16(a.act == 1 ? gelu_tanh(h) : h);
+                    if (a.idx) {
+                        const int64_t st = a.idx[m];
+                        if (st >= 0 && st * a.F + a.K <= a.R * a.F) row = a.A + st * a.F;
+                    } else {
+                        row = a.A + (int64_t)m * a.lda;
+                    }
+                }
+            } else {
+                const int n = n0 + trow[k];
+                if (n < a.N) row = a.B + (int64_t)n * a.ldb;
+            }
+            src[k] = row ? row + kcol[k] : nullptr;
+        }
+    };
+    auto issue = [&](int kt, int st) {
+        const int k0 = kt * kGBK;
+        const bool full = k0 + kGBK <= a.K;
+#pragma unroll
+        for (int k = 0; k < kGPW; ++k) {
+            const int i = wave + kGWaves * k;
+            if (i >= 2 * kGNI) break;
+            const uint16_t* tile = (i < kGNI) ? sa[st] : sb[st];
+            const uint32_t dst = lds_addr(tile + (i % kGNI) * 64 * 8);
+            const bool ok = src[k] != nullptr && (full || k0 + kcol[k] < a.K);
+            dma16(ok ? (const void*)(src[k] + k0) : (const void*)g_zero_line, dst);
+        }
+    };
+
+    int m0, n0, nt;
+    gemm_tile(t, nm, nn, m0, n0, nt);
+    set_rows(m0, n0);
+    issue(0, 0);
+    int st = 0;  // stage of the next K step to consume
+    for (; t < ntiles; t += gridDim.x) {
+        f32x16 acc[kGTJ][kGTI];  // [j: 32 columns of W][i: 32 rows of A]
+#pragma unroll
+        for (int j = 0; j < kGTJ; ++j)
+#pragma unroll
+            for (int i = 0; i < kGTI; ++i) acc[j][i] = f32x16{};
+        const bool write_xg = a.Xg != nullptr && nt == 0;
+        const int cm0 = m0, cn0 = n0;
+        for (int kt = 0; kt < nk; ++kt, st ^= 1) {
+            tile_arrive();
+            if (kt + 1 < nk) {
+                issue(kt + 1, st ^ 1);
+            } else if (t + (int)gridDim.x < ntiles) {  // first stage of this workgroup's next tile
+                gemm_tile(t + gridDim.x, nm, nn, m0, n0, nt);
+                set_rows(m0, n0);
+                issue(0, st ^ 1);
+            }
+            const uint16_t* A = sa[st];
+            const uint16_t* Bt = sb[st];
+            if (write_xg) {
+                // the gathered rows of this K stage, from LDS to Xg (first column of tiles)
+#pragma unroll
+                for (int q = 0; q < kGBM * (kGBK / 8) / kGThreads; ++q) {
+                    const int v = tid + kGThreads * q;
+                    const int r = v / (kGBK / 8), c = v - r * (kGBK / 8);
+                    const int m = cm0 + r, k = kt * kGBK + c * 8;
+                    if (m < a.M && k < a.K)
+                        st16(a.Xg + (int64_t)m * a.ldxg + k, *reinterpret_cast<const uint4*>(A + r * kGLD + c * 8));
                 }
             }
+#pragma unroll
+            for (int c = 0; c < kGBK / 16; ++c) {
+                bf16x8 av[kGTI], bv[kGTJ];
+#pragma unroll
+                for (int i = 0; i < kGTI; ++i)
+                    av[i] = *reinterpret_cast<const bf16x8*>(A + (wm + 32 * i + (lane & 31)) * kGLD + 16 * c + 8 * g);
+#pragma unroll
+                for (int j = 0; j < kGTJ; ++j)
+                    bv[j] = *reinterpret_cast<const bf16x8*>(Bt + (wn + 32 * j + (lane & 31)) * kGLD + 16 * c + 8 * g);
+#pragma unroll
+                for (int j = 0; j < kGTJ; ++j)
+#pragma unroll
+                    for (int i = 0; i < kGTI; ++i) acc[j][i] = mfma32g(av[i], bv[j], acc[j][i]);
+            }
+        }
+
+        // epilogue (standard orientation): lane holds column n = cn0 + wn + 32 j + lane%32
+        // and rows cm0 + wm + 32 i + 8 (e/4) + 4 g + e%4; a half-wave stores 64 contiguous bytes
+#pragma unroll
+        for (int j = 0; j < kGTJ; ++j) {
+            const int n = cn0 + wn + 32 * j + (lane & 31);
+            if (n >= a.N) continue;
+            const float bn = a.bias ? bf16_to_f32(a.bias[n]) : 0.f;
+#pragma unroll
+            for (int i = 0; i < kGTI; ++i)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int m = cm0 + wm + 32 * i + 8 * (e >> 2) + 4 * g + (e & 3);
+                    if (m < a.M) {
+                        const float h = acc[j][i][e] + bn;
+                        if (a.H) a.H[(int64_t)m * a.ldh + n] = f32_to_bf16(h);
+                        a.C[(int64_t)m * a.ldc + n] = f32_to_bf16(a.act == 1 ? gelu_tanh(h) : h);
+                    }
+                }
+        }
     }
 }
 
@@ -228,9 +297,20 @@ extern "C" int fx_linear_fwd(const uint16_t* X, int64_t ldx, const int32_t* idx,
     a.N = (int)N;
     a.K = (int)K;
     a.act = act;
-    const dim3 grid((unsigned)((N + kGBN - 1) / kGBN), (unsigned)((M + kGBM - 1) / kGBM));
-    FX_REQUIRE(grid.y <= 65535u * 16u, "fx_linear_fwd: M too large");
-    hipLaunchKernelGGL(gemm_bias_act_kernel, grid, dim3(kGThreads), 0, (hipStream_t)stream, a);
+    const int64_t tiles = ((M + kGBM - 1) / kGBM) * ((N + kGBN - 1) / kGBN);
+    FX_REQUIRE(tiles < 0x7fffffffLL, "fx_linear_fwd: too many tiles");
+    // persistent grid: one workgroup per CU (the LDS of one is 147 KB)
+    static int s_cus = 0;
+    if (s_cus == 0) {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
+            s_cus = cus;
+        else
+            s_cus = 256;
+    }
+    const int64_t grid = tiles < (int64_t)s_cus ? tiles : (int64_t)s_cus;
+    hipLaunchKernelGGL(gemm_bias_act_kernel, dim3((unsigned)grid), dim3(kGThreads), 0, (hipStream_t)stream, a);
     return check_launch("gemm_bias_act");
 }
 
