@@ -164,7 +164,8 @@ int fx_adamw_step(const fxAdamWState* state, const fxTensorList* lists, int32_t 
  * the head dimension as a field and one Delta workspace.
  * q, k, v, dq, dk, dv: (B, T, H, D) with unit stride along D and the element strides
  * below along b, t, h (views of a fused (B, T, 3, H, D) buffer are fine);
- * o, dout: (B, T, H, D) contiguous; lse, delta: (B, H, T) fp32. */
+ * o, dout: (B, T, H, D) contiguous; lse, delta: (B, H, T) fp32.  Every bf16 tensor is
+ * 16-byte aligned and its strides are multiples of 8 elements. */
 typedef struct fxAttnArgs {
     const uint16_t* q;
     const uint16_t* k;

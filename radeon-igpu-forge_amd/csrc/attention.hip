@@ -109,12 +109,35 @@ __device__ __forceinline__ void grid_map(int ntiles, int nbh, int& bh, int& tile
     bh = x - tile * nbh;
 }
 
-// 4 consecutive fp32 accumulator values (elements 4r..4r+3) * mul -> 4 bf16 (8-byte store)
-__device__ __forceinline__ void store4(uint16_t* p, const f32x16& c, int r, float mul) {
-    uint2 u;
-    u.x = pack_bf16x2(c[4 * r + 0] * mul, c[4 * r + 1] * mul);
-    u.y = pack_bf16x2(c[4 * r + 2] * mul, c[4 * r + 3] * mul);
-    *reinterpret_cast<uint2*>(p) = u;
+// Store a wave's 32 x D output block held in the transposed accumulator layout
+// (lane l: output row l % 32; elements 4r..4r+3 of tile dt are columns
+// 32 dt + 8 r + 4 (l / 32) + 0..3), scaled by `mul` (per lane), to rows
+// first + i * rs (i < nvalid).  The block goes through the wave's private LDS
+// region `tmp` (32 x (D + 8) bf16) so that each lane then writes 16 contiguous bytes
+// and eight lanes cover a 128-byte row; storing 8 bytes per lane straight from the
+// accumulators spreads every instruction over 32 rows.  LDS operations of one wave
+// complete in order, so no barrier is needed between the writes and the reads.
+template <int D>
+__device__ __forceinline__ void store_rows(const f32x16 (&acc)[D / 32], float mul, uint16_t* tmp,
+                                           uint16_t* first, int64_t rs, int nvalid, int lane) {
+    constexpr int LDT = D + 8;
+    constexpr int CPR = D / 8;  // 16-byte chunks per row
+    const int g = lane >> 5, ln = lane & 31;
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            uint2 u;
+            u.x = pack_bf16x2(acc[dt][4 * r + 0] * mul, acc[dt][4 * r + 1] * mul);
+            u.y = pack_bf16x2(acc[dt][4 * r + 2] * mul, acc[dt][4 * r + 3] * mul);
+            *reinterpret_cast<uint2*>(tmp + ln * LDT + 32 * dt + 8 * r + 4 * g) = u;
+        }
+#pragma unroll
+    for (int c = 0; c < 32 * CPR / 64; ++c) {
+        const int ch = c * 64 + lane;
+        const int row = ch / CPR, col = (ch - row * CPR) * 8;
+        if (row < nvalid) st16(first + row * rs + col, *reinterpret_cast<const uint4*>(tmp + row * LDT + col));
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -304,16 +327,11 @@ __global__ void __launch_bounds__(kAttThreads) attn_fwd_kernel(fxAttnArgs a) {
     }
 
     const float l_tot = pair_sum(l_run);
-    if (qi < T) {
-        const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-        uint16_t* orow = a.o_out + (((int64_t)b * T + qi) * a.H + h) * D;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) store4(orow + 32 * dt + 8 * r + 4 * g, acc[dt], r, inv);
-        if (g == 0)
-            a.lse_out[(int64_t)bh * T + qi] = l_tot > 0.f ? (m_run + log2_fast(l_tot)) * kLn2 : kNegInfA;
-    }
+    if (qi < T && g == 0)
+        a.lse_out[(int64_t)bh * T + qi] = l_tot > 0.f ? (m_run + log2_fast(l_tot)) * kLn2 : kNegInfA;
+    __syncthreads();  // every wave is done with the K/V stages: they become store scratch
+    store_rows<D>(acc, l_tot > 0.f ? 1.f / l_tot : 0.f, (wave < 2 ? sk0 : sk1) + (wave & 1) * 32 * LD,
+                  a.o_out + (((int64_t)b * T + q0w) * a.H + h) * D, (int64_t)a.H * D, T - q0w, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -427,13 +445,9 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dq_kern
         if (j + 1 < nblk) step(j + 1, sk1, sv1, sk0, sv0);
     }
 
-    if (qok) {
-        uint16_t* dqrow = a.dq + b * a.dqb + h * a.dqh + (int64_t)qi * a.dqt;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) store4(dqrow + 32 * dt + 8 * r + 4 * g, acc[dt], r, a.scale);
-    }
+    __syncthreads();  // every wave is done with the K/V stages: they become store scratch
+    store_rows<D>(acc, a.scale, (wave < 2 ? sk0 : sk1) + (wave & 1) * 32 * LD,
+                  a.dq + b * a.dqb + h * a.dqh + (int64_t)q0w * a.dqt, a.dqt, T - q0w, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -579,17 +593,10 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dkv_ker
         if (j + 1 < nblk) step(j + 1, sq1, sdo1, sq0, sdo0);
     }
 
-    if (kok) {
-        uint16_t* dkrow = a.dk + b * a.dkb + h * a.dkh + (int64_t)ki * a.dkt;
-        uint16_t* dvrow = a.dv + b * a.dvb + h * a.dvh + (int64_t)ki * a.dvt;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                store4(dkrow + 32 * dt + 8 * r + 4 * g, adk[dt], r, a.scale);
-                store4(dvrow + 32 * dt + 8 * r + 4 * g, adv[dt], r, 1.f);
-            }
-    }
+    __syncthreads();  // every wave is done with the Q/dO stages: they become store scratch
+    uint16_t* tmp = (wave < 2 ? sq0 : sq1) + (wave & 1) * 32 * LD;
+    store_rows<D>(adk, a.scale, tmp, a.dk + b * a.dkb + h * a.dkh + (int64_t)k0w * a.dkt, a.dkt, T - k0w, lane);
+    store_rows<D>(adv, 1.f, tmp, a.dv + b * a.dvb + h * a.dvh + (int64_t)k0w * a.dvt, a.dvt, T - k0w, lane);
 }
 
 }  // namespace fx
@@ -620,10 +627,10 @@ static int attn_check(const fxAttnArgs* p, bool bwd) {
     } else {
         FX_REQUIRE(a.o && a.dout && a.lse && a.delta && a.dq && a.dk && a.dv, "fx_attn_bwd: null pointer");
         FX_REQUIRE((((uintptr_t)a.o | (uintptr_t)a.dout) & 15) == 0, "fx_attn_bwd: o/dout must be 16-byte aligned");
-        FX_REQUIRE((((uintptr_t)a.dq | (uintptr_t)a.dk | (uintptr_t)a.dv) & 7) == 0,
-                   "fx_attn_bwd: dq/dk/dv must be 8-byte aligned");
+        FX_REQUIRE((((uintptr_t)a.dq | (uintptr_t)a.dk | (uintptr_t)a.dv) & 15) == 0,
+                   "fx_attn_bwd: dq/dk/dv must be 16-byte aligned");
         const int64_t t[] = {a.dqb, a.dqt, a.dqh, a.dkb, a.dkt, a.dkh, a.dvb, a.dvt, a.dvh};
-        for (int64_t x : t) FX_REQUIRE(x % 4 == 0, "fx_attn_bwd: dq/dk/dv strides must be multiples of 4");
+        for (int64_t x : t) FX_REQUIRE(x % 8 == 0, "fx_attn_bwd: dq/dk/dv strides must be multiples of 8");
     }
     return 0;
 }
