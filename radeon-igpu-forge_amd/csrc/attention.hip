@@ -161,19 +161,22 @@ struct TileDma2 {
     static_assert(R * SPR % 64 == 0, "tile must be a whole number of wave loads");
     static constexpr int PW = (2 * NI + kAttWaves - 1) / kAttWaves;  // per wave, at most
     uint32_t off[PW];  // byte offset of this lane's chunk from the tile's first row
-    int row[PW];       // tile row of this lane's chunk
     int wave;
+    // tile row and in-row chunk of this lane's slot in wave instruction i
+    __device__ __forceinline__ static void slot(int i, int lane, int& r, int& c) {
+        const int s = (i % NI) * 64 + lane;
+        r = s / SPR;
+        c = s - r * SPR;
+        if (c == SPR - 1) c = SPR - 2;  // pad slot: any in-row chunk
+    }
     __device__ __forceinline__ void init(int64_t rs0, int64_t rs1) {
         wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
         const int lane = threadIdx.x & 63;
 #pragma unroll
         for (int k = 0; k < PW; ++k) {
             const int i = wave + k * kAttWaves;
-            const int s = (i % NI) * 64 + lane;
-            const int r = s / SPR;
-            int c = s - r * SPR;
-            if (c == SPR - 1) c = SPR - 2;  // pad slot: any in-row chunk
-            row[k] = r;
+            int r, c;
+            slot(i, lane, r, c);
             off[k] = (uint32_t)(r * (i < NI ? rs0 : rs1) + c * 8) * 2u;
         }
     }
@@ -191,8 +194,10 @@ struct TileDma2 {
                 if (full) {
                     dma16_so(base, off[k], dst);
                 } else {
-                    const void* p = row[k] < valid ? (const void*)((const char*)base + off[k])
-                                                   : (const void*)g_zero_line;
+                    int r, c;
+                    slot(i, threadIdx.x & 63, r, c);
+                    const void* p = r < valid ? (const void*)((const char*)base + off[k])
+                                              : (const void*)g_zero_line;
                     dma16(p, dst);
                 }
             }
@@ -408,23 +413,15 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dq_kern
         for (int hh = 0; hh < 2; ++hh) {
             const int kh = kb + 32 * hh;
             if (kh >= T || (a.causal && kh > q0w + 31)) continue;
-            bf16x8 kop[DC], vop[DC];
-#pragma unroll
-            for (int c = 0; c < DC; ++c) {
-                kop[c] = lds_op_row(K, LD, 32 * hh, 16 * c, lane);
-                vop[c] = lds_op_row(V, LD, 32 * hh, 16 * c, lane);
-            }
+            // S^T = K Q^T and dP^T = V dO^T, operands read chunk by chunk (few live registers)
             f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
             for (int c = 0; c < DC; ++c) {
-                s = mfma32(kop[c], qop[c], s);
-                dp = mfma32(vop[c], dop[c], dp);
+                const bf16x8 kop = lds_op_row(K, LD, 32 * hh, 16 * c, lane);
+                const bf16x8 vop = lds_op_row(V, LD, 32 * hh, 16 * c, lane);
+                s = mfma32(kop, qop[c], s);
+                dp = mfma32(vop, dop[c], dp);
             }
-            bf16x8 ktop[DT][2];
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-                for (int kc = 0; kc < 2; ++kc) ktop[dt][kc] = lds_op_t(K, LD, 32 * hh + 16 * kc, 32 * dt, lane);
             if ((kh + 32 > T) || (a.causal && kh + 31 > q0w))  // masked scores give P = 0
                 mask_rows(s, 0, (a.causal ? min(qi, T - 1) : T - 1) - kh - 4 * g);
 #pragma unroll
@@ -435,8 +432,10 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dq_kern
             const bf16x8 d0 = pack_op(s, 0), d1 = pack_op(s, 1);
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
-                acc[dt] = mfma32(ktop[dt][0], d0, acc[dt]);
-                acc[dt] = mfma32(ktop[dt][1], d1, acc[dt]);
+                const bf16x8 k0t = lds_op_t(K, LD, 32 * hh, 32 * dt, lane);
+                const bf16x8 k1t = lds_op_t(K, LD, 32 * hh + 16, 32 * dt, lane);
+                acc[dt] = mfma32(k0t, d0, acc[dt]);
+                acc[dt] = mfma32(k1t, d1, acc[dt]);
             }
         }
     };
@@ -536,39 +535,26 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dkv_ker
         for (int hh = 0; hh < 2; ++hh) {
             const int qh = qb + 32 * hh;  // first query of this half
             if (qh >= T || (a.causal && qh + 31 < k0w)) continue;  // all of this wave's keys follow these queries
-            bf16x8 qa[DC], da[DC];
-#pragma unroll
-            for (int c = 0; c < DC; ++c) {
-                qa[c] = lds_op_row(Q, LD, 32 * hh, 16 * c, lane);
-                da[c] = lds_op_row(DO, LD, 32 * hh, 16 * c, lane);
-            }
-            float4 l4[4], d4[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int qr = 32 * hh + 8 * r + 4 * g;  // 4 consecutive queries of this lane
-                l4[r] = *reinterpret_cast<const float4*>(&slse[st][qr]);
-                d4[r] = *reinterpret_cast<const float4*>(&sdelta[st][qr]);
-            }
+            // S = Q K^T and dP = dO V^T, operands read chunk by chunk (few live registers)
             f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
             for (int c = 0; c < DC; ++c) {
-                s = mfma32(qa[c], kop[c], s);
-                dp = mfma32(da[c], vop[c], dp);
+                const bf16x8 qa = lds_op_row(Q, LD, 32 * hh, 16 * c, lane);
+                const bf16x8 da = lds_op_row(DO, LD, 32 * hh, 16 * c, lane);
+                s = mfma32(qa, kop[c], s);
+                dp = mfma32(da, vop[c], dp);
             }
-            bf16x8 dot[DT][2], qtr[DT][2];
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-                for (int kc = 0; kc < 2; ++kc) {
-                    dot[dt][kc] = lds_op_t(DO, LD, 32 * hh + 16 * kc, 32 * dt, lane);
-                    qtr[dt][kc] = lds_op_t(Q, LD, 32 * hh + 16 * kc, 32 * dt, lane);
-                }
             if ((qh + 32 > T) || (a.causal && qh < k0w + 31))  // queries past T or before the key
                 mask_rows(s, a.causal ? ki - qh - 4 * g : INT32_MIN, T - 1 - qh - 4 * g);
+            // P and dS / scale in fp32, four rows (queries) at a time with their lse and
+            // Delta, then packed: only the bf16 operands stay live for the products
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float lv[4] = {l4[r].x, l4[r].y, l4[r].z, l4[r].w};
-                const float dv[4] = {d4[r].x, d4[r].y, d4[r].z, d4[r].w};
+                const int qr = 32 * hh + 8 * r + 4 * g;  // 4 consecutive queries of this lane
+                const float4 l4 = *reinterpret_cast<const float4*>(&slse[st][qr]);
+                const float4 d4 = *reinterpret_cast<const float4*>(&sdelta[st][qr]);
+                const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+                const float dv[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int i = 4 * r + e;
@@ -581,10 +567,14 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dkv_ker
             const bf16x8 d0 = pack_op(dp, 0), d1 = pack_op(dp, 1);
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
-                adv[dt] = mfma32(dot[dt][0], p0, adv[dt]);
-                adk[dt] = mfma32(qtr[dt][0], d0, adk[dt]);
-                adv[dt] = mfma32(dot[dt][1], p1, adv[dt]);
-                adk[dt] = mfma32(qtr[dt][1], d1, adk[dt]);
+                const bf16x8 o0 = lds_op_t(DO, LD, 32 * hh, 32 * dt, lane);
+                const bf16x8 o1 = lds_op_t(DO, LD, 32 * hh + 16, 32 * dt, lane);
+                const bf16x8 q0t = lds_op_t(Q, LD, 32 * hh, 32 * dt, lane);
+                const bf16x8 q1t = lds_op_t(Q, LD, 32 * hh + 16, 32 * dt, lane);
+                adv[dt] = mfma32(o0, p0, adv[dt]);
+                adk[dt] = mfma32(q0t, d0, adk[dt]);
+                adv[dt] = mfma32(o1, p1, adv[dt]);
+                adk[dt] = mfma32(q1t, d1, adk[dt]);
             }
         }
     };

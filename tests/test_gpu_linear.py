@@ -83,7 +83,7 @@ def test_gather_window_outside_reads_zero(dev):
 
 
 @pytest.mark.parametrize("M,K,N,bias", [(300, 768, 3072, False), (77, 40, 100, True), (1, 8, 1, True),
-                                        (513, 256, 129, False)])
+                                        (513, 256, 129, False), (300, 200, 300, True)])
 def test_linear_gelu_against_oracle(dev, M, K, N, bias):
     from fxgpu.fused_linear import fused_linear
     torch.manual_seed(M + K + N)
@@ -113,3 +113,25 @@ def test_cfg5_mlp_shape(dev):
     y = fused_linear(x, W, None, "gelu_tanh")
     ref = F.gelu(x.float() @ W.float().t(), approximate="tanh")
     assert float((y.float() - ref).abs().max()) <= ATOL_BF16
+
+
+def test_gather_more_tiles_than_workgroups(dev):
+    # 17 x 16 = 272 output tiles of 256 x 256: more than one tile per persistent
+    # workgroup, so the next tile's loads run during an epilogue and the gathered rows
+    # (Xg) are written by workgroups that hold several tiles; windows of 4 rows x 64
+    from fxgpu.fused_linear import FusedGatherLinear
+    g = torch.Generator(device=dev).manual_seed(11)
+    R, F_, Wn, M, N = 5000, 64, 4, 4352, 4096
+    X = torch.randn(R, F_, device=dev, generator=g).bfloat16()
+    idx = torch.randint(0, R - Wn + 1, (M,), device=dev, dtype=torch.int32, generator=g)
+    W = (torch.randn(N, Wn * F_, device=dev, generator=g) * 0.05).bfloat16().requires_grad_()
+    b = torch.randn(N, device=dev, generator=g).bfloat16().requires_grad_()
+    out = FusedGatherLinear.apply(X, idx, W, b)
+    xg = X.unfold(0, Wn, 1)[idx.long()].transpose(1, 2).reshape(M, Wn * F_)
+    ref = xg.float() @ W.detach().float().t() + b.detach().float()
+    assert float((out.float() - ref).abs().max()) <= ATOL_BF16 * max(1.0, float(ref.abs().max()) / 4)
+    # dW = g^T Xg uses the gathered rows the forward wrote out
+    gy = (torch.randn(M, N, device=dev, generator=g) * 0.01).bfloat16()
+    out.backward(gy)
+    rdw = gy.float().t() @ xg.float()
+    assert float((W.grad.float() - rdw).abs().max()) <= _rel_tol(rdw)
