@@ -219,8 +219,10 @@ ce_loss_finalize_kernel(const float* __restrict__ row_loss, int64_t N,
 
 __global__ void __launch_bounds__(256)
 ce_scale_grad_kernel(uint16_t* __restrict__ grad, int64_t numel, const float* __restrict__ g,
-                     const float* __restrict__ applied) {
-    const float f = (*g) / (*applied);
+                     float* __restrict__ applied, int src) {
+    const float gv = *g;
+    const float f = gv / applied[src];
+    if (blockIdx.x == 0 && threadIdx.x == 0) applied[1 - src] = gv;  // no block reads this slot
     if (f == 1.f) return;
     const int64_t stride = (int64_t)gridDim.x * 256;
     const int64_t n8 = numel >> 3;
@@ -233,10 +235,6 @@ ce_scale_grad_kernel(uint16_t* __restrict__ grad, int64_t numel, const float* __
     }
     for (int64_t i = n8 * 8 + (int64_t)blockIdx.x * 256 + threadIdx.x; i < numel; i += stride)
         grad[i] = f32_to_bf16(bf16_to_f32(grad[i]) * f);
-}
-
-__global__ void ce_set_applied_kernel(const float* __restrict__ g, float* __restrict__ applied) {
-    if (threadIdx.x == 0) *applied = *g;
 }
 
 }  // namespace fx
@@ -313,19 +311,17 @@ extern "C" int fx_ce_loss_finalize(const float* row_loss, int64_t N, const float
 }
 
 extern "C" int fx_ce_scale_grad(uint16_t* grad, int64_t numel, const float* g, float* applied,
-                                void* stream) {
+                                int32_t src, void* stream) {
     FX_REQUIRE(g != nullptr && applied != nullptr, "fx_ce_scale_grad: null scalar");
+    FX_REQUIRE(src == 0 || src == 1, "fx_ce_scale_grad: src=%d must be 0 or 1", src);
     FX_REQUIRE(numel >= 0 && (numel == 0 || grad != nullptr), "fx_ce_scale_grad: bad grad");
     FX_REQUIRE(((uintptr_t)grad & 15) == 0, "fx_ce_scale_grad: grad not 16-byte aligned");
-    hipStream_t s = (hipStream_t)stream;
-    if (numel > 0) {
-        int64_t blocks = (numel / 8 + 255) / 256;
-        if (blocks > 2048) blocks = 2048;  // grid-stride; small, since usually every block exits at once
-        if (blocks < 1) blocks = 1;
-        hipLaunchKernelGGL(ce_scale_grad_kernel, dim3((unsigned)blocks), dim3(256), 0, s, grad, numel, g,
-                           (const float*)applied);
-        if (int e = check_launch("ce_scale_grad")) return e;
-    }
-    hipLaunchKernelGGL(ce_set_applied_kernel, dim3(1), dim3(64), 0, s, g, applied);
-    return check_launch("ce_set_applied");
+    // one launch whatever the ratio (the kernel writes applied[1 - src]); a grid-stride
+    // grid of 4 blocks per CU streams the scaling and exits cheaply when it is a no-op
+    int64_t blocks = (numel / 8 + 255) / 256;
+    if (blocks > 1024) blocks = 1024;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(ce_scale_grad_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, grad,
+                       numel, g, applied, (int)src);
+    return check_launch("ce_scale_grad");
 }

@@ -90,15 +90,18 @@ class _FusedCE(torch.autograd.Function):
             grad = torch.empty(N, V, device=dev, dtype=torch.bfloat16)
         _ce_rows(logits, target, grad, row_loss, mul, ignore_index)
         ctx.save_for_backward(grad)
-        ctx.applied = torch.ones((), device=dev, dtype=torch.float32)
+        # multiplier already in grad: slot ctx.src of two (the kernel writes the other)
+        ctx.applied = torch.ones(2, device=dev, dtype=torch.float32)
+        ctx.src = 0
         return _finalize(row_loss, inv_n)
 
     @staticmethod
     def backward(ctx, g):
         (grad,) = ctx.saved_tensors
         g32 = g.detach().to(torch.float32).reshape(()).contiguous()
-        call("fx_ce_scale_grad", ptr(grad), grad.numel(), ptr(g32), ptr(ctx.applied),
+        call("fx_ce_scale_grad", ptr(grad), grad.numel(), ptr(g32), ptr(ctx.applied), ctx.src,
              stream_of(grad))
+        ctx.src ^= 1
         return grad, None, None
 
 

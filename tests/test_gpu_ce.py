@@ -65,6 +65,28 @@ def test_backward_scales_by_incoming_grad(dev):
     assert torch.equal(b.grad, (a.grad.float() * 4.0).bfloat16())
 
 
+def test_backward_twice_with_retained_graph(dev):
+    # the gradient buffer is rescaled in place; the multiplier it carries is tracked in
+    # two device slots, so repeated backward calls each see grad * (their g)
+    from fxlm.cross_entropy import fused_cross_entropy
+    torch.manual_seed(4)
+    lg = torch.randn(17, 256, device=dev).bfloat16()
+    tg = torch.randint(0, 256, (17,), device=dev)
+    ref = lg.clone().requires_grad_()
+    fused_cross_entropy(ref, tg).backward()
+    c = lg.clone().requires_grad_()
+    loss = fused_cross_entropy(c, tg)
+    (loss * 2.0).backward(retain_graph=True)
+    first = c.grad.clone()
+    assert torch.equal(first, (ref.grad.float() * 2.0).bfloat16())
+    c.grad = None
+    (loss * 2.0).backward(retain_graph=True)  # same g again: no second scaling
+    assert torch.equal(c.grad, first)
+    c.grad = None
+    (loss * 0.5).backward()                   # a different g: rescaled from 2 to 0.5
+    assert torch.allclose(c.grad.float(), ref.grad.float() * 0.5, rtol=2 ** -7, atol=1e-6)
+
+
 def test_cfg3_full_size(dev):
     # cfg3: logits (16384, 50304) ~ N(0, 2), 5% ignored targets; fp32 torch math on the GPU
     from fxlm.cross_entropy import fused_cross_entropy
