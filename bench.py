@@ -94,12 +94,15 @@ def bench_ce(torch):
         lg.grad = None
     t = time_us(torch, fb, iters=10, warm=3)
     n_valid = int((tg != -100).sum())
-    # logits of rows with a valid target read once, dlogits of every row written once
-    # (ignored rows get a zero gradient row without being read), targets
-    nbytes = (n_valid + N) * V * 2 + N * 8
+    # algorithmic work of the config: logits read once, dlogits written once, targets
+    nbytes = 2 * N * V * 2 + N * 8
+    # what the kernel moves: rows with an ignored target get a zero gradient row
+    # without their logits being read
+    moved = (n_valid + N) * V * 2 + N * 8
     del lg
     return {"shape": [N, V], "fwdbwd_us": round(t, 2), "gbs": round(nbytes / t / 1e3, 1),
-            "frac_of_hbm": round(nbytes / t / 1e3 / HBM_PEAK_GBS, 4), "bytes": nbytes}
+            "frac_of_hbm": round(nbytes / t / 1e3 / HBM_PEAK_GBS, 4), "bytes": nbytes,
+            "moved_bytes": moved, "moved_gbs": round(moved / t / 1e3, 1)}
 
 
 def bench_norm(torch):
