@@ -225,10 +225,25 @@ def cpu_baseline(torch):
                     break
     except OSError:
         pass
+    # cfg1, the reference's CPU-runnable case: 4L-d256 H4 V256, T256, batch 32, lr 3e-4
+    torch.manual_seed(0)
+    m1 = ogpt.GPT(256, 256, 4, 4, 256)
+    opt1 = ogpt.make_optimizer(m1, lr=3e-4)
+    d1 = torch.randint(0, 256, (32, 257), generator=gen)
+    x1, y1 = d1[:, :-1], d1[:, 1:]
+    ogpt.cpu_train_step(m1, opt1, x1, y1)      # warm-up
+    n1, t1 = 0, time.perf_counter()
+    while n1 < 3 or (time.perf_counter() - t1 < 5.0 and n1 < 10):
+        ogpt.cpu_train_step(m1, opt1, x1, y1)
+        n1 += 1
+    dt1 = (time.perf_counter() - t1) / n1
     return {"value": round(Bc * T / dt, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
             "sample": (f"oracle/gpt.py naive-PyTorch fp32 GPT 12L-d768 V50304 (SDPA, F.rms_norm, "
                        f"F.cross_entropy, AdamW + clip 1.0) at batch {Bc} x {T} tokens, "
-                       f"1 warm-up + {n} timed steps ({dt:.2f} s/step) on {cores} threads, {cpu_model}")}
+                       f"1 warm-up + {n} timed steps ({dt:.2f} s/step) on {cores} threads, {cpu_model}"),
+            "cfg1_tok_s": round(32 * 256 / dt1, 1),
+            "cfg1_sample": (f"cfg1 4L-d256 H4 V256 T256 B32 fp32 step, 1 warm-up + {n1} timed steps "
+                            f"({dt1:.3f} s/step) on {cores} threads")}
 
 
 def bench_copy(torch):
