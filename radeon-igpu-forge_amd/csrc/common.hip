@@ -23,6 +23,19 @@ int check_launch(const char* what) {
     return 0;
 }
 
+int device_cus() {
+    static int s_cus = 0;
+    if (s_cus == 0) {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
+            s_cus = cus;
+        else
+            s_cus = 256;
+    }
+    return s_cus;
+}
+
 __global__ void __launch_bounds__(256) fill_f32_kernel(float* __restrict__ p, int64_t n, float value) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = value;

@@ -15,6 +15,8 @@ namespace fx {
 
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);   // hipGetLastError -> return code
+// compute units of the current device (queried once per process; 256 if the query fails)
+int device_cus();
 
 }  // namespace fx
 

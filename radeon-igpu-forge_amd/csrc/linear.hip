@@ -300,16 +300,8 @@ extern "C" int fx_linear_fwd(const uint16_t* X, int64_t ldx, const int32_t* idx,
     const int64_t tiles = ((M + kGBM - 1) / kGBM) * ((N + kGBN - 1) / kGBN);
     FX_REQUIRE(tiles < 0x7fffffffLL, "fx_linear_fwd: too many tiles");
     // persistent grid: one workgroup per CU (the LDS of one is 147 KB)
-    static int s_cus = 0;
-    if (s_cus == 0) {
-        int dev = 0, cus = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
-            s_cus = cus;
-        else
-            s_cus = 256;
-    }
-    const int64_t grid = tiles < (int64_t)s_cus ? tiles : (int64_t)s_cus;
+    const int64_t cus = device_cus();
+    const int64_t grid = tiles < cus ? tiles : cus;
     hipLaunchKernelGGL(gemm_bias_act_kernel, dim3((unsigned)grid), dim3(kGThreads), 0, (hipStream_t)stream, a);
     return check_launch("gemm_bias_act");
 }
