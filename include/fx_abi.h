@@ -221,6 +221,20 @@ int fx_linear_fwd(const uint16_t* X, int64_t ldx, const int32_t* idx, int64_t F,
  * of F.gelu(approximate="tanh"), ml/fxlm/model.py:71). */
 int fx_gelu_bwd(const uint16_t* dy, const uint16_t* h, uint16_t* dh, int64_t n, void* stream);
 
+/* Bytes of fp32 workspace fx_linear_wgrad needs for an (M, N) weight gradient over K
+ * tokens (0: none; the K split depends on the device's CU count). */
+int64_t fx_linear_wgrad_workspace(int64_t M, int64_t N, int64_t K);
+
+/* Weight gradient dW (M, N) = dY^T X, dY (K, M) with row stride ldy, X (K, N) with row
+ * stride ldx, dW row stride ldw; bf16 in and out, fp32 accumulation, the K (token)
+ * dimension split over workgroups and the fp32 partials (in `work`) summed in a fixed
+ * order.  M, N, ldy, ldx, ldw multiples of 8; 16-byte aligned buffers.
+ * Replaces the rocBLAS dW = g^T Xg of FusedGatherLinear.backward
+ * (ml/fxgpu/fused_linear.py:90-101) and the dense layers' weight gradients of the GPT
+ * (ml/fxlm/model.py:22-130, torch autograd of nn.Linear). */
+int fx_linear_wgrad(const uint16_t* dY, int64_t ldy, const uint16_t* X, int64_t ldx, uint16_t* dW,
+                    int64_t ldw, float* work, int64_t M, int64_t N, int64_t K, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

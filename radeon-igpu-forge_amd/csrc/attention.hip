@@ -1,13 +1,6 @@
 // Flash attention (forward and backward) for gfx950 with bf16 MFMA.
 //
-// Matrix-core layouts (v_mfma_f32_32x32x16_bf16, wave64):
-//   A (32 x 16): lane l supplies row l%32, k = 8*(l/32) + 0..7
-//   B (16 x 32): lane l supplies column l%32, k = 8*(l/32) + 0..7
-//   C (32 x 32): lane l holds column l%32, rows 8*(i/4) + 4*(l/32) + i%4, i = 0..15
-// A product whose K dimension is strided in LDS (V in P.V, K in dS.K, Q / dO in the
-// key-side products) is fed with ds_read_b64_tr_b16: within a group of 16 lanes,
-// lane s points at row k0 + s/4, column m0 + 4*(s%4) of a row-major tile and lane i
-// receives column m0 + i of rows k0..k0+3.  Two such reads give the 8 K-values.
+// Operand layouts and the transposed LDS reads are described in fx_mfma.h.
 // Accumulator tiles are reused as the next product's operand without any shuffle:
 // the 16 values a lane holds for one column are packed as the operand's 8 K-values
 // of two 16-wide K chunks, and the other operand's K order is permuted to match
@@ -27,7 +20,7 @@
 // loads that are in flight during the previous tile's math (one barrier per tile).
 #include <math.h>
 
-#include "fx_device.h"
+#include "fx_mfma.h"
 
 namespace fx {
 
@@ -43,21 +36,6 @@ constexpr float kNegInfA = -__builtin_huge_valf();
 // it by more than this (log2 units), so P stays <= 2^8 and most tiles skip the O rescale.
 constexpr float kLazyRescale = 8.f;
 
-typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
-
-__device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ bf16x4 lds_tr16(const uint16_t* p) {
-    return __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-        (lds_bf16x4*)(__attribute__((address_space(3))) void*)(p));
-}
-
-__device__ __forceinline__ bf16x8 cat8(const bf16x4& lo, const bf16x4& hi) {
-    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-}
-
 __device__ __forceinline__ bf16x8 as_bf16x8(const uint4& v) { return __builtin_bit_cast(bf16x8, v); }
 
 // 8 fp32 accumulator values (elements 8h..8h+7) -> bf16x8 operand
@@ -65,23 +43,6 @@ __device__ __forceinline__ bf16x8 pack_op(const f32x16& c, int h) {
     const f32x8 v = h == 0 ? __builtin_shufflevector(c, c, 0, 1, 2, 3, 4, 5, 6, 7)
                            : __builtin_shufflevector(c, c, 8, 9, 10, 11, 12, 13, 14, 15);
     return __builtin_convertvector(v, bf16x8);
-}
-
-// A operand whose K dimension runs down the rows of a row-major LDS tile with row
-// stride `ld` (elements): rows k0.. (8 K-values at the permuted positions), columns
-// m0 + 0..31 (lane l -> column m0 + l%32).  k0 is the 16-row chunk base.
-__device__ __forceinline__ bf16x8 lds_op_t(const uint16_t* tile, int ld, int k0, int m0, int lane) {
-    const int grp = lane >> 4, s = lane & 15;
-    const int row = k0 + 4 * (grp >> 1) + (s >> 2);
-    const int col = m0 + 16 * (grp & 1) + 4 * (s & 3);
-    const uint16_t* p = tile + row * ld + col;
-    return cat8(lds_tr16(p), lds_tr16(p + 8 * ld));
-}
-
-// Operand whose K dimension runs along a row: lane l reads 8 contiguous elements of
-// row r0 + l%32 starting at column c0 + 8*(l/32).
-__device__ __forceinline__ bf16x8 lds_op_row(const uint16_t* tile, int ld, int r0, int c0, int lane) {
-    return *reinterpret_cast<const bf16x8*>(tile + (r0 + (lane & 31)) * ld + c0 + 8 * (lane >> 5));
 }
 
 // row index (within a 32-row accumulator tile) of accumulator element i of lane l is

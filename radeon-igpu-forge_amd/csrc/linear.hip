@@ -21,7 +21,7 @@
 // Tiles sharing an A row panel are dealt to one XCD (shared L2).
 #include <math.h>
 
-#include "fx_device.h"
+#include "fx_mfma.h"
 
 namespace fx {
 
@@ -55,10 +55,6 @@ struct GemmArgs {
     int M, N, K;
     int act;   // 0: identity, 1: GELU (tanh approximation)
 };
-
-__device__ __forceinline__ f32x16 mfma32g(const bf16x8& a, const bf16x8& b, const f32x16& c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
 
 // GELU, tanh approximation: 0.5 h (1 + tanh(u)), u = sqrt(2/pi) (h + 0.044715 h^3),
 // evaluated as h - h / (e + 1) with e = exp(2u) (= h * sigmoid(2u)); the reciprocal is
@@ -212,7 +208,7 @@ __global__ void __launch_bounds__(kGThreads, 1) gemm_bias_act_kernel(GemmArgs a)
 #pragma unroll
                 for (int j = 0; j < kGTJ; ++j)
 #pragma unroll
-                    for (int i = 0; i < kGTI; ++i) acc[j][i] = mfma32g(av[i], bv[j], acc[j][i]);
+                    for (int i = 0; i < kGTI; ++i) acc[j][i] = mfma32(av[i], bv[j], acc[j][i]);
             }
         }
 
@@ -235,6 +231,162 @@ __global__ void __launch_bounds__(kGThreads, 1) gemm_bias_act_kernel(GemmArgs a)
                     }
                 }
         }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Weight gradient of a linear layer: C (M x N) = A^T B, A (K x M) = dY and B (K x N) =
+// X, both row-major with the contraction (tokens) down the rows, so dW = dY^T X.
+// The long K (16384 tokens at cfg5) and the small output (768 x 3072 is 36 tiles of
+// 256 x 256) leave most CUs idle without splitting K: the grid is tiles x slices
+// workgroups, slice s covering an even share of the K steps, and each slice writes an
+// fp32 partial tile that one reduce kernel sums in slice order (deterministic).  With
+// a single slice the tile is written as bf16 directly.
+// Both operands are staged K-major (64 token rows x 256 columns per stage, row stride
+// 288 elements = 144 dwords = 16 banks mod 64, so the four rows of a transposed read
+// fall in disjoint banks) and fed to the MFMAs with ds_read_b64_tr_b16; the wave
+// layout, MFMA tiles and the two-stage direct global -> LDS pipeline are those of the
+// forward GEMM above.
+constexpr int kWBK = 64;                          // K (token) rows per stage
+constexpr int kWLD = kGBM + 32;                   // LDS row stride (elements)
+constexpr int kWSPR = kWLD / 8;                   // 16-byte slots per LDS row; the last 4 are padding
+constexpr int kWNI = kWBK * kWSPR / 64;           // wave loads per operand tile
+constexpr int kWPW = (2 * kWNI + kGWaves - 1) / kGWaves;  // wave loads per wave per stage
+static_assert(kWBK * kWSPR % 64 == 0 && kGBM == kGBN, "wgrad tile shape");
+
+struct WgradArgs {
+    const uint16_t* A;  // dY (K x M)
+    int64_t lda;
+    const uint16_t* B;  // X (K x N)
+    int64_t ldb;
+    uint16_t* C;        // dW (M x N), written when slices == 1 and by the reduce
+    int64_t ldc;
+    float* part;        // slices x M x N fp32 partials (slices > 1)
+    int M, N, K, slices;
+};
+
+__global__ void __launch_bounds__(kGThreads, 1) gemm_wgrad_kernel(WgradArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t sa[2][kWBK * kWLD];
+    __shared__ __attribute__((aligned(16))) uint16_t sb[2][kWBK * kWLD];
+
+    const int nn = (a.N + kGBN - 1) / kGBN;
+    // slice-major order: the workgroups dispatched together cover all tiles of a slice
+    const int ntiles = ((a.M + kGBM - 1) / kGBM) * nn;
+    const int sl = blockIdx.x / ntiles, t = blockIdx.x - sl * ntiles;
+    const int m0 = (t / nn) * kGBM, n0 = (t - (t / nn) * nn) * kGBN;
+    const int nk = (a.K + kWBK - 1) / kWBK;
+    const int kb = (int)((int64_t)nk * sl / a.slices), ke = (int)((int64_t)nk * (sl + 1) / a.slices);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = (wave / (kGBN / kGWN)) * kGWM, wn = (wave % (kGBN / kGWN)) * kGWN;
+    const int g = lane >> 5;
+
+    // this wave's slot loads: instruction i = wave + 16 k covers 64 slots of the A tile
+    // (i < kWNI) or the B tile; per lane the column chunk's address at token row 0 (null:
+    // columns past M / N, read as zeros) and the slot's token row
+    const uint16_t* src[kWPW];
+    int trow[kWPW];
+#pragma unroll
+    for (int k = 0; k < kWPW; ++k) {
+        const int i = wave + kGWaves * k;
+        const int slot = (i % kWNI) * 64 + lane;
+        const int r = slot / kWSPR;
+        int c = slot - r * kWSPR;
+        if (c >= kGBM / 8) c -= kGBM / 8;  // pad slot: any in-row chunk
+        trow[k] = r;
+        src[k] = nullptr;
+        if (i < kWNI) {
+            if (m0 + 8 * c < a.M) src[k] = a.A + (int64_t)r * a.lda + m0 + 8 * c;
+        } else if (i < 2 * kWNI) {
+            if (n0 + 8 * c < a.N) src[k] = a.B + (int64_t)r * a.ldb + n0 + 8 * c;
+        }
+    }
+    auto issue = [&](int kt, int st) {
+        const int k0 = kt * kWBK;
+#pragma unroll
+        for (int k = 0; k < kWPW; ++k) {
+            const int i = wave + kGWaves * k;
+            if (i >= 2 * kWNI) break;
+            const bool isa = i < kWNI;
+            const uint16_t* tile = isa ? sa[st] : sb[st];
+            const uint32_t dst = lds_addr(tile + (i % kWNI) * 64 * 8);
+            const bool ok = src[k] != nullptr && k0 + trow[k] < a.K;
+            dma16(ok ? (const void*)(src[k] + (int64_t)k0 * (isa ? a.lda : a.ldb)) : (const void*)g_zero_line, dst);
+        }
+    };
+
+    f32x16 acc[kGTJ][kGTI];  // [j: 32 columns of B][i: 32 columns of A]
+#pragma unroll
+    for (int j = 0; j < kGTJ; ++j)
+#pragma unroll
+        for (int i = 0; i < kGTI; ++i) acc[j][i] = f32x16{};
+    if (kb < ke) issue(kb, 0);
+    int st = 0;
+    for (int kt = kb; kt < ke; ++kt, st ^= 1) {
+        tile_arrive();
+        if (kt + 1 < ke) issue(kt + 1, st ^ 1);
+        const uint16_t* At = sa[st];
+        const uint16_t* Bt = sb[st];
+#pragma unroll
+        for (int c = 0; c < kWBK / 16; ++c) {
+            bf16x8 av[kGTI], bv[kGTJ];
+#pragma unroll
+            for (int i = 0; i < kGTI; ++i) av[i] = lds_op_t(At, kWLD, 16 * c, wm + 32 * i, lane);
+#pragma unroll
+            for (int j = 0; j < kGTJ; ++j) bv[j] = lds_op_t(Bt, kWLD, 16 * c, wn + 32 * j, lane);
+#pragma unroll
+            for (int j = 0; j < kGTJ; ++j)
+#pragma unroll
+                for (int i = 0; i < kGTI; ++i) acc[j][i] = mfma32(av[i], bv[j], acc[j][i]);
+        }
+    }
+
+    // lane holds column n = n0 + wn + 32 j + lane%32 and rows m0 + wm + 32 i + 8 (e/4) + 4 g
+    // + e%4; a half-wave stores 32 consecutive columns of a row
+    float* part = a.slices > 1 ? a.part + (int64_t)sl * a.M * a.N : nullptr;
+#pragma unroll
+    for (int j = 0; j < kGTJ; ++j) {
+        const int n = n0 + wn + 32 * j + (lane & 31);
+        if (n >= a.N) continue;
+#pragma unroll
+        for (int i = 0; i < kGTI; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int m = m0 + wm + 32 * i + 8 * (e >> 2) + 4 * g + (e & 3);
+                if (m < a.M) {
+                    if (part)
+                        part[(int64_t)m * a.N + n] = acc[j][i][e];
+                    else
+                        a.C[(int64_t)m * a.ldc + n] = f32_to_bf16(acc[j][i][e]);
+                }
+            }
+    }
+}
+
+// C = bf16(sum over slices of the fp32 partials), slice 0 first; 8 consecutive
+// elements (one 16-byte store) per thread and step, N % 8 == 0
+__global__ void __launch_bounds__(256)
+wgrad_reduce_kernel(const float* __restrict__ part, int slices, int64_t MN, int N, uint16_t* __restrict__ C,
+                    int64_t ldc) {
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x; v < MN / 8; v += stride) {
+        float s[8];
+        const float4* p = reinterpret_cast<const float4*>(part + v * 8);
+        float4 lo = p[0], hi = p[1];
+        s[0] = lo.x; s[1] = lo.y; s[2] = lo.z; s[3] = lo.w;
+        s[4] = hi.x; s[5] = hi.y; s[6] = hi.z; s[7] = hi.w;
+        for (int k = 1; k < slices; ++k) {
+            const float4* q = reinterpret_cast<const float4*>(part + (int64_t)k * MN + v * 8);
+            lo = q[0];
+            hi = q[1];
+            s[0] += lo.x; s[1] += lo.y; s[2] += lo.z; s[3] += lo.w;
+            s[4] += hi.x; s[5] += hi.y; s[6] += hi.z; s[7] += hi.w;
+        }
+        const int64_t e = v * 8;
+        const int64_t m = e / N, n = e - m * N;
+        st16(C + m * ldc + n, pack8(s));
     }
 }
 
@@ -304,6 +456,62 @@ extern "C" int fx_linear_fwd(const uint16_t* X, int64_t ldx, const int32_t* idx,
     const int64_t grid = tiles < cus ? tiles : cus;
     hipLaunchKernelGGL(gemm_bias_act_kernel, dim3((unsigned)grid), dim3(kGThreads), 0, (hipStream_t)stream, a);
     return check_launch("gemm_bias_act");
+}
+
+// K steps of 64 tokens per slice at least 4, at most 32 slices, and no more workgroups
+// than CUs (one 147 KB workgroup per CU)
+static int wgrad_slices(int64_t M, int64_t N, int64_t K) {
+    const int64_t tiles = ((M + kGBM - 1) / kGBM) * ((N + kGBN - 1) / kGBN);
+    const int64_t nk = (K + kWBK - 1) / kWBK;
+    int64_t s = device_cus() / tiles;
+    if (s > nk / 4) s = nk / 4;
+    if (s > 32) s = 32;
+    return s < 1 ? 1 : (int)s;
+}
+
+extern "C" int64_t fx_linear_wgrad_workspace(int64_t M, int64_t N, int64_t K) {
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    const int s = wgrad_slices(M, N, K);
+    return s > 1 ? (int64_t)s * M * N * (int64_t)sizeof(float) : 0;
+}
+
+extern "C" int fx_linear_wgrad(const uint16_t* dY, int64_t ldy, const uint16_t* X, int64_t ldx, uint16_t* dW,
+                               int64_t ldw, float* work, int64_t M, int64_t N, int64_t K, void* stream) {
+    FX_REQUIRE(dW && (K == 0 || (dY && X)), "fx_linear_wgrad: null pointer");
+    FX_REQUIRE(M >= 8 && N >= 8 && K >= 0 && M % 8 == 0 && N % 8 == 0,
+               "fx_linear_wgrad: bad shape M=%lld N=%lld K=%lld (M, N multiples of 8)", (long long)M,
+               (long long)N, (long long)K);
+    FX_REQUIRE(M < 0x7fffffffLL && N < 0x7fffffffLL && K < 0x7fffffffLL && M * N < 0x7fffffffLL * 8,
+               "fx_linear_wgrad: size too large");
+    FX_REQUIRE(ldy >= M && ldx >= N && ldw >= N && ldy % 8 == 0 && ldx % 8 == 0 && ldw % 8 == 0,
+               "fx_linear_wgrad: bad leading dimension (ldy=%lld ldx=%lld ldw=%lld)", (long long)ldy,
+               (long long)ldx, (long long)ldw);
+    FX_REQUIRE(((((uintptr_t)dY) | ((uintptr_t)X) | ((uintptr_t)dW) | ((uintptr_t)work)) & 15) == 0,
+               "fx_linear_wgrad: dY, X, dW and work must be 16-byte aligned");
+    const int slices = K > 0 ? wgrad_slices(M, N, K) : 1;
+    FX_REQUIRE(slices == 1 || work != nullptr, "fx_linear_wgrad: null workspace (%d slices)", slices);
+    WgradArgs a;
+    a.A = dY;
+    a.lda = ldy;
+    a.B = X;
+    a.ldb = ldx;
+    a.C = dW;
+    a.ldc = ldw;
+    a.part = work;
+    a.M = (int)M;
+    a.N = (int)N;
+    a.K = (int)K;
+    a.slices = slices;
+    const int64_t tiles = ((M + kGBM - 1) / kGBM) * ((N + kGBN - 1) / kGBN);
+    hipStream_t s = (hipStream_t)stream;
+    hipLaunchKernelGGL(gemm_wgrad_kernel, dim3((unsigned)(tiles * slices)), dim3(kGThreads), 0, s, a);
+    if (int e = check_launch("gemm_wgrad")) return e;
+    if (slices == 1) return 0;
+    int64_t blocks = (M * N / 8 + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(wgrad_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, s, (const float*)work, slices,
+                       M * N, (int)N, dW, ldw);
+    return check_launch("wgrad_reduce");
 }
 
 extern "C" int fx_gelu_bwd(const uint16_t* dy, const uint16_t* h, uint16_t* dh, int64_t n, void* stream) {

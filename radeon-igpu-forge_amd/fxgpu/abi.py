@@ -96,6 +96,9 @@ SIGNATURES = {
     "fx_linear_fwd": (c_int32, [_P, c_int64, _P, c_int64, c_int64, _P, _P, _P, _P, _P,
                                 c_int64, c_int64, c_int64, c_int32, _P]),
     "fx_gelu_bwd": (c_int32, [_P, _P, _P, c_int64, _P]),
+    "fx_linear_wgrad_workspace": (c_int64, [c_int64, c_int64, c_int64]),
+    "fx_linear_wgrad": (c_int32, [_P, c_int64, _P, c_int64, _P, c_int64, _P, c_int64, c_int64, c_int64,
+                                  _P]),
 }
 
 _LIB = None

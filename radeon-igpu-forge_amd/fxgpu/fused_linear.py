@@ -9,13 +9,78 @@
   dense form with the activation fused into the GEMM epilogue, used by the
   GPT MLP as fc -> GELU(tanh): y = gelu(x W^T + b).  The pre-activation is kept
   for the backward: dh = dy * gelu'(h) (one elementwise kernel), then dx = dh W
-  and dW = dh^T x on the library GEMM.
+  on the library GEMM and dW = dh^T x on this build's split-K weight-gradient GEMM.
+* ``linear(x, weight)`` -- y = x W^T (no bias) with the same backward split: the
+  GPT's qkv, proj and fc2 projections.
+* ``linear_wgrad(dy, x)`` -- dW = dy^T x for dy (T, N) and x (T, K): the weight
+  gradient that ml/fxgpu/fused_linear.py:90-101 computes with rocBLAS.
 """
 import torch
 
-from fxgpu.abi import call, ptr, stream_of
+from fxgpu.abi import call, lib, ptr, stream_of
 
 _ACTS = {None: 0, "none": 0, "identity": 0, "gelu_tanh": 1}
+
+
+def _rows(t):
+    """t as a (rows, cols) view whose rows are 16-byte aligned and unit-stride."""
+    t2 = t.reshape(-1, t.shape[-1])
+    if t2.stride(1) != 1 or t2.stride(0) % 8 or t2.data_ptr() % 16:
+        t2 = t2.contiguous()
+    return t2
+
+
+def linear_wgrad(dy, x):
+    """dW = dy^T x in bf16 (fp32 accumulation): dy (..., N), x (..., K) bf16 with the
+    same leading shape; returns (N, K).  Widths that are not multiples of 8 (the
+    kernel stages 16-byte column chunks) take the library GEMM, as the reference's
+    rocBLAS dW does for every shape (ml/fxgpu/fused_linear.py:90-101)."""
+    if dy.dtype != torch.bfloat16 or x.dtype != torch.bfloat16:
+        raise TypeError("dy and x must be bfloat16")
+    if not (dy.is_cuda and x.is_cuda):
+        raise TypeError("dy and x must be cuda tensors")
+    dy2, x2 = _rows(dy), _rows(x)
+    if dy2.shape[0] != x2.shape[0]:
+        raise ValueError(f"dy has {dy2.shape[0]} rows, x has {x2.shape[0]}")
+    T, N = dy2.shape
+    K = x2.shape[1]
+    if N % 8 or K % 8:
+        return torch.mm(dy2.t(), x2)
+    dW = torch.empty(N, K, device=x.device, dtype=torch.bfloat16)
+    nbytes = int(lib().fx_linear_wgrad_workspace(N, K, T))
+    work = torch.empty((nbytes + 3) // 4, device=x.device, dtype=torch.float32) if nbytes else None
+    call("fx_linear_wgrad", ptr(dy2), dy2.stride(0), ptr(x2), x2.stride(0), ptr(dW), K, ptr(work), N, K, T,
+         stream_of(x))
+    return dW
+
+
+class Linear(torch.autograd.Function):
+    """y = x W^T for x (..., K) bf16, weight (N, K) bf16; dW on the split-K GEMM."""
+
+    @staticmethod
+    def forward(ctx, x, weight):
+        if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+            raise TypeError("x and weight must be bfloat16")
+        if weight.dim() != 2 or weight.shape[1] != x.shape[-1]:
+            raise ValueError(f"weight must be (N, {x.shape[-1]}), got {tuple(weight.shape)}")
+        x2 = _rows(x)
+        y = torch.mm(x2, weight.t())
+        ctx.save_for_backward(x2, weight)
+        ctx.xshape = x.shape
+        return y.view(*x.shape[:-1], weight.shape[0])
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, weight = ctx.saved_tensors
+        dy2 = _rows(dy.to(torch.bfloat16) if dy.dtype != torch.bfloat16 else dy)
+        dx = torch.mm(dy2, weight).view(ctx.xshape) if ctx.needs_input_grad[0] else None
+        dW = linear_wgrad(dy2, x2) if ctx.needs_input_grad[1] else None
+        return dx, dW
+
+
+def linear(x, weight):
+    """y = x @ weight.T (bf16), the weight gradient on this build's split-K GEMM."""
+    return Linear.apply(x, weight)
 
 
 class FusedGatherLinear(torch.autograd.Function):
@@ -67,7 +132,7 @@ class FusedGatherLinear(torch.autograd.Function):
     def backward(ctx, g):
         (Xg,) = ctx.saved_tensors
         g = g.contiguous()
-        dW = torch.mm(g.t(), Xg)          # (N, K)
+        dW = linear_wgrad(g, Xg)          # (N, K)
         db = g.sum(0)
         return None, None, dW, db
 
@@ -124,7 +189,7 @@ class FusedLinear(torch.autograd.Function):
         else:
             dh = dy2
         dx = torch.mm(dh, weight).view(ctx.xshape) if ctx.needs_input_grad[0] else None
-        dW = torch.mm(dh.t(), x2) if ctx.needs_input_grad[1] else None
+        dW = linear_wgrad(dh, x2) if ctx.needs_input_grad[1] else None
         db = dh.sum(0) if (ctx.has_bias and ctx.needs_input_grad[2]) else None
         return dx, dW, db, None
 

@@ -16,7 +16,7 @@ import torch
 import torch.nn.functional as Fn
 from torch import nn
 
-from fxgpu.fused_linear import fused_linear
+from fxgpu.fused_linear import fused_linear, linear
 
 from .attention import flash_attention_qkv
 from .cross_entropy import linear_cross_entropy
@@ -36,6 +36,7 @@ class GPTConfig:
     norm_impl: str = "fused"      # "fused" | "torch"
     ce_impl: str = "fused"        # "fused" | "torch"
     mlp_impl: str = "fused"       # "fused" | "torch"
+    linear_impl: str = "fused"    # qkv / proj / fc2: "fused" (split-K dW) | "torch"
     eps: float = 1e-6
 
 
@@ -48,6 +49,7 @@ class Block(nn.Module):
         self.attn_impl = cfg.attn_impl
         self.norm_impl = cfg.norm_impl
         self.mlp_impl = cfg.mlp_impl
+        self.linear_impl = cfg.linear_impl
         self.eps = cfg.eps
         self.ln1_w = nn.Parameter(torch.ones(D))
         self.ln2_w = nn.Parameter(torch.ones(D))
@@ -61,23 +63,28 @@ class Block(nn.Module):
             return rms_norm(x, w, self.eps)
         return Fn.rms_norm(x, (x.shape[-1],), w, self.eps)
 
+    def _lin(self, x, layer):
+        if self.linear_impl == "fused":
+            return linear(x, layer.weight)
+        return layer(x)
+
     def forward(self, x):
         B, T, D = x.shape
         h = self._norm(x, self.ln1_w)
-        qkv = self.qkv(h).view(B, T, 3, self.n_head, self.head_dim)
+        qkv = self._lin(h, self.qkv).view(B, T, 3, self.n_head, self.head_dim)
         if self.attn_impl == "flash":
             y = flash_attention_qkv(qkv, causal=True)
         else:
             q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))   # (B,H,T,Dh)
             y = Fn.scaled_dot_product_attention(q, k, v, is_causal=True)
             y = y.transpose(1, 2)
-        x = x + self.proj(y.reshape(B, T, D))
+        x = x + self._lin(y.reshape(B, T, D), self.proj)
         h = self._norm(x, self.ln2_w)
         if self.mlp_impl == "fused":
             u = fused_linear(h, self.fc.weight, None, "gelu_tanh")
         else:
             u = Fn.gelu(self.fc(h), approximate="tanh")
-        return x + self.fc2(u)
+        return x + self._lin(u, self.fc2)
 
 
 class GPT(nn.Module):

@@ -27,7 +27,7 @@ def test_fused_vs_torch_paths(dev):
     from fxlm.model import GPT
     torch.manual_seed(0)
     m_f = GPT(_cfg()).to(dev)
-    torch_cfg = dict(attn_impl="sdpa", norm_impl="torch", ce_impl="torch", mlp_impl="torch")
+    torch_cfg = dict(attn_impl="sdpa", norm_impl="torch", ce_impl="torch", mlp_impl="torch", linear_impl="torch")
     m_t = GPT(_cfg(**torch_cfg))
     m_r = GPT(_cfg(**torch_cfg))
     m_t.load_state_dict(m_f.state_dict())

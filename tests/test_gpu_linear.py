@@ -59,8 +59,11 @@ def test_reference_selftest_gather(dev):
     assert float((out_f.double() - out_r.double()).abs().max()) < 0.05
     g = torch.randn(B, HID, device=dev).bfloat16()
     out_f.backward(g)
-    dW_r = torch.mm(g.t(), xb)           # the reference's backward on the unfolded rows
-    assert float((w_f.grad.double() - dW_r.double()).abs().max()) < 1e-3
+    # the reference's backward on the unfolded rows, in fp64: the bf16 dW is its rounding
+    # (2^-9 relative) up to the fp32 accumulation order
+    from tolerances import bf16_close
+    dW_r = g.double().t() @ xb.double()
+    assert bf16_close(w_f.grad, dW_r, atol=1e-3 * float(dW_r.abs().max()), rtol=2.0 ** -8)
     assert float((b_f.grad.double() - g.sum(0).double()).abs().max()) < 1e-3
     bad = torch.randn(1000, 37, device=dev).bfloat16()
     with pytest.raises(ValueError, match="multiple of 8"):
@@ -135,3 +138,80 @@ def test_gather_more_tiles_than_workgroups(dev):
     out.backward(gy)
     rdw = gy.float().t() @ xg.float()
     assert float((W.grad.float() - rdw).abs().max()) <= _rel_tol(rdw)
+
+
+# ---- weight gradient dW = dY^T X (split-K GEMM) --------------------------------------
+# Elementwise bound: the bf16 rounding of the result (2^-9 relative, 2^-8 allowed) plus
+# 1e-3 of the largest |dW| for the fp32 accumulation over T tokens; a wrong slice,
+# transposed operand or dropped K step is off by O(1) relative.
+
+@pytest.mark.parametrize("T,N,K", [
+    (16384, 768, 3072),   # cfg5 fc2 dW
+    (16384, 3072, 768),   # cfg5 fc dW
+    (16384, 2304, 768),   # cfg5 qkv dW
+    (16384, 768, 768),    # cfg5 proj dW
+    (100, 64, 40),        # one slice, ragged token tail, N and K below a tile
+    (1000, 8, 2056),      # several slices, K past a tile boundary
+    (333, 264, 520),      # ragged everywhere
+    (1, 16, 8),
+])
+def test_wgrad_against_fp64(dev, T, N, K):
+    from fxgpu.fused_linear import linear_wgrad
+    from tolerances import bf16_close
+    g = torch.Generator(device=dev).manual_seed(T * 7 + N * 3 + K)
+    dy = torch.randn(T, N, device=dev, generator=g).bfloat16()
+    x = torch.randn(T, K, device=dev, generator=g).bfloat16()
+    dW = linear_wgrad(dy, x)
+    ref = dy.double().t() @ x.double()
+    scale = float(ref.abs().max())
+    assert dW.shape == (N, K) and dW.dtype == torch.bfloat16
+    assert bf16_close(dW, ref, atol=1e-3 * scale, rtol=2.0 ** -8)
+
+
+def test_wgrad_strided_rows(dev):
+    # dy and x as column windows of wider row-major buffers (row strides > width)
+    from fxgpu.fused_linear import linear_wgrad
+    from tolerances import bf16_close
+    g = torch.Generator(device=dev).manual_seed(5)
+    big_dy = torch.randn(2048, 800, device=dev, generator=g).bfloat16()
+    big_x = torch.randn(2048, 520, device=dev, generator=g).bfloat16()
+    dy, x = big_dy[:, 16:16 + 768], big_x[:, 8:8 + 512]
+    dW = linear_wgrad(dy, x)
+    ref = dy.double().t() @ x.double()
+    assert bf16_close(dW, ref, atol=1e-3 * float(ref.abs().max()), rtol=2.0 ** -8)
+
+
+def test_wgrad_no_tokens(dev):
+    from fxgpu.fused_linear import linear_wgrad
+    dW = linear_wgrad(torch.empty(0, 64, device=dev).bfloat16(), torch.empty(0, 32, device=dev).bfloat16())
+    assert dW.shape == (64, 32) and int((dW != 0).sum()) == 0
+
+
+def test_wgrad_rejects_bad_shapes(dev):
+    from fxgpu.abi import call, ptr
+    from fxgpu.fused_linear import linear_wgrad
+    with pytest.raises(ValueError):
+        linear_wgrad(torch.zeros(4, 16, device=dev).bfloat16(), torch.zeros(5, 16, device=dev).bfloat16())
+    # the C ABI itself refuses widths that are not multiples of 8
+    a = torch.zeros(4, 12, device=dev).bfloat16()
+    b = torch.zeros(4, 16, device=dev).bfloat16()
+    w = torch.zeros(12, 16, device=dev).bfloat16()
+    with pytest.raises(ValueError, match="multiples of 8"):
+        call("fx_linear_wgrad", ptr(a), 12, ptr(b), 16, ptr(w), 16, None, 12, 16, 4, None)
+
+
+def test_linear_autograd_against_fp32(dev):
+    from fxgpu.fused_linear import linear
+    g = torch.Generator(device=dev).manual_seed(11)
+    x = torch.randn(4, 256, 768, device=dev, generator=g).bfloat16()
+    W = (torch.randn(2304, 768, device=dev, generator=g) * 0.02).bfloat16()
+    dy = torch.randn(4, 256, 2304, device=dev, generator=g).bfloat16()
+    xa, Wa = x.clone().requires_grad_(), W.clone().requires_grad_()
+    y = linear(xa, Wa)
+    y.backward(dy)
+    xr, Wr = x.float().requires_grad_(), W.float().requires_grad_()
+    yr = xr @ Wr.t()
+    yr.backward(dy.float())
+    assert max_abs(y, yr) <= ATOL_BF16
+    assert max_abs(xa.grad, xr.grad) <= _rel_tol(xr.grad)
+    assert max_abs(Wa.grad, Wr.grad) <= _rel_tol(Wr.grad)
