@@ -307,7 +307,10 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
+    # 4 warm-up steps: one pass over each of the 4 synthetic batches the step cycles
+    # through (torch's embedding backward sizes its temporaries from the batch's token
+    # counts, so a batch's first step can allocate; 42 ms once when it fell in the timed steps)
+    ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU baseline")
     ap.add_argument("--only", choices=["attention", "ce", "norm", "adamw", "linear", "step", "copy"],
                     help="run one workload and print its figures (for profiling runs)")
