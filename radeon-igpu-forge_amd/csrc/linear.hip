@@ -56,25 +56,6 @@ struct GemmArgs {
     int act;   // 0: identity, 1: GELU (tanh approximation)
 };
 
-// GELU, tanh approximation: 0.5 h (1 + tanh(u)), u = sqrt(2/pi) (h + 0.044715 h^3),
-// evaluated as h - h / (e + 1) with e = exp(2u) (= h * sigmoid(2u)); the reciprocal is
-// v_rcp_f32 (1 ulp), not a correctly rounded division (a ten-instruction sequence).
-// e = inf gives h, e = 0 gives 0.
-__device__ __forceinline__ float gelu_tanh(float h) {
-    const float u = 0.7978845608028654f * fmaf(0.044715f * h, h * h, h);
-    const float e = exp2_fast(2.f * kLog2e * u);
-    return h - h * __builtin_amdgcn_rcpf(e + 1.f);
-}
-
-// d/dh of the above: 0.5 (1 + t) + 0.5 h (1 - t^2) u'(h), t = tanh(u) = 1 - 2 / (e + 1)
-__device__ __forceinline__ float gelu_tanh_grad(float h) {
-    const float u = 0.7978845608028654f * fmaf(0.044715f * h, h * h, h);
-    const float e = exp2_fast(2.f * kLog2e * u);
-    const float th = 1.f - 2.f * __builtin_amdgcn_rcpf(e + 1.f);
-    return 0.5f * (1.f + th) +
-           0.5f * h * (1.f - th * th) * 0.7978845608028654f * (1.f + 3.f * 0.044715f * h * h);
-}
-
 // tile t -> (row panel, column tile): with a multiple of 8 row panels, tiles with
 // t % 8 == c (run by the workgroups on XCD c) cover panels c, c+8, ... and walk all
 // column tiles of one panel in a row, so a panel's A rows are shared in that XCD's L2
