@@ -201,6 +201,34 @@ int fx_attn_fwd(const fxAttnArgs* args, void* stream);
  * ml/fxlm/kernels/attention.hip:228-534). */
 int fx_attn_bwd(const fxAttnArgs* args, void* stream);
 
+/* ---- decode attention (KV cache) ------------------------------------------- */
+
+/* One new query per (sequence, head) against the first lens[b] cached keys:
+ * o[b, h] = softmax(scale q[b, h] . K[b, :lens[b], h]^T) V[b, :lens[b], h].
+ * q element (b, h, d) at q[b*qsb + h*qsh + d]; cache element (b, t, h, d) at
+ * k[b*ksb + t*kst + h*ksh + d] (same for v); o (B, H, D) contiguous; lse (B, H) or NULL;
+ * work: fx_attn_decode_workspace(B, H, Tmax, D) bytes of fp32 (NULL when that is 0). */
+typedef struct fxAttnDecodeArgs {
+    const uint16_t* q;
+    const uint16_t* k;
+    const uint16_t* v;
+    const int32_t* lens;      /* (B,) device array, 0 <= lens[b] <= Tmax */
+    uint16_t* o;
+    float* lse;
+    float* work;
+    int64_t qsb, qsh, ksb, kst, ksh, vsb, vst, vsh;
+    int32_t B, H, Tmax, D;    /* D in {64, 128} */
+    float scale;              /* > 0 and finite */
+} fxAttnDecodeArgs;
+
+int64_t fx_attn_decode_workspace(int32_t B, int32_t H, int32_t Tmax, int32_t D);
+
+/* No counterpart in the reference, whose sampler re-runs the whole context through the
+ * model for every new token (ml/fxlm/sample.py:62-73); this is the KV-cache step that
+ * SURVEY ranks next for the inference path (bf16 in and out, fp32 softmax).  All
+ * vectors 16-byte aligned, strides multiples of 8 elements. */
+int fx_attn_decode(const fxAttnDecodeArgs* args, void* stream);
+
 /* ---- fused (gather) linear ------------------------------------------------- */
 
 /* Y = act(A W^T + bias), A (M, K): dense rows (A row m = X + m*ldx) when idx is NULL,

@@ -65,3 +65,27 @@ def attn_bwd(q, k, v, o, lse, do, causal=True, scale=None, dtype=torch.float64):
 def delta(o, do, dtype=torch.float64):
     """Delta (B,H,T) = rowsum(dO * O)."""
     return (_bhtd(do, dtype) * _bhtd(o, dtype)).sum(-1)
+
+
+def attn_decode(q, k_cache, v_cache, lens, scale=None, dtype=torch.float64):
+    """Decode step: q (B, H, D) against the first lens[b] rows of k_cache / v_cache
+    (B, Tmax, H, D).  Returns (o (B, H, D), lse (B, H)) in `dtype`: the last row of the
+    causal forward above over those keys (an empty cache gives o = 0, lse = -inf)."""
+    B, Tmax, H, D = k_cache.shape
+    scale = D ** -0.5 if scale is None else scale
+    qd = q.detach().to("cpu", dtype)
+    kd, vd = k_cache.detach().to("cpu", dtype), v_cache.detach().to("cpu", dtype)
+    lens = [int(x) for x in lens.detach().cpu()]
+    o = torch.zeros(B, H, D, dtype=dtype)
+    lse = torch.full((B, H), float("-inf"), dtype=dtype)
+    for b in range(B):
+        n = max(0, min(lens[b], Tmax))
+        if n == 0:
+            continue
+        s = torch.einsum("hd,thd->ht", qd[b], kd[b, :n]) * scale    # (H, n)
+        m = s.amax(-1, keepdim=True)
+        e = torch.exp(s - m)
+        l = e.sum(-1, keepdim=True)
+        o[b] = torch.einsum("ht,thd->hd", e / l, vd[b, :n])
+        lse[b] = (m + torch.log(l)).squeeze(-1)
+    return o, lse

@@ -75,6 +75,17 @@ class fxAttnArgs(ctypes.Structure):
     ]
 
 
+class fxAttnDecodeArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", c_void_p), ("k", c_void_p), ("v", c_void_p), ("lens", c_void_p),
+        ("o", c_void_p), ("lse", c_void_p), ("work", c_void_p),
+        ("qsb", c_int64), ("qsh", c_int64), ("ksb", c_int64), ("kst", c_int64), ("ksh", c_int64),
+        ("vsb", c_int64), ("vst", c_int64), ("vsh", c_int64),
+        ("B", c_int32), ("H", c_int32), ("Tmax", c_int32), ("D", c_int32),
+        ("scale", c_float),
+    ]
+
+
 _P = c_void_p
 # name -> (restype, argtypes); must list exactly the functions of fx_abi.h
 SIGNATURES = {
@@ -93,6 +104,8 @@ SIGNATURES = {
                                 c_int32, _P]),
     "fx_attn_fwd": (c_int32, [ctypes.POINTER(fxAttnArgs), _P]),
     "fx_attn_bwd": (c_int32, [ctypes.POINTER(fxAttnArgs), _P]),
+    "fx_attn_decode_workspace": (c_int64, [c_int32, c_int32, c_int32, c_int32]),
+    "fx_attn_decode": (c_int32, [ctypes.POINTER(fxAttnDecodeArgs), _P]),
     "fx_linear_fwd": (c_int32, [_P, c_int64, _P, c_int64, c_int64, _P, _P, _P, _P, _P,
                                 c_int64, c_int64, c_int64, c_int32, _P]),
     "fx_gelu_bwd": (c_int32, [_P, _P, _P, c_int64, _P]),

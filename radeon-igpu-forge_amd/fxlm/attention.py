@@ -11,7 +11,7 @@ import math
 
 import torch
 
-from fxgpu.abi import call, fxAttnArgs, stream_of
+from fxgpu.abi import call, fxAttnArgs, fxAttnDecodeArgs, lib, stream_of
 
 
 def _check_qkv(q, k, v):
@@ -151,3 +151,49 @@ def attention_fwd_raw(q, k, v, causal=True, scale=None):
     if scale is None:
         scale = 1.0 / math.sqrt(q.shape[-1])
     return _fwd(q, k, v, causal, float(scale))
+
+
+def decode_attention(q, k_cache, v_cache, lens, scale=None, return_lse=False):
+    """One new query per (sequence, head) against a KV cache (inference).
+
+    q (B, H, Dh) bf16; k_cache, v_cache (B, Tmax, H, Dh) bf16 (unit stride along Dh,
+    b/t/h strides multiples of 8); lens (B,) int32 cuda: the number of valid cached keys
+    of each sequence (the new token's own key included).  Returns o (B, H, Dh) bf16 =
+    softmax(scale q K[:lens]^T) V[:lens], and the fp32 logsumexp (B, H) if asked.
+    """
+    if q.dim() != 3 or k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
+        raise ValueError(f"q (B,H,Dh) and caches (B,Tmax,H,Dh): {tuple(q.shape)} "
+                         f"{tuple(k_cache.shape)} {tuple(v_cache.shape)}")
+    B, Tmax, H, Dh = k_cache.shape
+    if tuple(q.shape) != (B, H, Dh):
+        raise ValueError(f"q {tuple(q.shape)} does not match the cache {tuple(k_cache.shape)}")
+    if Dh not in (64, 128):
+        raise ValueError(f"head_dim {Dh} not supported (must be 64 or 128)")
+    for nm, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache)):
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"{nm} must be bfloat16, got {t.dtype}")
+        if not t.is_cuda:
+            raise TypeError(f"{nm} must be a cuda tensor")
+        if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:-1]) or t.data_ptr() % 16:
+            raise ValueError(f"{nm}: last dim must be contiguous, other strides multiples of 8 "
+                             "elements and the base 16-byte aligned")
+    if lens.dtype != torch.int32 or not lens.is_cuda or lens.shape != (B,):
+        raise TypeError(f"lens must be an int32 cuda tensor of shape ({B},)")
+    if scale is None:
+        scale = 1.0 / math.sqrt(Dh)
+    lens = lens.contiguous()
+    o = torch.empty(B, H, Dh, device=q.device, dtype=torch.bfloat16)
+    lse = torch.empty(B, H, device=q.device, dtype=torch.float32) if return_lse else None
+    nbytes = int(lib().fx_attn_decode_workspace(B, H, Tmax, Dh))
+    work = torch.empty((nbytes + 3) // 4, device=q.device, dtype=torch.float32) if nbytes else None
+    a = fxAttnDecodeArgs()
+    a.q, a.k, a.v, a.lens, a.o = q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), lens.data_ptr(), o.data_ptr()
+    a.lse = lse.data_ptr() if lse is not None else None
+    a.work = work.data_ptr() if work is not None else None
+    a.qsb, a.qsh = q.stride(0), q.stride(1)
+    a.ksb, a.kst, a.ksh = _strides3(k_cache)
+    a.vsb, a.vst, a.vsh = _strides3(v_cache)
+    a.B, a.H, a.Tmax, a.D = B, H, Tmax, Dh
+    a.scale = float(scale)
+    call("fx_attn_decode", ctypes.byref(a), stream_of(q))
+    return (o, lse) if return_lse else o

@@ -107,3 +107,55 @@ def test_cfg2_full_size(dev):
         rdq, rdk, rdv = oatt.attn_bwd(q[sl], k[sl], v[sl], o[sl].detach(), rl, do[sl], True,
                                       dtype=torch.float32)
         _check((o[sl], lse[sl], qq.grad[sl], kk.grad[sl], vv.grad[sl]), (ro, rl, rdq, rdk, rdv))
+
+
+# ---- decode attention (KV cache) ------------------------------------------------------
+
+@pytest.mark.parametrize("B,Tmax,H,D,lens", [
+    (2, 1024, 12, 64, [1024, 513]),        # four 256-key chunks, ragged second sequence
+    (3, 300, 4, 128, [1, 256, 257]),       # chunk boundaries at D = 128
+    (1, 256, 2, 64, [200]),                # one chunk: written without the merge
+    (4, 2048, 8, 64, [2048, 1, 1500, 0]),  # an empty sequence
+])
+def test_decode_against_oracle(dev, B, Tmax, H, D, lens):
+    from fxlm.attention import decode_attention
+    g = torch.Generator(device=dev).manual_seed(B * 1000 + Tmax + D)
+    q = torch.randn(B, H, D, device=dev, generator=g).bfloat16()
+    k = torch.randn(B, Tmax, H, D, device=dev, generator=g).bfloat16()
+    v = torch.randn(B, Tmax, H, D, device=dev, generator=g).bfloat16()
+    lt = torch.tensor(lens, dtype=torch.int32, device=dev)
+    o, lse = decode_attention(q, k, v, lt, return_lse=True)
+    ro, rlse = oatt.attn_decode(q, k, v, lt)
+    assert max_abs(o, ro) <= ATOL_BF16
+    lse_c = lse.cpu().double()
+    fin = torch.isfinite(rlse)
+    assert torch.equal(torch.isfinite(lse_c), fin)
+    assert float(((lse_c[fin] - rlse[fin]).abs() / rlse[fin].abs().clamp_min(1.0)).max()) <= 1e-3
+    assert float(o.float().cpu()[~fin].abs().max() if (~fin).any() else 0.0) == 0.0
+
+
+def test_decode_matches_forward_last_row(dev):
+    # a cache that is the (strided) k / v view of a fused qkv buffer
+    from fxlm.attention import attention_fwd_raw, decode_attention
+    g = torch.Generator(device=dev).manual_seed(17)
+    B, T, H, D = 2, 777, 12, 64
+    qkv = torch.randn(B, T, 3, H, D, device=dev, generator=g).bfloat16()
+    q, k, v = qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2]
+    o_full, _ = attention_fwd_raw(q, k, v, causal=True)
+    for n in (1, 256, 500, T):
+        lt = torch.full((B,), n, dtype=torch.int32, device=dev)
+        o = decode_attention(q[:, n - 1], k, v, lt)
+        assert max_abs(o, o_full[:, n - 1].float()) <= ATOL_BF16
+
+
+def test_decode_rejects_bad_arguments(dev):
+    from fxlm.attention import decode_attention
+    q = torch.zeros(1, 2, 64, device=dev).bfloat16()
+    k = torch.zeros(1, 8, 2, 64, device=dev).bfloat16()
+    with pytest.raises(TypeError):
+        decode_attention(q, k, k, torch.ones(1, dtype=torch.int64, device=dev))
+    with pytest.raises(ValueError):
+        decode_attention(torch.zeros(1, 2, 96, device=dev).bfloat16(),
+                         torch.zeros(1, 8, 2, 96, device=dev).bfloat16(),
+                         torch.zeros(1, 8, 2, 96, device=dev).bfloat16(),
+                         torch.ones(1, dtype=torch.int32, device=dev))

@@ -81,6 +81,25 @@ def test_attention_special_cases():
     assert torch.allclose(o[:, 0], v[:, 0])       # causal row 0 sees only key 0
 
 
+def test_attention_decode_is_the_last_causal_row():
+    # the decode step over the first n keys equals row n-1 of the causal forward, for
+    # every n (closed under the forward oracle pinned above)
+    g = torch.Generator().manual_seed(3)
+    B, T, H, D = 2, 9, 3, 64
+    q, k, v = (torch.randn(B, T, H, D, generator=g) for _ in range(3))
+    o_full, lse_full = oatt.attn_fwd(q, k, v, causal=True)
+    for n in range(1, T + 1):
+        lens = torch.full((B,), n, dtype=torch.int32)
+        o, lse = oatt.attn_decode(q[:, n - 1], k, v, lens)
+        assert torch.allclose(o, o_full[:, n - 1], atol=1e-12)
+        assert torch.allclose(lse, lse_full[:, :, n - 1], atol=1e-12)
+    # per-sequence lengths: sequence 0 empty, sequence 1 at its second token
+    q_sel = torch.stack([q[0, 0], q[1, 1]])
+    o, lse = oatt.attn_decode(q_sel, k, v, torch.tensor([0, 2], dtype=torch.int32))
+    assert float(o[0].abs().max()) == 0 and bool(torch.isinf(lse[0]).all())
+    assert torch.allclose(o[1], o_full[1, 1], atol=1e-12)
+
+
 def test_attention_delta_uses_stored_output():
     # Delta is rowsum(dO * O) of the output handed in (the rounded one), not a recomputed O.
     torch.manual_seed(5)
