@@ -18,7 +18,7 @@ from torch import nn
 
 from fxgpu.fused_linear import fused_linear, linear
 
-from .attention import flash_attention_qkv
+from .attention import decode_attention, flash_attention_qkv
 from .cross_entropy import linear_cross_entropy
 from .norm import rms_norm
 
@@ -68,10 +68,23 @@ class Block(nn.Module):
             return linear(x, layer.weight)
         return layer(x)
 
-    def forward(self, x):
+    def _mlp(self, x):
+        h = self._norm(x, self.ln2_w)
+        if self.mlp_impl == "fused":
+            u = fused_linear(h, self.fc.weight, None, "gelu_tanh")
+        else:
+            u = Fn.gelu(self.fc(h), approximate="tanh")
+        return x + self._lin(u, self.fc2)
+
+    def forward(self, x, kv=None):
+        """kv: optional (k_cache, v_cache) (B, Tmax, H, Dh) that receive this block's
+        keys and values at positions 0..T-1 (the prompt of a cached generation)."""
         B, T, D = x.shape
         h = self._norm(x, self.ln1_w)
         qkv = self._lin(h, self.qkv).view(B, T, 3, self.n_head, self.head_dim)
+        if kv is not None:
+            kv[0][:, :T].copy_(qkv[:, :, 1])
+            kv[1][:, :T].copy_(qkv[:, :, 2])
         if self.attn_impl == "flash":
             y = flash_attention_qkv(qkv, causal=True)
         else:
@@ -79,12 +92,19 @@ class Block(nn.Module):
             y = Fn.scaled_dot_product_attention(q, k, v, is_causal=True)
             y = y.transpose(1, 2)
         x = x + self._lin(y.reshape(B, T, D), self.proj)
-        h = self._norm(x, self.ln2_w)
-        if self.mlp_impl == "fused":
-            u = fused_linear(h, self.fc.weight, None, "gelu_tanh")
-        else:
-            u = Fn.gelu(self.fc(h), approximate="tanh")
-        return x + self._lin(u, self.fc2)
+        return self._mlp(x)
+
+    def step(self, x, kv, pos, lens):
+        """One new token per sequence: x (B, 1, D) at position `pos`; its key and value
+        go into the caches at `pos`, then attention over the first pos + 1 cached keys."""
+        B, _, D = x.shape
+        h = self._norm(x, self.ln1_w)
+        qkv = self._lin(h, self.qkv).view(B, 1, 3, self.n_head, self.head_dim)
+        kv[0][:, pos].copy_(qkv[:, 0, 1])
+        kv[1][:, pos].copy_(qkv[:, 0, 2])
+        y = decode_attention(qkv[:, 0, 0], kv[0], kv[1], lens)          # (B, H, Dh)
+        x = x + self._lin(y.reshape(B, 1, D), self.proj)
+        return self._mlp(x)
 
 
 class GPT(nn.Module):
@@ -138,3 +158,75 @@ class GPT(nn.Module):
                                         targets.reshape(-1), grad_scale=grad_scale)
         logits = Fn.linear(x, self._head_w())
         return Fn.cross_entropy(logits.float().view(-1, logits.shape[-1]), targets.reshape(-1))
+
+    # -- cached inference ------------------------------------------------------------
+    # The reference's sampler re-runs the whole (cropped) context for every new token
+    # (ml/fxlm/sample.py:62-73).  Here the prompt runs once through the blocks, which
+    # leave their keys and values in a bf16 cache, and each new token runs the blocks
+    # on one row per sequence with decode attention over the cache.
+
+    def init_cache(self, batch, max_len=None):
+        """Per-layer (k, v) caches (batch, max_len, H, Dh) bf16 on the model's device."""
+        cfg = self.cfg
+        T = cfg.seq_len if max_len is None else min(int(max_len), cfg.seq_len)
+        H, Dh = cfg.n_head, cfg.d_model // cfg.n_head
+        dev = self.pos_emb.device
+        return [(torch.empty(batch, T, H, Dh, device=dev, dtype=torch.bfloat16),
+                 torch.empty(batch, T, H, Dh, device=dev, dtype=torch.bfloat16))
+                for _ in self.blocks]
+
+    @torch.no_grad()
+    def prefill(self, idx, cache):
+        """Run the prompt idx (B, T) and fill the caches; returns the last position's
+        logits (B, V) in fp32."""
+        if self.cfg.attn_impl != "flash":
+            raise ValueError("cached inference needs attn_impl='flash'")
+        B, T = idx.shape
+        if T > cache[0][0].shape[1]:
+            raise ValueError(f"prompt of {T} tokens exceeds the cache ({cache[0][0].shape[1]})")
+        x = self.tok_emb(idx) + self.pos_emb[:T]
+        for blk, kv in zip(self.blocks, cache):
+            x = blk(x, kv)
+        x = self._norm_f(x[:, -1:].contiguous())
+        return Fn.linear(x[:, 0], self._head_w()).float()
+
+    @torch.no_grad()
+    def decode_step(self, tok, cache, pos):
+        """tok (B,) int64 at position pos (< the cache length, every sequence at the same
+        position); returns its logits (B, V) in fp32."""
+        B = tok.shape[0]
+        lens = torch.full((B,), pos + 1, dtype=torch.int32, device=tok.device)
+        x = self.tok_emb(tok.view(B, 1)) + self.pos_emb[pos:pos + 1]
+        for blk, kv in zip(self.blocks, cache):
+            x = blk.step(x, kv, pos, lens)
+        x = self._norm_f(x)
+        return Fn.linear(x[:, 0], self._head_w()).float()
+
+    @torch.no_grad()
+    def generate(self, idx, max_new, temperature=0.8, top_k=50, generator=None):
+        """Sample max_new tokens after idx (B, T) as ml/fxlm/sample.py:62-73 does
+        (temperature, top-k, multinomial); returns (B, max_new) int64.  While the
+        context fits seq_len each token is one cached step; past it, as in the
+        reference, the model re-runs the last seq_len tokens."""
+        x = idx
+        B = idx.shape[0]
+        L = self.cfg.seq_len
+        cache = self.init_cache(B, min(L, idx.shape[1] + max_new)) if idx.shape[1] < L else None
+        logits = self.prefill(idx, cache) if cache is not None else None
+        out = []
+        for _ in range(max_new):
+            if logits is None:  # context beyond seq_len: re-run the cropped window
+                logits = self(x[:, -L:])[:, -1, :].float()
+            logits = logits / max(temperature, 1e-5)
+            if top_k > 0:
+                v, _ = torch.topk(logits, min(top_k, logits.shape[-1]))
+                logits = logits.masked_fill(logits < v[:, -1:], -float("inf"))
+            nxt = torch.multinomial(torch.softmax(logits, dim=-1), 1, generator=generator)
+            out.append(nxt)
+            x = torch.cat([x, nxt], dim=1)
+            pos = x.shape[1] - 1
+            if len(out) == max_new:
+                break
+            logits = self.decode_step(nxt[:, 0], cache, pos) if cache is not None and pos < cache[0][0].shape[1] \
+                else None
+        return torch.cat(out, dim=1) if out else idx.new_zeros(B, 0)
