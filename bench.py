@@ -60,6 +60,30 @@ def time_us(torch, fn, iters=20, warm=5):
     return s.elapsed_time(e) / iters * 1e3
 
 
+def graph_time_us(torch, fn, reps=20, iters=10):
+    """Average duration (us) of fn() captured `reps` times in one HIP graph and replayed
+    `iters` times: the GPU time of short launches without the host's per-call cost."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    t0, t1 = _events(torch)
+    t0.record()
+    for _ in range(iters):
+        g.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / (iters * reps) * 1e3
+
+
 def bench_attention(torch):
     from fxlm.attention import _bwd, _fwd
     B, T, H, D = 16, 1024, 12, 64
@@ -163,6 +187,57 @@ def bench_linear(torch):
     return {"shape": [M, K, N], "fwd_us": round(t, 2), "tflops": round(f / t / 1e6, 1),
             "frac_of_bf16_peak": round(f / t / 1e6 / BF16_PEAK_TFLOPS, 4),
             "hipblaslt_mm_plus_gelu_us": round(t_ref, 2)}
+
+
+def bench_decode(torch):
+    """Inference: decode attention over a KV cache (HBM-bound kernel) and one cached
+    token step of the cfg5 model against the reference sampler's full-context re-run."""
+    from fxlm.attention import decode_attention
+    from fxlm.model import GPT, GPTConfig
+    B, T, H, D = 16, 1024, 12, 64
+    g = torch.Generator(device="cuda").manual_seed(7)
+    q = torch.randn(B, H, D, device="cuda", generator=g).bfloat16()
+    k = torch.randn(B, T, H, D, device="cuda", generator=g).bfloat16()
+    v = torch.randn(B, T, H, D, device="cuda", generator=g).bfloat16()
+    lens = torch.full((B,), T, dtype=torch.int32, device="cuda")
+    t_k = graph_time_us(torch, lambda: decode_attention(q, k, v, lens))
+    nbytes = 2 * B * T * H * D * 2 + 2 * B * H * D * 2           # K and V read once, q, o
+    del q, k, v
+    # the step's few-row GEMMs (16 rows): this build's kernel against the library GEMM
+    from fxgpu.fused_linear import fused_linear, linear
+    gemms = {}
+    for name, (n, kk) in {"qkv": (2304, 768), "fc_gelu": (3072, 768), "fc2": (768, 3072),
+                          "head": (CFG5["vocab_size"], 768)}.items():
+        x = torch.randn(B, kk, device="cuda", generator=g).bfloat16()
+        w = (torch.randn(n, kk, device="cuda", generator=g) * 0.02).bfloat16()
+        ours = (lambda: fused_linear(x, w, None, "gelu_tanh")) if name == "fc_gelu" else (lambda: linear(x, w))
+        with torch.no_grad():
+            t_o = graph_time_us(torch, ours)
+            t_l = graph_time_us(torch, lambda: torch.mm(x, w.t()))
+        gemms[name] = {"us": round(t_o, 2), "library_mm_us": round(t_l, 2),
+                       "weight_gbs": round(n * kk * 2 / t_o / 1e3, 1)}
+        del x, w
+    c = CFG5
+    torch.manual_seed(0)
+    m = GPT(GPTConfig(vocab_size=c["vocab_size"], seq_len=c["seq_len"], n_layer=c["n_layer"],
+                      n_head=c["n_head"], d_model=c["d_model"])).cuda().bfloat16().eval()
+    ctx = 512
+    idx = torch.randint(0, c["vocab_size"], (B, ctx + 1), device="cuda", generator=g)
+    cache = m.init_cache(B, ctx + 1)
+    with torch.no_grad():
+        m.prefill(idx[:, :ctx], cache)
+        t_step = time_us(torch, lambda: m.decode_step(idx[:, ctx], cache, ctx), iters=10, warm=3)
+        step = m.decode_graph(cache, B)
+        t_graph = time_us(torch, lambda: step(idx[:, ctx], ctx), iters=50, warm=5)
+        t_full = time_us(torch, lambda: m(idx[:, 1:ctx + 1])[:, -1, :].float(), iters=10, warm=3)
+    del m, cache, step
+    return {"kernel_shape": [B, T, H, D], "kernel_us": round(t_k, 2), "kernel_gbs": round(nbytes / t_k / 1e3, 1),
+            "kernel_frac_of_hbm": round(nbytes / t_k / 1e3 / HBM_PEAK_GBS, 4), "kernel_bytes": nbytes,
+            "few_row_gemms": gemms,
+            "model": f"cfg5 GPT, batch {B}, context {ctx}", "cached_step_us": round(t_step, 1),
+            "cached_graph_step_us": round(t_graph, 1), "recompute_step_us": round(t_full, 1),
+            "tok_s_cached_graph": round(B / t_graph * 1e6, 1), "tok_s_cached": round(B / t_step * 1e6, 1),
+            "tok_s_recompute": round(B / t_full * 1e6, 1)}
 
 
 def gpu_step_bench(torch, steps, warmup):
@@ -319,7 +394,7 @@ def main():
     # counts, so a batch's first step can allocate; 42 ms once when it fell in the timed steps)
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU baseline")
-    ap.add_argument("--only", choices=["attention", "ce", "norm", "adamw", "linear", "step", "copy"],
+    ap.add_argument("--only", choices=["attention", "ce", "norm", "adamw", "linear", "step", "copy", "decode"],
                     help="run one workload and print its figures (for profiling runs)")
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV",
                                                        "COPY_WRITE_CSV"),
@@ -340,7 +415,7 @@ def main():
     lib()
     if args.only:
         fn = {"attention": bench_attention, "ce": bench_ce, "norm": bench_norm, "adamw": bench_adamw,
-              "linear": bench_linear, "copy": bench_copy,
+              "linear": bench_linear, "copy": bench_copy, "decode": bench_decode,
               "step": lambda t: gpu_step_bench(t, args.steps, args.warmup)}[args.only]
         r = fn(torch)
         print(json.dumps({k: v for k, v in r.items() if not k.startswith("flop")}))
@@ -351,6 +426,7 @@ def main():
     norm = bench_norm(torch)
     adamw = bench_adamw(torch)
     lin = bench_linear(torch)
+    dec = bench_decode(torch)
     torch.cuda.empty_cache()
     step = gpu_step_bench(torch, args.steps, args.warmup)
     torch.cuda.empty_cache()
@@ -380,7 +456,7 @@ def main():
         "gpu_over_cpu": (round(step["tok_s"] / cpu["value"], 1) if cpu else None),
         "kernels": {"attention_cfg2": {k: v for k, v in attn.items() if not k.startswith("flop")},
                     "cross_entropy_cfg3": ce, "rmsnorm_cfg4": norm, "flat_adamw_cfg4": adamw,
-                    "fused_linear_gelu_cfg5_fc": lin},
+                    "fused_linear_gelu_cfg5_fc": lin, "decode": dec},
         "final_loss": round(step["loss"], 4),
     }
     print(json.dumps(out))

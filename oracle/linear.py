@@ -14,12 +14,17 @@ import torch
 
 
 def gather(X, idx, K):
-    """Xg (B, K) from X (R, F) and window starts idx (B,)."""
+    """Xg (B, K) from X (R, F) and window starts idx (B,).  A window that leaves X
+    (idx < 0 or idx + W > R) is all zeros: the reference does not range-check idx
+    (ml/fxgpu/gather_gemm.hip:45-46 reads X[idx + w] unchecked), so this build defines
+    that case and its kernels follow the definition."""
     Xf = X.detach().cpu()
-    F = Xf.shape[1]
+    R, F = Xf.shape
     W = K // F
-    rows = idx.detach().cpu().long()[:, None] + torch.arange(W)[None, :]   # (B, W)
-    return Xf[rows].reshape(rows.shape[0], W * F)
+    st = idx.detach().cpu().long()
+    ok = (st >= 0) & (st + W <= R)
+    rows = torch.where(ok, st, 0)[:, None] + torch.arange(W)[None, :]     # (B, W)
+    return (Xf[rows] * ok[:, None, None].to(Xf.dtype)).reshape(rows.shape[0], W * F)
 
 
 def gather_linear(X, idx, weight, bias, dtype=torch.float64):

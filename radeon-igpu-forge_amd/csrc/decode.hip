@@ -5,29 +5,30 @@
 // recomputes from the whole context for every token (ml/fxlm/sample.py:62-73).
 //
 // HBM-bound (each cached key and value is read once per step, 4 D bytes per key and
-// head), so the work is split over the keys: one wave per (sequence, head, chunk of
-// kChunk keys).  A key row is read by D/8 lanes, 16 bytes each, so one load instruction
+// head), so the work is split over the keys: one wave per (sequence, head, chunk of CH
+// keys), CH = 256, 128 or 64, the largest that still gives kDecWaves waves (enough
+// loads in flight to cover HBM latency).  A key row is read by D/8 lanes, 16 bytes each, so one load instruction
 // covers 64 / (D/8) whole rows.  Pass 1 keeps all of the chunk's scores in registers
 // (log2 domain, q pre-scaled), then one max / exp pass; pass 2 accumulates P V with
 // each lane owning 8 of the D outputs; the partial (max, sum, o) of every chunk is
-// merged by the second kernel with the same rule as the forward's lse (a chunk without
-// valid keys carries max = -inf, sum = 0).  With a single chunk the first kernel writes
-// the result itself.
+// merged by the second kernel with the same rule as the forward's lse.  Chunks that
+// start at or past the sequence's length do nothing and the merge reads only the
+// chunks below it.  With a single chunk the first kernel writes the result itself.
 #include <math.h>
 
 #include "fx_device.h"
 
 namespace fx {
 
-constexpr int kDecChunk = 256;   // keys per wave
-constexpr int kDecBatch = 8;     // key loads in flight per lane
+constexpr int kDecBatch = 8;      // key loads in flight per lane
+constexpr int kDecWaves = 2048;   // grid size the chunk choice aims for
 constexpr float kDecNegInf = -__builtin_huge_valf();
 
-template <int D>
+template <int D, int CH>
 __global__ void __launch_bounds__(64) attn_decode_kernel(fxAttnDecodeArgs a, int nchunks) {
     constexpr int LPK = D / 8;       // lanes per key row
     constexpr int KPI = 64 / LPK;    // key rows per load instruction
-    constexpr int NS = kDecChunk / KPI;  // load steps per chunk
+    constexpr int NS = CH / KPI;     // load steps per chunk
     static_assert(NS % kDecBatch == 0, "chunk");
     const int lane = threadIdx.x;
     const int kg = lane / LPK, dl = lane % LPK;  // key group and 8-element slice of D
@@ -36,7 +37,8 @@ __global__ void __launch_bounds__(64) attn_decode_kernel(fxAttnDecodeArgs a, int
     const int b = bh / a.H, h = bh - b * a.H;
     int len = a.lens[b];
     len = len < 0 ? 0 : (len > a.Tmax ? a.Tmax : len);
-    const int j0 = c * kDecChunk;
+    const int j0 = c * CH;
+    if (nchunks > 1 && j0 >= len) return;  // the merge skips this chunk
 
     float qf[8];
     {
@@ -123,23 +125,27 @@ __global__ void __launch_bounds__(64) attn_decode_kernel(fxAttnDecodeArgs a, int
     if (dl == 0) *reinterpret_cast<float2*>(w) = make_float2(m, l);
 }
 
-// merge the chunk partials of one (sequence, head) per wave: M = max m_c,
-// L = sum l_c 2^(m_c - M), o = sum o_c 2^(m_c - M) / L, lse = (M + log2 L) ln 2
-template <int D>
+// merge the chunk partials of one (sequence, head) per wave, over the chunks that hold
+// keys (c CH < len): M = max m_c, L = sum l_c 2^(m_c - M), o = sum o_c 2^(m_c - M) / L,
+// lse = (M + log2 L) ln 2
+template <int D, int CH>
 __global__ void __launch_bounds__(64) attn_decode_merge_kernel(fxAttnDecodeArgs a, int nchunks) {
     constexpr int EPL = D / 64;  // outputs per lane
     const int lane = threadIdx.x;
     const int bh = blockIdx.x;
+    int len = a.lens[bh / a.H];
+    len = len < 0 ? 0 : (len > a.Tmax ? a.Tmax : len);
+    const int nc = (len + CH - 1) / CH;  // <= nchunks
     const float* w = a.work + (int64_t)bh * nchunks * (D + 4);
     float M = kDecNegInf;
-    for (int c = 0; c < nchunks; ++c) M = fmaxf(M, w[(int64_t)c * (D + 4)]);
+    for (int c = 0; c < nc; ++c) M = fmaxf(M, w[(int64_t)c * (D + 4)]);
     const float mu = M == kDecNegInf ? 0.f : M;
     float L = 0.f, o[EPL];
 #pragma unroll
     for (int e = 0; e < EPL; ++e) o[e] = 0.f;
-    for (int c = 0; c < nchunks; ++c) {
+    for (int c = 0; c < nc; ++c) {
         const float* p = w + (int64_t)c * (D + 4);
-        const float f = exp2_fast(p[0] - mu);  // 0 for a chunk without keys
+        const float f = exp2_fast(p[0] - mu);
         L += p[1] * f;
 #pragma unroll
         for (int e = 0; e < EPL; ++e) o[e] += p[4 + lane * EPL + e] * f;
@@ -151,7 +157,26 @@ __global__ void __launch_bounds__(64) attn_decode_merge_kernel(fxAttnDecodeArgs 
     if (a.lse && lane == 0) a.lse[bh] = L > 0.f ? (M + log2_fast(L)) * kLn2 : kDecNegInf;
 }
 
-static int decode_chunks(int32_t Tmax) { return (Tmax + kDecChunk - 1) / kDecChunk; }
+// keys per chunk: the largest of 256, 128, 64 whose grid reaches kDecWaves waves
+static int decode_chunk(int32_t B, int32_t H, int32_t Tmax) {
+    for (int ch = 256; ch > 64; ch >>= 1)
+        if ((int64_t)B * H * ((Tmax + ch - 1) / ch) >= kDecWaves) return ch;
+    return 64;
+}
+static int decode_chunks(int32_t B, int32_t H, int32_t Tmax) {
+    const int ch = decode_chunk(B, H, Tmax);
+    return (Tmax + ch - 1) / ch;
+}
+
+template <int D, int CH>
+static int decode_launch(const fxAttnDecodeArgs& a, int nc, hipStream_t st) {
+    const unsigned nbh = (unsigned)(a.B * a.H);
+    hipLaunchKernelGGL((attn_decode_kernel<D, CH>), dim3(nbh * nc), dim3(64), 0, st, a, nc);
+    if (int e = check_launch("attn_decode")) return e;
+    if (nc == 1) return 0;
+    hipLaunchKernelGGL((attn_decode_merge_kernel<D, CH>), dim3(nbh), dim3(64), 0, st, a, nc);
+    return check_launch("attn_decode_merge");
+}
 
 }  // namespace fx
 
@@ -159,7 +184,7 @@ using namespace fx;
 
 extern "C" int64_t fx_attn_decode_workspace(int32_t B, int32_t H, int32_t Tmax, int32_t D) {
     if (B <= 0 || H <= 0 || Tmax <= 0 || D <= 0) return 0;
-    const int nc = decode_chunks(Tmax);
+    const int nc = decode_chunks(B, H, Tmax);
     return nc > 1 ? (int64_t)B * H * nc * (D + 4) * (int64_t)sizeof(float) : 0;
 }
 
@@ -169,7 +194,7 @@ extern "C" int fx_attn_decode(const fxAttnDecodeArgs* args, void* stream) {
     FX_REQUIRE(a.D == 64 || a.D == 128, "fx_attn_decode: head_dim %d not supported (64 or 128)", a.D);
     FX_REQUIRE(a.B >= 1 && a.H >= 1 && a.Tmax >= 1, "fx_attn_decode: bad shape B=%d H=%d Tmax=%d", a.B, a.H,
                a.Tmax);
-    FX_REQUIRE((int64_t)a.B * a.H * decode_chunks(a.Tmax) < 0x7fffffffLL, "fx_attn_decode: grid too large");
+    FX_REQUIRE((int64_t)a.B * a.H * ((a.Tmax + 63) / 64) < 0x7fffffffLL, "fx_attn_decode: grid too large");
     FX_REQUIRE(a.q && a.k && a.v && a.lens && a.o, "fx_attn_decode: null pointer");
     FX_REQUIRE(a.scale > 0.f && a.scale < __builtin_huge_valf(), "fx_attn_decode: scale %g must be positive and finite",
                (double)a.scale);
@@ -177,19 +202,15 @@ extern "C" int fx_attn_decode(const fxAttnDecodeArgs* args, void* stream) {
     for (int64_t x : s) FX_REQUIRE(x % 8 == 0, "fx_attn_decode: strides must be multiples of 8 elements");
     FX_REQUIRE((((uintptr_t)a.q | (uintptr_t)a.k | (uintptr_t)a.v | (uintptr_t)a.o | (uintptr_t)a.work) & 15) == 0,
                "fx_attn_decode: q, k, v, o and work must be 16-byte aligned");
-    const int nc = decode_chunks(a.Tmax);
+    const int ch = decode_chunk(a.B, a.H, a.Tmax);
+    const int nc = (a.Tmax + ch - 1) / ch;
     FX_REQUIRE(nc == 1 || a.work != nullptr, "fx_attn_decode: null workspace (%d chunks)", nc);
-    const unsigned nbh = (unsigned)(a.B * a.H);
     hipStream_t st = (hipStream_t)stream;
     if (a.D == 64)
-        hipLaunchKernelGGL(attn_decode_kernel<64>, dim3(nbh * nc), dim3(64), 0, st, a, nc);
-    else
-        hipLaunchKernelGGL(attn_decode_kernel<128>, dim3(nbh * nc), dim3(64), 0, st, a, nc);
-    if (int e = check_launch("attn_decode")) return e;
-    if (nc == 1) return 0;
-    if (a.D == 64)
-        hipLaunchKernelGGL(attn_decode_merge_kernel<64>, dim3(nbh), dim3(64), 0, st, a, nc);
-    else
-        hipLaunchKernelGGL(attn_decode_merge_kernel<128>, dim3(nbh), dim3(64), 0, st, a, nc);
-    return check_launch("attn_decode_merge");
+        return ch == 256 ? decode_launch<64, 256>(a, nc, st)
+             : ch == 128 ? decode_launch<64, 128>(a, nc, st)
+                         : decode_launch<64, 64>(a, nc, st);
+    return ch == 256 ? decode_launch<128, 256>(a, nc, st)
+         : ch == 128 ? decode_launch<128, 128>(a, nc, st)
+                     : decode_launch<128, 64>(a, nc, st);
 }

@@ -371,6 +371,145 @@ wgrad_reduce_kernel(const float* __restrict__ part, int slices, int64_t MN, int 
     }
 }
 
+// ---------------------------------------------------------------------------
+// Few-row forward (M <= 64: decoding, small batches).  The GEMM is then a stream
+// over W (N K bf16 read once), so the kernel is shaped for loads in flight, not for
+// operand reuse.  It computes the transpose, C^T (N x M) = W X^T, with
+// v_mfma_f32_16x16x32_bf16: A = 16 W rows, B = 16 X rows, both read straight from
+// global memory in 16-byte row chunks (lane l takes row l%16 and k = k0 + 8(l/16) +
+// 0..7 in both operands: the K order inside one instruction is the same for the two,
+// so the product is the plain contraction); the accumulator lane l holds column
+// (X row) l%16 and rows (W rows) 4(l/16) + 0..3.  A workgroup owns 16 NT rows of W and
+// its sw waves split the K steps of 32; each wave keeps NT x MT accumulator tiles.
+// The partial tiles meet in LDS and are summed in wave order (deterministic), then
+// + bias, activation and the stores.  Gathered rows work as in the tiled kernel; the
+// first workgroup writes them out (Xg) while it streams them.
+constexpr int kSKMaxM = 64;
+constexpr int kSKMaxTiles = 16;  // sw * NT * MT: 1 KB of LDS per accumulator tile
+
+__device__ __forceinline__ f32x4 mfma16(const uint4& a, const uint4& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+
+template <int NT, int MT>
+__global__ void __launch_bounds__(1024) gemm_skinny_kernel(GemmArgs a, int sw) {
+    constexpr int U = NT * MT >= 4 ? 2 : 4;  // K steps per load batch
+    __shared__ __attribute__((aligned(16))) float red[kSKMaxTiles * 256];
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, kg = lane >> 4;
+    const int n0 = blockIdx.x * 16 * NT;
+    const int ks = (a.K + 31) / 32;
+    const int kb = w * ks / sw, ke = (w + 1) * ks / sw;
+
+    const uint16_t* wrow[NT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+        const int n = n0 + 16 * i + r;
+        wrow[i] = n < a.N ? a.B + (int64_t)n * a.ldb + 8 * kg : nullptr;
+    }
+    const uint16_t* xrow[MT];
+#pragma unroll
+    for (int j = 0; j < MT; ++j) {
+        const int m = 16 * j + r;
+        const uint16_t* row = nullptr;
+        if (m < a.M) {
+            if (a.idx) {
+                const int64_t st = a.idx[m];
+                if (st >= 0 && st * a.F + a.K <= a.R * a.F) row = a.A + st * a.F;
+            } else {
+                row = a.A + (int64_t)m * a.lda;
+            }
+        }
+        xrow[j] = row ? row + 8 * kg : nullptr;
+    }
+    const bool wxg = a.Xg != nullptr && blockIdx.x == 0;
+
+    f32x4 acc[NT][MT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i)
+#pragma unroll
+        for (int j = 0; j < MT; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const uint4 zero = make_uint4(0u, 0u, 0u, 0u);
+    for (int s0 = kb; s0 < ke; s0 += U) {
+        uint4 wv[U][NT], xv[U][MT];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int s = s0 + u;
+            const bool ok = s < ke && s * 32 + 8 * kg < a.K;
+#pragma unroll
+            for (int i = 0; i < NT; ++i) wv[u][i] = ok && wrow[i] ? ld16(wrow[i] + s * 32) : zero;
+#pragma unroll
+            for (int j = 0; j < MT; ++j) xv[u][j] = ok && xrow[j] ? ld16(xrow[j] + s * 32) : zero;
+        }
+        if (wxg) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int s = s0 + u;
+                if (s >= ke || s * 32 + 8 * kg >= a.K) continue;
+#pragma unroll
+                for (int j = 0; j < MT; ++j) {
+                    const int m = 16 * j + r;
+                    if (m < a.M) st16(a.Xg + (int64_t)m * a.ldxg + s * 32 + 8 * kg, xv[u][j]);
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int i = 0; i < NT; ++i)
+#pragma unroll
+                for (int j = 0; j < MT; ++j) acc[i][j] = mfma16(wv[u][i], xv[u][j], acc[i][j]);
+    }
+#pragma unroll
+    for (int i = 0; i < NT; ++i)
+#pragma unroll
+        for (int j = 0; j < MT; ++j)
+            *reinterpret_cast<f32x4*>(&red[((w * NT + i) * MT + j) * 256 + lane * 4]) = acc[i][j];
+    __syncthreads();
+    // value (tile, m_local, n_local), n_local fastest so neighbouring threads store
+    // neighbouring columns; in the accumulator layout it sits at lane m_local +
+    // 16 (n_local / 4), element n_local % 4
+    constexpr int kVals = NT * MT * 256;
+    for (int v = threadIdx.x; v < kVals; v += blockDim.x) {
+        const int tile = v >> 8, ml = (v >> 4) & 15, nl = v & 15;
+        const int off = tile * 256 + (ml + 16 * (nl >> 2)) * 4 + (nl & 3);
+        float sum = 0.f;
+        for (int ww = 0; ww < sw; ++ww) sum += red[ww * kVals + off];
+        const int n = n0 + 16 * (tile / MT) + nl, m = 16 * (tile % MT) + ml;
+        if (n < a.N && m < a.M) {
+            const float h = sum + (a.bias ? bf16_to_f32(a.bias[n]) : 0.f);
+            if (a.H) a.H[(int64_t)m * a.ldh + n] = f32_to_bf16(h);
+            a.C[(int64_t)m * a.ldc + n] = f32_to_bf16(a.act == 1 ? gelu_tanh(h) : h);
+        }
+    }
+}
+
+template <int NT>
+static int skinny_launch(const GemmArgs& a, hipStream_t st) {
+    const int mt = (a.M + 15) / 16;
+    const int64_t nblk = ((int64_t)a.N + 16 * NT - 1) / (16 * NT);
+    const int64_t ks = (a.K + 31) / 32;
+    const int64_t target = 4LL * device_cus();  // waves
+    int sw = 1;
+    while (sw < 16 && nblk * sw < target && 2 * sw <= ks && 2 * sw * NT * mt <= kSKMaxTiles) sw *= 2;
+    const dim3 grid((unsigned)nblk), block(64 * sw);
+    switch (mt) {
+        case 1: hipLaunchKernelGGL((gemm_skinny_kernel<NT, 1>), grid, block, 0, st, a, sw); break;
+        case 2: hipLaunchKernelGGL((gemm_skinny_kernel<NT, 2>), grid, block, 0, st, a, sw); break;
+        case 3: hipLaunchKernelGGL((gemm_skinny_kernel<NT, 3>), grid, block, 0, st, a, sw); break;
+        default: hipLaunchKernelGGL((gemm_skinny_kernel<NT, 4>), grid, block, 0, st, a, sw); break;
+    }
+    return check_launch("gemm_skinny");
+}
+
+// two W row tiles per workgroup once there are enough workgroups (fewer re-reads of X)
+static int linear_skinny(const GemmArgs& a, hipStream_t st) {
+    if ((a.N + 31) / 32 >= 2LL * device_cus()) return skinny_launch<2>(a, st);
+    return skinny_launch<1>(a, st);
+}
+
 __global__ void __launch_bounds__(256)
 gelu_bwd_kernel(const uint16_t* __restrict__ dy, const uint16_t* __restrict__ h, uint16_t* __restrict__ dh,
                 int64_t n) {
@@ -430,7 +569,8 @@ extern "C" int fx_linear_fwd(const uint16_t* X, int64_t ldx, const int32_t* idx,
     a.N = (int)N;
     a.K = (int)K;
     a.act = act;
-    const int64_t tiles = ((M + kGBM - 1) / kGBM) * ((N + kGBN - 1) / kGBN);
+    if (M <= kSKMaxM) return linear_skinny(a, (hipStream_t)stream);
+    const int64_t tiles =((M + kGBM - 1) / kGBM) * ((N + kGBN - 1) / kGBN);
     FX_REQUIRE(tiles < 0x7fffffffLL, "fx_linear_fwd: too many tiles");
     // persistent grid: one workgroup per CU (the LDS of one is 147 KB)
     const int64_t cus = device_cus();

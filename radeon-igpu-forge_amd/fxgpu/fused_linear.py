@@ -11,7 +11,9 @@
   for the backward: dh = dy * gelu'(h) (one elementwise kernel), then dx = dh W
   on the library GEMM and dW = dh^T x on this build's split-K weight-gradient GEMM.
 * ``linear(x, weight)`` -- y = x W^T (no bias) with the same backward split: the
-  GPT's qkv, proj and fc2 projections.
+  GPT's qkv, proj and fc2 projections.  Forwards of at most FEW_ROWS rows (decode
+  steps) run on the few-row kernel behind fx_linear_fwd, larger ones on the library
+  GEMM.
 * ``linear_wgrad(dy, x)`` -- dW = dy^T x for dy (T, N) and x (T, K): the weight
   gradient that ml/fxgpu/fused_linear.py:90-101 computes with rocBLAS.
 """
@@ -54,6 +56,19 @@ def linear_wgrad(dy, x):
     return dW
 
 
+# Up to this many rows the forward GEMM is a stream over the weight (decoding, small
+# batches) and runs on this build's few-row kernel; above it on the library GEMM.
+FEW_ROWS = 64
+
+
+def _few_rows(x2, weight):
+    M, K = x2.shape
+    y = torch.empty(M, weight.shape[0], device=x2.device, dtype=torch.bfloat16)
+    call("fx_linear_fwd", ptr(x2), x2.stride(0), None, 0, 0, ptr(weight), None, ptr(y), None, None,
+         M, weight.shape[0], K, 0, stream_of(x2))
+    return y
+
+
 class Linear(torch.autograd.Function):
     """y = x W^T for x (..., K) bf16, weight (N, K) bf16; dW on the split-K GEMM."""
 
@@ -64,7 +79,11 @@ class Linear(torch.autograd.Function):
         if weight.dim() != 2 or weight.shape[1] != x.shape[-1]:
             raise ValueError(f"weight must be (N, {x.shape[-1]}), got {tuple(weight.shape)}")
         x2 = _rows(x)
-        y = torch.mm(x2, weight.t())
+        if (0 < x2.shape[0] <= FEW_ROWS and x2.shape[1] % 8 == 0 and x2.is_cuda and weight.is_contiguous()
+                and weight.data_ptr() % 16 == 0):
+            y = _few_rows(x2, weight)
+        else:
+            y = torch.mm(x2, weight.t())
         ctx.save_for_backward(x2, weight)
         ctx.xshape = x.shape
         return y.view(*x.shape[:-1], weight.shape[0])

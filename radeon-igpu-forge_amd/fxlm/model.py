@@ -95,13 +95,15 @@ class Block(nn.Module):
         return self._mlp(x)
 
     def step(self, x, kv, pos, lens):
-        """One new token per sequence: x (B, 1, D) at position `pos`; its key and value
-        go into the caches at `pos`, then attention over the first pos + 1 cached keys."""
+        """One new token per sequence: x (B, 1, D) at the position held by the device
+        tensor pos (1,) int64; its key and value go into the caches there, then attention
+        over the first lens[b] cached keys.  No host value depends on the position, so a
+        step can be captured once in a HIP graph and replayed for every token."""
         B, _, D = x.shape
         h = self._norm(x, self.ln1_w)
         qkv = self._lin(h, self.qkv).view(B, 1, 3, self.n_head, self.head_dim)
-        kv[0][:, pos].copy_(qkv[:, 0, 1])
-        kv[1][:, pos].copy_(qkv[:, 0, 2])
+        kv[0].index_copy_(1, pos, qkv[:, :, 1])
+        kv[1].index_copy_(1, pos, qkv[:, :, 2])
         y = decode_attention(qkv[:, 0, 0], kv[0], kv[1], lens)          # (B, H, Dh)
         x = x + self._lin(y.reshape(B, 1, D), self.proj)
         return self._mlp(x)
@@ -131,6 +133,12 @@ class GPT(nn.Module):
     def _init(m):
         if isinstance(m, (nn.Linear, nn.Embedding)):
             nn.init.normal_(m.weight, std=0.02)
+
+    def _head(self, x):
+        """Logits of a few rows (prefill's last position, decode steps)."""
+        if self.cfg.linear_impl == "fused" and x.is_cuda:
+            return linear(x, self._head_w())
+        return Fn.linear(x, self._head_w())
 
     def _norm_f(self, x):
         if self.cfg.norm_impl == "fused":
@@ -188,31 +196,51 @@ class GPT(nn.Module):
         for blk, kv in zip(self.blocks, cache):
             x = blk(x, kv)
         x = self._norm_f(x[:, -1:].contiguous())
-        return Fn.linear(x[:, 0], self._head_w()).float()
+        return self._head(x[:, 0]).float()
+
+    def _decode(self, tok, cache, pos, lens):
+        """Cached step with the position in device memory: tok (B,) int64, pos (1,) int64,
+        lens (B,) int32 = pos + 1; returns the logits (B, V) fp32."""
+        B = tok.shape[0]
+        x = self.tok_emb(tok.view(B, 1)) + self.pos_emb.index_select(0, pos)
+        for blk, kv in zip(self.blocks, cache):
+            x = blk.step(x, kv, pos, lens)
+        x = self._norm_f(x)
+        return self._head(x[:, 0]).float()
 
     @torch.no_grad()
     def decode_step(self, tok, cache, pos):
         """tok (B,) int64 at position pos (< the cache length, every sequence at the same
         position); returns its logits (B, V) in fp32."""
         B = tok.shape[0]
+        if pos >= cache[0][0].shape[1]:
+            raise ValueError(f"position {pos} is past the cache ({cache[0][0].shape[1]})")
+        p = torch.full((1,), pos, dtype=torch.int64, device=tok.device)
         lens = torch.full((B,), pos + 1, dtype=torch.int32, device=tok.device)
-        x = self.tok_emb(tok.view(B, 1)) + self.pos_emb[pos:pos + 1]
-        for blk, kv in zip(self.blocks, cache):
-            x = blk.step(x, kv, pos, lens)
-        x = self._norm_f(x)
-        return Fn.linear(x[:, 0], self._head_w()).float()
+        return self._decode(tok, cache, p, lens)
+
+    def decode_graph(self, cache, batch):
+        """A HIP graph of one cached step for `cache` (the launches of ~14 ops per layer
+        otherwise cost more host time than the step's GPU work).  Call the returned
+        object as step(tok, pos) -> logits (B, V) fp32; the logits tensor is reused by
+        the next call."""
+        return _DecodeGraph(self, cache, batch)
 
     @torch.no_grad()
-    def generate(self, idx, max_new, temperature=0.8, top_k=50, generator=None):
+    def generate(self, idx, max_new, temperature=0.8, top_k=50, generator=None, graph=True):
         """Sample max_new tokens after idx (B, T) as ml/fxlm/sample.py:62-73 does
         (temperature, top-k, multinomial); returns (B, max_new) int64.  While the
-        context fits seq_len each token is one cached step; past it, as in the
-        reference, the model re-runs the last seq_len tokens."""
+        context fits seq_len each token is one cached step (replayed from a HIP graph
+        when `graph`); past it, as in the reference, the model re-runs the last seq_len
+        tokens."""
         x = idx
         B = idx.shape[0]
         L = self.cfg.seq_len
         cache = self.init_cache(B, min(L, idx.shape[1] + max_new)) if idx.shape[1] < L else None
         logits = self.prefill(idx, cache) if cache is not None else None
+        step = None
+        if cache is not None and max_new > 1:
+            step = self.decode_graph(cache, B) if graph else (lambda t, p: self.decode_step(t, cache, p))
         out = []
         for _ in range(max_new):
             if logits is None:  # context beyond seq_len: re-run the cropped window
@@ -227,6 +255,43 @@ class GPT(nn.Module):
             pos = x.shape[1] - 1
             if len(out) == max_new:
                 break
-            logits = self.decode_step(nxt[:, 0], cache, pos) if cache is not None and pos < cache[0][0].shape[1] \
-                else None
+            logits = step(nxt[:, 0], pos) if step is not None and pos < cache[0][0].shape[1] else None
         return torch.cat(out, dim=1) if out else idx.new_zeros(B, 0)
+
+
+class _DecodeGraph:
+    """One cached decode step captured in a HIP graph (torch.cuda.CUDAGraph).  Inputs
+    are copied into static device tensors before each replay; the kernels read the
+    position from them, so one capture serves every position of the cache."""
+
+    def __init__(self, model, cache, batch):
+        dev = cache[0][0].device
+        self.cache_len = cache[0][0].shape[1]
+        self.tok = torch.zeros(batch, dtype=torch.int64, device=dev)
+        self.pos = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.lens = torch.ones(batch, dtype=torch.int32, device=dev)
+        with torch.no_grad():
+            # warm-up off the capture (library handles, workspaces), as torch requires;
+            # position 0 only rewrites a cache row the real prompt fills again
+            s = torch.cuda.Stream(device=dev)
+            s.wait_stream(torch.cuda.current_stream(dev))
+            saved = [(k[:, :1].clone(), v[:, :1].clone()) for k, v in cache]
+            with torch.cuda.stream(s):
+                for _ in range(2):
+                    model._decode(self.tok, cache, self.pos, self.lens)
+            torch.cuda.current_stream(dev).wait_stream(s)
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph):
+                self.logits = model._decode(self.tok, cache, self.pos, self.lens)
+            for (k, v), (k0, v0) in zip(cache, saved):
+                k[:, :1].copy_(k0)
+                v[:, :1].copy_(v0)
+
+    def __call__(self, tok, pos):
+        if pos >= self.cache_len:
+            raise ValueError(f"position {pos} is past the cache ({self.cache_len})")
+        self.tok.copy_(tok)
+        self.pos.fill_(pos)
+        self.lens.fill_(pos + 1)
+        self.graph.replay()
+        return self.logits

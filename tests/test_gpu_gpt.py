@@ -134,3 +134,39 @@ def test_generate_samples_with_top_k(dev):
     out = m.generate(idx, 16, temperature=0.8, top_k=50, generator=g)
     assert out.shape == (3, 16) and int(out.min()) >= 0 and int(out.max()) < 512
     assert m.generate(idx, 0).shape == (3, 0)
+
+
+def test_decode_graph_replays_match_eager(dev):
+    # one capture serves every position: each replay is checked against the eager step
+    # on a copy of the cache, with eager work and synchronisations between replays
+    m = _bf16_model(dev)
+    g = torch.Generator(device=dev).manual_seed(11)
+    B, T0, n = 3, 9, 6
+    x = torch.randint(0, 512, (B, T0 + n), device=dev, generator=g)
+    cache = m.init_cache(B, T0 + n)
+    with torch.no_grad():
+        m.prefill(x[:, :T0], cache)
+    ref_cache = [(k.clone(), v.clone()) for k, v in cache]
+    step = m.decode_graph(cache, B)
+    for t in range(T0, T0 + n):
+        got = step(x[:, t], t).clone()
+        torch.cuda.synchronize()
+        want = m.decode_step(x[:, t], ref_cache, t)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), t
+        for (k, v), (rk, rv) in zip(cache, ref_cache):
+            assert torch.equal(k[:, :t + 1], rk[:, :t + 1]) and torch.equal(v[:, :t + 1], rv[:, :t + 1])
+    with pytest.raises(ValueError):
+        step(x[:, 0], T0 + n)
+
+
+def test_generate_graph_equals_eager(dev):
+    # same logits and the same sampler stream give the same tokens (bf16 logits can tie
+    # exactly, so even top_k = 1 draws: each run gets an identically seeded generator)
+    m = _bf16_model(dev)
+    g = torch.Generator(device=dev).manual_seed(4)
+    idx = torch.randint(0, 512, (2, 30), device=dev, generator=g)
+    a = m.generate(idx, 20, temperature=0.9, top_k=40, generator=torch.Generator(device=dev).manual_seed(1))
+    b = m.generate(idx, 20, temperature=0.9, top_k=40, generator=torch.Generator(device=dev).manual_seed(1),
+                   graph=False)
+    assert torch.equal(a, b)

@@ -290,3 +290,15 @@ def test_cpu_gpt_initial_loss_and_learning():
     for _ in range(15):
         l1 = ogpt.cpu_train_step(m, opt, x, y)
     assert l1 < 0.9 * l0
+
+
+def test_gather_windows_against_unfold_and_outside_zero():
+    # in-range windows are the window-major unfold of X; a window leaving X is zeros
+    from oracle.linear import gather
+    X = torch.randn(30, 8, dtype=torch.float64)
+    idx = torch.tensor([0, 26, 13, -1, 27, 5])
+    Xg = gather(X, idx, 4 * 8)
+    unf = X.unfold(0, 4, 1).transpose(1, 2).reshape(27, 32)   # (R - W + 1, W F)
+    for b, st in enumerate(idx.tolist()):
+        want = unf[st] if 0 <= st <= 26 else torch.zeros(32, dtype=torch.float64)
+        assert torch.equal(Xg[b], want)
