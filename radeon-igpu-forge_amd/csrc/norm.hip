@@ -136,10 +136,10 @@ template <int LPR, int NV, int NT = kNormBwdThreads, int MW = norm_bwd_min_waves
 __global__ void __launch_bounds__(NT, MW)
 rms_bwd_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ dy,
                const uint16_t* __restrict__ w, const float* __restrict__ rstd,
-               uint16_t* __restrict__ dx, float* __restrict__ part, int64_t N, int D) {
+               uint16_t* __restrict__ dx, float* __restrict__ part, int64_t N, int D, int per_wave) {
     constexpr int G = NT / LPR;
     constexpr int NW = NT / 64;
-    extern __shared__ float red[];  // D floats
+    extern __shared__ float red[];  // NW x D floats (per_wave) or D floats
     const int lane = threadIdx.x % LPR;
     const int grp = threadIdx.x / LPR;
     const int V8 = D >> 3;
@@ -174,8 +174,32 @@ rms_bwd_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ dy,
         for (int i = 0; i < NV; ++i)
 #pragma unroll
             for (int j = 0; j < 8; ++j) acc[i][j] += __shfl_xor(acc[i][j], off, 64);
-    // waves: fixed-order fold through LDS
+    // waves: with per_wave, each writes its partial row to LDS, one barrier, then every
+    // column is summed over the waves in order (1 us faster at [65536, 768] than the
+    // wave-by-wave fold with a barrier per wave, which wide rows use: NW x D floats
+    // would not fit in LDS)
     const int wave = threadIdx.x >> 6;
+    float* pr = part + (int64_t)blockIdx.x * D;
+    if (per_wave) {
+        if ((threadIdx.x & 63) < LPR) {
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                const int c = i * LPR + lane;
+                if (c < V8) {
+                    float4* r = reinterpret_cast<float4*>(red + wave * D + c * 8);
+                    r[0] = make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+                    r[1] = make_float4(acc[i][4], acc[i][5], acc[i][6], acc[i][7]);
+                }
+            }
+        }
+        __syncthreads();
+        for (int c = threadIdx.x; c < D; c += NT) {
+            float sum = red[c];
+            for (int k = 1; k < NW; ++k) sum += red[k * D + c];
+            pr[c] = sum;
+        }
+        return;
+    }
     for (int wv = 0; wv < NW; ++wv) {
         if (wave == wv && (threadIdx.x & 63) < LPR) {
 #pragma unroll
@@ -190,44 +214,43 @@ rms_bwd_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ dy,
         }
         __syncthreads();
     }
-    float* pr = part + (int64_t)blockIdx.x * D;
     for (int c = threadIdx.x; c < D; c += NT) pr[c] = red[c];
 }
 
-// dw[c] = sum_p part[p][c] in a fixed order.  A block owns 16 columns (4 float4
-// lanes) and 64 partial-row lanes (16 per wave); each thread sums every 64th partial
-// row of its 4 columns with all its loads in flight, the row lanes of a wave fold
-// with a butterfly (every lane ends with the same bits) and the 4 waves through LDS.
-// D % 8 == 0, so a column quad never straddles D.
+// dw[c] = sum_p part[p][c] in a fixed order.  A block owns 8 columns (2 float4 lanes)
+// and 128 partial-row lanes (32 per wave): each thread sums every 128th partial row of
+// its 4 columns with its loads in flight, the row lanes of a wave fold with a butterfly
+// (every lane ends with the same bits) and the 4 waves through LDS.  96 blocks at D = 768
+// (16-column blocks with 64 row lanes: 0.3 us slower).
 __global__ void __launch_bounds__(256)
 rms_dw_reduce_kernel(const float* __restrict__ part, int64_t P, int D, float* __restrict__ dw_f32,
                      uint16_t* __restrict__ dw) {
-    __shared__ float4 red[4][4];
-    const int ql = threadIdx.x & 3, rl = threadIdx.x >> 2;
-    const int col = blockIdx.x * 16 + ql * 4;
+    __shared__ float4 red[4][2];
+    const int cg = threadIdx.x & 1, rl = threadIdx.x >> 1;
+    const int col = blockIdx.x * 8 + cg * 4;
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
     if (col < D) {
-#pragma unroll 16
-        for (int64_t p = rl; p < P; p += 64) {
+#pragma unroll 8
+        for (int64_t p = rl; p < P; p += 128) {
             const float4 v = *reinterpret_cast<const float4*>(part + p * D + col);
             s.x += v.x; s.y += v.y; s.z += v.z; s.w += v.w;
         }
     }
 #pragma unroll
-    for (int off = 4; off < 64; off <<= 1) {
+    for (int off = 2; off < 64; off <<= 1) {
         s.x += __shfl_xor(s.x, off, 64);
         s.y += __shfl_xor(s.y, off, 64);
         s.z += __shfl_xor(s.z, off, 64);
         s.w += __shfl_xor(s.w, off, 64);
     }
     const int wave = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) < 4) red[wave][ql] = s;
+    if ((threadIdx.x & 63) < 2) red[wave][cg] = s;
     __syncthreads();
-    if (threadIdx.x < 4 && col < D) {
-        float4 t = red[0][ql];
+    if (threadIdx.x < 2 && col < D) {
+        float4 t = red[0][cg];
 #pragma unroll
         for (int k = 1; k < 4; ++k) {
-            const float4 v = red[k][ql];
+            const float4 v = red[k][cg];
             t.x += v.x; t.y += v.y; t.z += v.z; t.w += v.w;
         }
         *reinterpret_cast<float4*>(dw_f32 + col) = t;
@@ -347,7 +370,7 @@ extern "C" int fx_rms_norm_bwd(const uint16_t* x, const uint16_t* dy, const uint
                "fx_rms_norm_bwd: null pointer");
     if (N == 0) {
         // dw of an empty batch is zero
-        hipLaunchKernelGGL(rms_dw_reduce_kernel, dim3((D + 15) / 16), dim3(256), 0,
+        hipLaunchKernelGGL(rms_dw_reduce_kernel, dim3((D + 7) / 8), dim3(256), 0,
                            (hipStream_t)stream, (const float*)nullptr, (int64_t)0, (int)D, dw_f32, dw);
         return check_launch("rms_dw_reduce");
     }
@@ -355,14 +378,16 @@ extern "C" int fx_rms_norm_bwd(const uint16_t* x, const uint16_t* dy, const uint
     const RowShape s = pick_bwd_shape(D);
     const int G = kNormBwdThreads / s.lpr;
     const int64_t P = bwd_blocks((N + G - 1) / G);  // every block gets a row group's worth
-    const size_t lds = (size_t)D * sizeof(float);
+    // one LDS partial row per wave while two blocks' worth fits a CU's 160 KB
+    const int per_wave = (kNormBwdThreads / 64) * D * (int)sizeof(float) <= 64 * 1024;
+    const size_t lds = (size_t)(per_wave ? kNormBwdThreads / 64 : 1) * D * sizeof(float);
 #define FX_CALL(L, V)                                                                          \
     hipLaunchKernelGGL((rms_bwd_kernel<L, V>), dim3((unsigned)P), dim3(kNormBwdThreads), lds,  \
-                       (hipStream_t)stream, x, dy, w, rstd, dx, work, N, (int)D)
+                       (hipStream_t)stream, x, dy, w, rstd, dx, work, N, (int)D, per_wave)
     FX_NORM_DISPATCH(s, FX_CALL)
 #undef FX_CALL
     if (int e = check_launch("rms_norm_bwd")) return e;
-    hipLaunchKernelGGL(rms_dw_reduce_kernel, dim3((D + 15) / 16), dim3(256), 0, (hipStream_t)stream,
+    hipLaunchKernelGGL(rms_dw_reduce_kernel, dim3((D + 7) / 8), dim3(256), 0, (hipStream_t)stream,
                        (const float*)work, P, (int)D, dw_f32, dw);
     return check_launch("rms_dw_reduce");
 }

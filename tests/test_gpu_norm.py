@@ -27,8 +27,10 @@ def test_golden(dev):
     assert torch.equal(dw.cpu(), dw32.cpu().bfloat16())
 
 
+# D <= 2048 folds the backward's per-wave dw partials through one LDS row per wave,
+# wider rows wave by wave: (64, 2048) and (64, 2056) sit either side of the switch
 @pytest.mark.parametrize("N,D", [(4, 8), (37, 64), (129, 768), (1000, 512), (300, 8192),
-                                 (5, 1032), (3, 96)])
+                                 (5, 1032), (3, 96), (64, 2048), (64, 2056)])
 def test_against_oracle(dev, N, D):
     # the reference selftest's cases (ml/fxlm/selftest.py:186-204) plus odd row shapes
     torch.manual_seed(N * 1000 + D)
