@@ -62,6 +62,15 @@ int fx_rms_norm_bwd(const uint16_t* x, const uint16_t* dy, const uint16_t* w,
                     const float* rstd, uint16_t* dx, float* dw_f32, uint16_t* dw,
                     float* work, int64_t N, int32_t D, void* stream);
 
+/* fx_rms_norm_bwd with dx += dres ((N, D) bf16, 16-byte aligned) in the same pass: the
+ * gradient of a pre-norm residual block's input, dres arriving along the residual path
+ * and dy through the norm.  No counterpart in the reference: it fuses the sum that
+ * autograd forms for ml/fxlm/model.py:69,71 (x = x + proj(attn(norm(x))), x = x + mlp(norm(x))),
+ * one bf16 add kernel per norm in the backward. */
+int fx_rms_norm_bwd_add(const uint16_t* x, const uint16_t* dy, const uint16_t* dres,
+                        const uint16_t* w, const float* rstd, uint16_t* dx, float* dw_f32,
+                        uint16_t* dw, float* work, int64_t N, int32_t D, void* stream);
+
 /* ---- softmax cross-entropy ---------------------------------------------- */
 
 /* inv_n = 1/count(target != ignore_index) (0 when the count is 0);

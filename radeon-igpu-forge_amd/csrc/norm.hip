@@ -66,11 +66,11 @@ constexpr int kNormBwdThreads = 512;
 
 template <int LPR, int NV>
 struct NormBwdRow {
-    uint4 xv[NV], dv[NV];
+    uint4 xv[NV], dv[NV], rv[NV];  // x, dy and (dres != null) the residual gradient
     float r;
     __device__ __forceinline__ void load(const uint16_t* __restrict__ x, const uint16_t* __restrict__ dy,
-                                         const float* __restrict__ rstd, int64_t row, int64_t n,
-                                         int D, int lane) {
+                                         const uint16_t* __restrict__ dres, const float* __restrict__ rstd,
+                                         int64_t row, int64_t n, int D, int lane) {
         if (row >= n) return;  // past the last row: nothing is read (uniform per row group)
         const uint16_t* xr = x + row * D;
         const uint16_t* dr = dy + row * D;
@@ -80,20 +80,23 @@ struct NormBwdRow {
             const int c = i * LPR + lane;
             xv[i] = make_uint4(0u, 0u, 0u, 0u);
             dv[i] = make_uint4(0u, 0u, 0u, 0u);
+            rv[i] = make_uint4(0u, 0u, 0u, 0u);
             if (c < V8) {
                 xv[i] = ld16_nt(xr + (int64_t)c * 8);
                 dv[i] = ld16_nt(dr + (int64_t)c * 8);
+                if (dres) rv[i] = ld16_nt(dres + row * D + (int64_t)c * 8);
             }
         }
         r = rstd[row];
     }
 };
 
-// `wv`: this lane's vectors of w (zero past D), loaded once per block
+// `wv`: this lane's vectors of w (zero past D), loaded once per block; `res`: add the
+// residual gradient row b.rv to dx
 template <int LPR, int NV>
 __device__ __forceinline__ void norm_bwd_row(const NormBwdRow<LPR, NV>& b, const uint4 (&wv)[NV],
                                              uint16_t* __restrict__ dxr, float (&acc)[NV][8], int D,
-                                             float invD, int lane) {
+                                             float invD, int lane, bool res) {
     const int V8 = D >> 3;
     float t = 0.f;
 #pragma unroll
@@ -120,6 +123,12 @@ __device__ __forceinline__ void norm_bwd_row(const NormBwdRow<LPR, NV>& b, const
             unpack8(wv[i], fw);
 #pragma unroll
             for (int j = 0; j < 8; ++j) o[j] = fmaf(b.r * fw[j], fd[j], -fx_[j] * corr);
+            if (res) {
+                float fr[8];
+                unpack8(b.rv[i], fr);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) o[j] += fr[j];
+            }
             st16_nt(dxr + (int64_t)c * 8, pack8(o));
         }
     }
@@ -136,7 +145,8 @@ template <int LPR, int NV, int NT = kNormBwdThreads, int MW = norm_bwd_min_waves
 __global__ void __launch_bounds__(NT, MW)
 rms_bwd_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ dy,
                const uint16_t* __restrict__ w, const float* __restrict__ rstd,
-               uint16_t* __restrict__ dx, float* __restrict__ part, int64_t N, int D, int per_wave) {
+               const uint16_t* __restrict__ dres, uint16_t* __restrict__ dx, float* __restrict__ part, int64_t N,
+               int D, int per_wave) {
     constexpr int G = NT / LPR;
     constexpr int NW = NT / 64;
     extern __shared__ float red[];  // NW x D floats (per_wave) or D floats
@@ -163,8 +173,8 @@ rms_bwd_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ dy,
     }
     NormBwdRow<LPR, NV> b;
     for (int64_t row = first; row < N; row += stride) {
-        b.load(x, dy, rstd, row, N, D, lane);
-        norm_bwd_row<LPR, NV>(b, wv, dx + row * D, acc, D, invD, lane);
+        b.load(x, dy, dres, rstd, row, N, D, lane);
+        norm_bwd_row<LPR, NV>(b, wv, dx + row * D, acc, D, invD, lane, dres != nullptr);
     }
 
     // row groups sharing a wave: butterfly over the group index
@@ -359,22 +369,23 @@ extern "C" int64_t fx_rms_norm_bwd_workspace(int64_t N, int32_t D) {
     return bwd_blocks(N) * (int64_t)D * (int64_t)sizeof(float);  // >= the blocks any D uses
 }
 
-extern "C" int fx_rms_norm_bwd(const uint16_t* x, const uint16_t* dy, const uint16_t* w,
-                               const float* rstd, uint16_t* dx, float* dw_f32, uint16_t* dw,
-                               float* work, int64_t N, int32_t D, void* stream) {
-    if (int e = norm_check(x, w, N, D, "fx_rms_norm_bwd")) return e;
-    FX_REQUIRE(dw_f32 != nullptr, "fx_rms_norm_bwd: null dw");
+static int rms_norm_bwd(const uint16_t* x, const uint16_t* dy, const uint16_t* dres, const uint16_t* w,
+                        const float* rstd, uint16_t* dx, float* dw_f32, uint16_t* dw, float* work, int64_t N,
+                        int32_t D, void* stream, const char* who) {
+    if (int e = norm_check(x, w, N, D, who)) return e;
+    FX_REQUIRE(dw_f32 != nullptr, "%s: null dw", who);
     FX_REQUIRE(((uintptr_t)dw_f32 & 15) == 0 && ((uintptr_t)dw & 7) == 0 && ((uintptr_t)work & 15) == 0,
-               "fx_rms_norm_bwd: dw_f32 and work must be 16-byte aligned, dw 8-byte aligned");
+               "%s: dw_f32 and work must be 16-byte aligned, dw 8-byte aligned", who);
     FX_REQUIRE(N == 0 || (dy != nullptr && rstd != nullptr && dx != nullptr),
-               "fx_rms_norm_bwd: null pointer");
+               "%s: null pointer", who);
+    FX_REQUIRE(((uintptr_t)dres & 15) == 0, "%s: dres must be 16-byte aligned", who);
     if (N == 0) {
         // dw of an empty batch is zero
         hipLaunchKernelGGL(rms_dw_reduce_kernel, dim3((D + 7) / 8), dim3(256), 0,
                            (hipStream_t)stream, (const float*)nullptr, (int64_t)0, (int)D, dw_f32, dw);
         return check_launch("rms_dw_reduce");
     }
-    FX_REQUIRE(work != nullptr, "fx_rms_norm_bwd: null workspace");
+    FX_REQUIRE(work != nullptr, "%s: null workspace", who);
     const RowShape s = pick_bwd_shape(D);
     const int G = kNormBwdThreads / s.lpr;
     const int64_t P = bwd_blocks((N + G - 1) / G);  // every block gets a row group's worth
@@ -383,11 +394,24 @@ extern "C" int fx_rms_norm_bwd(const uint16_t* x, const uint16_t* dy, const uint
     const size_t lds = (size_t)(per_wave ? kNormBwdThreads / 64 : 1) * D * sizeof(float);
 #define FX_CALL(L, V)                                                                          \
     hipLaunchKernelGGL((rms_bwd_kernel<L, V>), dim3((unsigned)P), dim3(kNormBwdThreads), lds,  \
-                       (hipStream_t)stream, x, dy, w, rstd, dx, work, N, (int)D, per_wave)
+                       (hipStream_t)stream, x, dy, w, rstd, dres, dx, work, N, (int)D, per_wave)
     FX_NORM_DISPATCH(s, FX_CALL)
 #undef FX_CALL
     if (int e = check_launch("rms_norm_bwd")) return e;
     hipLaunchKernelGGL(rms_dw_reduce_kernel, dim3((D + 7) / 8), dim3(256), 0, (hipStream_t)stream,
                        (const float*)work, P, (int)D, dw_f32, dw);
     return check_launch("rms_dw_reduce");
+}
+
+extern "C" int fx_rms_norm_bwd(const uint16_t* x, const uint16_t* dy, const uint16_t* w,
+                               const float* rstd, uint16_t* dx, float* dw_f32, uint16_t* dw,
+                               float* work, int64_t N, int32_t D, void* stream) {
+    return rms_norm_bwd(x, dy, nullptr, w, rstd, dx, dw_f32, dw, work, N, D, stream, "fx_rms_norm_bwd");
+}
+
+extern "C" int fx_rms_norm_bwd_add(const uint16_t* x, const uint16_t* dy, const uint16_t* dres,
+                                   const uint16_t* w, const float* rstd, uint16_t* dx, float* dw_f32,
+                                   uint16_t* dw, float* work, int64_t N, int32_t D, void* stream) {
+    FX_REQUIRE(N == 0 || dres != nullptr, "fx_rms_norm_bwd_add: null dres");
+    return rms_norm_bwd(x, dy, dres, w, rstd, dx, dw_f32, dw, work, N, D, stream, "fx_rms_norm_bwd_add");
 }

@@ -95,6 +95,7 @@ SIGNATURES = {
     "fx_rms_norm_fwd": (c_int32, [_P, _P, _P, _P, c_int64, c_int32, c_float, _P]),
     "fx_rms_norm_bwd_workspace": (c_int64, [c_int64, c_int32]),
     "fx_rms_norm_bwd": (c_int32, [_P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int32, _P]),
+    "fx_rms_norm_bwd_add": (c_int32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int32, _P]),
     "fx_ce_inv_nvalid": (c_int32, [_P, c_int64, c_int64, _P, c_float, _P, _P, _P]),
     "fx_ce_fwd_grad": (c_int32, [ctypes.POINTER(fxCEArgs), _P]),
     "fx_ce_loss_finalize": (c_int32, [_P, c_int64, _P, _P, _P]),

@@ -20,7 +20,7 @@ from fxgpu.fused_linear import fused_linear, linear
 
 from .attention import decode_attention, flash_attention_qkv
 from .cross_entropy import linear_cross_entropy
-from .norm import rms_norm
+from .norm import pre_norm, rms_norm
 
 
 @dataclass
@@ -63,13 +63,19 @@ class Block(nn.Module):
             return rms_norm(x, w, self.eps)
         return Fn.rms_norm(x, (x.shape[-1],), w, self.eps)
 
+    def _prenorm(self, x, w):
+        """(x, norm(x)); the fused form sums x's two gradients in the norm's backward."""
+        if self.norm_impl == "fused":
+            return pre_norm(x, w, self.eps)
+        return x, self._norm(x, w)
+
     def _lin(self, x, layer):
         if self.linear_impl == "fused":
             return linear(x, layer.weight)
         return layer(x)
 
     def _mlp(self, x):
-        h = self._norm(x, self.ln2_w)
+        x, h = self._prenorm(x, self.ln2_w)
         if self.mlp_impl == "fused":
             u = fused_linear(h, self.fc.weight, None, "gelu_tanh")
         else:
@@ -80,7 +86,7 @@ class Block(nn.Module):
         """kv: optional (k_cache, v_cache) (B, Tmax, H, Dh) that receive this block's
         keys and values at positions 0..T-1 (the prompt of a cached generation)."""
         B, T, D = x.shape
-        h = self._norm(x, self.ln1_w)
+        x, h = self._prenorm(x, self.ln1_w)
         qkv = self._lin(h, self.qkv).view(B, T, 3, self.n_head, self.head_dim)
         if kv is not None:
             kv[0][:, :T].copy_(qkv[:, :, 1])

@@ -2,7 +2,9 @@
 
 y = x * rsqrt(mean(x^2) + eps) * w.  The forward stores rstd (fp32, one per
 row); the backward produces dx and dw from a single pass over x and dy
-(fx_rms_norm_bwd).  Surface and checks follow ml/fxlm/norm.py:30-90.
+(fx_rms_norm_bwd).  Surface and checks follow ml/fxlm/norm.py:30-90.  ``pre_norm``
+returns the residual stream with the normed input so that the GPT block's two
+gradients of x are summed inside that pass (fx_rms_norm_bwd_add).
 """
 import torch
 
@@ -42,23 +44,71 @@ class _RMSNorm(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy):
         x2, w, rstd = ctx.saved_tensors
-        N, D = x2.shape
-        dy2 = dy.contiguous().view(N, D)
-        if dy2.dtype != torch.bfloat16:
-            dy2 = dy2.to(torch.bfloat16)
-        dx = torch.empty_like(x2)
-        dw32 = torch.empty(D, device=x2.device, dtype=torch.float32)
-        dw = torch.empty(D, device=x2.device, dtype=w.dtype)
-        nbytes = lib().fx_rms_norm_bwd_workspace(N, D)
-        work = torch.empty(max(1, nbytes // 4), device=x2.device, dtype=torch.float32)
-        call("fx_rms_norm_bwd", ptr(x2), ptr(dy2), ptr(w), ptr(rstd), ptr(dx), ptr(dw32),
-             ptr(dw), ptr(work), N, D, stream_of(x2))
+        dx, dw = _bwd_into(x2, dy, w, rstd)
         return dx.view(ctx.oshape), dw, None
 
 
 def rms_norm(x, weight, eps=1e-6):
     """x (..., D) bf16, weight (D,) bf16 -> y (..., D) bf16."""
     return _RMSNorm.apply(x, weight, float(eps))
+
+
+def _bwd_into(x2, dy, w, rstd, dres=None):
+    """(dx, dw) of the norm for x2 (N, D); dx += dres in the same pass when given."""
+    N, D = x2.shape
+    dy2 = dy.contiguous().view(N, D)
+    if dy2.dtype != torch.bfloat16:
+        dy2 = dy2.to(torch.bfloat16)
+    dx = torch.empty_like(x2)
+    dw32 = torch.empty(D, device=x2.device, dtype=torch.float32)
+    dw = torch.empty(D, device=x2.device, dtype=w.dtype)
+    work = torch.empty(max(1, lib().fx_rms_norm_bwd_workspace(N, D) // 4), device=x2.device,
+                       dtype=torch.float32)
+    if dres is None:
+        call("fx_rms_norm_bwd", ptr(x2), ptr(dy2), ptr(w), ptr(rstd), ptr(dx), ptr(dw32),
+             ptr(dw), ptr(work), N, D, stream_of(x2))
+    else:
+        r2 = dres.contiguous().view(N, D)
+        if r2.dtype != torch.bfloat16:
+            r2 = r2.to(torch.bfloat16)
+        call("fx_rms_norm_bwd_add", ptr(x2), ptr(dy2), ptr(r2), ptr(w), ptr(rstd), ptr(dx),
+             ptr(dw32), ptr(dw), ptr(work), N, D, stream_of(x2))
+    return dx, dw
+
+
+class _PreNorm(torch.autograd.Function):
+    """(x, rms_norm(x)) for a pre-norm residual block, whose input feeds both the norm
+    and the residual sum: the backward gets both gradients and forms
+    dx = dres + d(norm)/dx in the norm kernel's pass (fx_rms_norm_bwd_add) instead of the
+    separate add autograd would run for ml/fxlm/model.py:69,71."""
+
+    @staticmethod
+    def forward(ctx, x, w, eps):
+        D = _check(x, w)
+        N = x.numel() // D
+        x2 = x.view(N, D)
+        y = torch.empty_like(x2)
+        rstd = torch.empty(N, device=x.device, dtype=torch.float32)
+        call("fx_rms_norm_fwd", ptr(x2), ptr(w), ptr(y), ptr(rstd), N, D, float(eps),
+             stream_of(x))
+        ctx.save_for_backward(x2, w, rstd)
+        ctx.oshape = x.shape
+        ctx.set_materialize_grads(False)
+        return x, y.view(x.shape)
+
+    @staticmethod
+    def backward(ctx, dres, dy):
+        x2, w, rstd = ctx.saved_tensors
+        if dy is None:
+            return dres, None, None
+        dx, dw = _bwd_into(x2, dy, w, rstd, dres)
+        return dx.view(ctx.oshape), dw, None
+
+
+def pre_norm(x, weight, eps=1e-6):
+    """(x, rms_norm(x, weight, eps)): the residual stream and the block's normed input,
+    with the two gradients of x summed inside the norm's backward kernel."""
+    return _PreNorm.apply(x, weight, float(eps))
 
 
 def rms_norm_fwd_stats(x, weight, eps=1e-6):

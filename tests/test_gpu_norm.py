@@ -80,3 +80,57 @@ def test_cfg4_full_size(dev):
     assert float((y.float() - yr).abs().max()) <= 2e-2
     assert float((dx.float() - xr.grad).abs().max()) <= 2e-2
     assert rel_err(rstd, rr) < RTOL_NORM and rel_err(dw32, wr.grad) < RTOL_NORM
+
+
+# ---- the residual block's fused gradient sum (fx_rms_norm_bwd_add / pre_norm) ----------
+
+@pytest.mark.parametrize("N,D", [(129, 768), (300, 8192), (64, 2056), (5, 96)])
+def test_bwd_add_against_oracle(dev, N, D):
+    # dx = dres + (the norm's dx) in one pass; dw is the norm's alone, bit for bit the
+    # plain backward's
+    from fxgpu.abi import call, lib, ptr, stream_of
+    torch.manual_seed(N + D)
+    x = (torch.randn(N, D) * 3).bfloat16()
+    w = (torch.randn(D) * 0.5 + 1).bfloat16()
+    dy = torch.randn(N, D).bfloat16()
+    dres = torch.randn(N, D).bfloat16()
+    xg, wg, dyg, rg = x.to(dev), w.to(dev), dy.to(dev), dres.to(dev)
+    _y, rstd, dx0, dw0, _ = _run(xg, wg, dyg)
+    dx = torch.empty_like(xg)
+    dw32 = torch.empty(D, device=dev)
+    work = torch.empty(max(1, lib().fx_rms_norm_bwd_workspace(N, D) // 4), device=dev)
+    call("fx_rms_norm_bwd_add", ptr(xg), ptr(dyg), ptr(rg), ptr(wg), ptr(rstd), ptr(dx), ptr(dw32), None,
+         ptr(work), N, D, stream_of(xg))
+    torch.cuda.synchronize()
+    _yr, rr = onorm.rms_norm_fwd(x, w, 1e-6)
+    dxr, _dwr = onorm.rms_norm_bwd(x, dy, w, rr)
+    assert bf16_close(dx, dxr + dres.double())
+    assert torch.equal(dw32, dw0)
+    with pytest.raises(ValueError, match="null dres"):
+        call("fx_rms_norm_bwd_add", ptr(xg), ptr(dyg), None, ptr(wg), ptr(rstd), ptr(dx), ptr(dw32), None,
+             ptr(work), N, D, stream_of(xg))
+
+
+def test_pre_norm_autograd(dev):
+    # (x, norm(x)) with both outputs used: x.grad = g_x + the norm's backward of g_y, as
+    # fp32 torch autograd computes it; with only the norm used it is the plain backward
+    from fxlm.norm import pre_norm, rms_norm
+    torch.manual_seed(2)
+    x0 = torch.randn(2, 9, 768, device=dev).bfloat16()
+    w0 = (torch.randn(768, device=dev) * 0.1 + 1).bfloat16()
+    gx = torch.randn(2, 9, 768, device=dev).bfloat16()
+    gy = torch.randn(2, 9, 768, device=dev).bfloat16()
+    x, w = x0.clone().requires_grad_(), w0.clone().requires_grad_()
+    xp, y = pre_norm(x, w)
+    assert torch.equal(xp, x0) and y.shape == x0.shape
+    torch.autograd.backward([xp, y], [gx, gy])
+    xr, wr = x0.float().requires_grad_(), w0.float().requires_grad_()
+    yr = F.rms_norm(xr, (768,), wr, 1e-6)
+    torch.autograd.backward([xr, yr], [gx.float(), gy.float()])
+    assert bf16_close(x.grad, xr.grad) and bf16_close(w.grad, wr.grad)
+    x2, w2 = x0.clone().requires_grad_(), w0.clone().requires_grad_()
+    _, y2 = pre_norm(x2, w2)
+    y2.backward(gy)
+    x3, w3 = x0.clone().requires_grad_(), w0.clone().requires_grad_()
+    rms_norm(x3, w3).backward(gy)
+    assert torch.equal(x2.grad, x3.grad) and torch.equal(w2.grad, w3.grad)
