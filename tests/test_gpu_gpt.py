@@ -170,3 +170,47 @@ def test_generate_graph_equals_eager(dev):
     b = m.generate(idx, 20, temperature=0.9, top_k=40, generator=torch.Generator(device=dev).manual_seed(1),
                    graph=False)
     assert torch.equal(a, b)
+
+
+def test_checkpoint_resume_continues_identically(dev, tmp_path):
+    # train_lm's loop on a byte corpus: 3 steps, checkpoint, then 2 more steps both on the
+    # running model and on a fresh model + FlatAdamW restored from the checkpoint; the
+    # two continue bit for bit (every kernel of the step is deterministic)
+    from fxlm import train as tr
+    from fxlm.model import GPT
+    from fxlm.optim import FlatAdamW
+    raw = (b"the quick brown fox jumps over the lazy dog; " * 200)
+    tr.write_byte_tokens(raw, str(tmp_path / "corpus"), val_frac=0.05)
+    meta, vocab = tr.read_meta(str(tmp_path / "corpus_train.bin"))
+    tokens = tr.load_tokens(str(tmp_path / "corpus_train.bin"), dev)
+    cfg = _cfg()
+
+    def fresh():
+        torch.manual_seed(0)
+        m = GPT(cfg).to(dev)
+        return m, FlatAdamW(m, lr=1e-3, weight_decay=0.1, max_grad_norm=1.0, init_scale=8.0)
+
+    def run(m, opt, first, n):
+        g = torch.Generator(device=dev).manual_seed(100 + first)
+        for s in range(first, first + n):
+            x, y = tr.get_batch(tokens, 4, 64, generator=g)
+            loss = m(x, y, grad_scale=opt.scale)
+            opt.backward(loss)
+            opt.step(lr=tr.lr_at(s, 1e-3, 2, 10))
+            opt.zero_grad()
+        return float(loss.detach())
+
+    m, opt = fresh()
+    assert vocab == 256 == cfg.vocab_size
+    run(m, opt, 0, 3)
+    path = tr.save_checkpoint(str(tmp_path / "out"), opt, cfg, 3, meta=meta)
+    m2, opt2 = fresh()
+    sd = tr.load_checkpoint(path, opt2, map_location=dev)
+    assert sd["step"] == 3
+    for (n1, p1), (n2, p2) in zip(m.named_parameters(), m2.named_parameters()):
+        assert torch.equal(p1, p2), n1
+    l1, l2 = run(m, opt, 3, 2), run(m2, opt2, 3, 2)
+    assert l1 == l2
+    for (n1, p1), (n2, p2) in zip(m.named_parameters(), m2.named_parameters()):
+        assert torch.equal(p1, p2), n1
+    assert torch.equal(opt.master, opt2.master) and torch.equal(opt.v, opt2.v)
