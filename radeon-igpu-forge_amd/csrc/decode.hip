@@ -4,41 +4,57 @@
 // causal attention over the cached keys, which is what the reference's sampler
 // recomputes from the whole context for every token (ml/fxlm/sample.py:62-73).
 //
-// HBM-bound (each cached key and value is read once per step, 4 D bytes per key and
-// head), so the work is split over the keys: one wave per (sequence, head, chunk of CH
-// keys), CH = 256, 128 or 64, the largest that still gives kDecWaves waves (enough
-// loads in flight to cover HBM latency).  A key row is read by D/8 lanes, 16 bytes each, so one load instruction
-// covers 64 / (D/8) whole rows.  Pass 1 keeps all of the chunk's scores in registers
-// (log2 domain, q pre-scaled), then one max / exp pass; pass 2 accumulates P V with
-// each lane owning 8 of the D outputs; the partial (max, sum, o) of every chunk is
-// merged by the second kernel with the same rule as the forward's lse.  Chunks that
-// start at or past the sequence's length do nothing and the merge reads only the
-// chunks below it.  With a single chunk the first kernel writes the result itself.
+// HBM-bound: each cached key and value is read once per step (4 D bytes per key and
+// head).  One workgroup per (sequence, head) -- or per (sequence, head, segment of the
+// keys) when there are fewer (sequence, head) pairs than half the CUs -- of up to 16
+// waves.  Wave w streams sub-chunks w, w + nw, ... of CH keys (64 at D = 64, 32 at
+// D = 128); a key row is read by D/8 lanes, 16 bytes each, and a sub-chunk's K and V
+// rows are all loaded at once (one memory round trip per sub-chunk).  Every lane keeps
+// an online softmax (max, sum, o for its 8 of the D outputs) over the keys of its key
+// group; the key groups of a wave combine with lane exchanges at the end, the waves
+// through LDS in wave order.  With one segment the workgroup writes the output; with
+// several it writes (max, sum, o) per segment and a second kernel merges them by the
+// forward's lse rule, reading only the segments below the sequence's length.
 #include <math.h>
 
 #include "fx_device.h"
 
 namespace fx {
 
-constexpr int kDecBatch = 8;      // key loads in flight per lane
-constexpr int kDecWaves = 2048;   // grid size the chunk choice aims for
+constexpr int kDecMaxWaves = 16;
 constexpr float kDecNegInf = -__builtin_huge_valf();
 
+// (m, l, o[8]) <- (m, l, o) merged with (m2, l2, o2): max-rescaled sums in the exp2 domain
+__device__ __forceinline__ void dec_merge(float& m, float& l, float (&o)[8], float m2, float l2,
+                                          const float (&o2)[8]) {
+    const float M = fmaxf(m, m2);
+    const float mu = M == kDecNegInf ? 0.f : M;
+    const float f1 = exp2_fast(m - mu), f2 = exp2_fast(m2 - mu);  // 0 for an empty side
+    l = l * f1 + l2 * f2;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = o[e] * f1 + o2[e] * f2;
+    m = M;
+}
+
 template <int D, int CH>
-__global__ void __launch_bounds__(64) attn_decode_kernel(fxAttnDecodeArgs a, int nchunks) {
+__global__ void __launch_bounds__(64 * kDecMaxWaves) attn_decode_kernel(fxAttnDecodeArgs a, int nseg,
+                                                                        int seglen) {
     constexpr int LPK = D / 8;       // lanes per key row
     constexpr int KPI = 64 / LPK;    // key rows per load instruction
-    constexpr int NS = CH / KPI;     // load steps per chunk
-    static_assert(NS % kDecBatch == 0, "chunk");
-    const int lane = threadIdx.x;
+    constexpr int NS = CH / KPI;     // load steps per sub-chunk
+    __shared__ float red[kDecMaxWaves][D + 2];
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nw = blockDim.x >> 6;
     const int kg = lane / LPK, dl = lane % LPK;  // key group and 8-element slice of D
-    const int c = blockIdx.x % nchunks;
-    const int bh = blockIdx.x / nchunks;
+    const int seg = blockIdx.x % nseg;
+    const int bh = blockIdx.x / nseg;
     const int b = bh / a.H, h = bh - b * a.H;
     int len = a.lens[b];
     len = len < 0 ? 0 : (len > a.Tmax ? a.Tmax : len);
-    const int j0 = c * CH;
-    if (nchunks > 1 && j0 >= len) return;  // the merge skips this chunk
+    const int k0 = seg * seglen;
+    if (nseg > 1 && k0 >= len) return;  // the merge skips this segment (uniform per block)
+    const int k1 = min(k0 + seglen, len);
 
     float qf[8];
     {
@@ -50,100 +66,112 @@ __global__ void __launch_bounds__(64) attn_decode_kernel(fxAttnDecodeArgs a, int
     const uint16_t* kb = a.k + b * a.ksb + h * a.ksh + dl * 8;
     const uint16_t* vb = a.v + b * a.vsb + h * a.vsh + dl * 8;
 
-    // pass 1: scores of keys j0 + s KPI + kg, s < NS
-    float sc[NS];
-    float m = kDecNegInf;
+    float m = kDecNegInf, l = 0.f;
+    float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int j0 = k0 + w * CH; j0 < k1; j0 += nw * CH) {
+        uint4 kv[NS], vv[NS];
 #pragma unroll
-    for (int s0 = 0; s0 < NS; s0 += kDecBatch) {
-        uint4 kv[kDecBatch];
-#pragma unroll
-        for (int u = 0; u < kDecBatch; ++u) {
-            const int j = j0 + (s0 + u) * KPI + kg;
-            kv[u] = j < len ? ld16(kb + (int64_t)j * a.kst) : make_uint4(0u, 0u, 0u, 0u);
+        for (int s = 0; s < NS; ++s) {
+            const int j = j0 + s * KPI + kg;
+            const bool ok = j < k1;
+            kv[s] = ok ? ld16(kb + (int64_t)j * a.kst) : make_uint4(0u, 0u, 0u, 0u);
+            vv[s] = ok ? ld16(vb + (int64_t)j * a.vst) : make_uint4(0u, 0u, 0u, 0u);
         }
+        float sc[NS];
+        float mc = kDecNegInf;
 #pragma unroll
-        for (int u = 0; u < kDecBatch; ++u) {
+        for (int s = 0; s < NS; ++s) {
             float kf[8];
-            unpack8(kv[u], kf);
+            unpack8(kv[s], kf);
             float t = 0.f;
 #pragma unroll
             for (int e = 0; e < 8; ++e) t = fmaf(qf[e], kf[e], t);
             t = group_sum<LPK>(t);
-            const int j = j0 + (s0 + u) * KPI + kg;
-            sc[s0 + u] = j < len ? t : kDecNegInf;
-            m = fmaxf(m, sc[s0 + u]);
+            sc[s] = (j0 + s * KPI + kg) < k1 ? t : kDecNegInf;
+            mc = fmaxf(mc, sc[s]);
         }
-    }
-    // chunk max over the key groups (lanes with equal dl hold equal values already)
+        // online softmax over this lane's key group (lanes of one group hold equal scores)
+        const float mn = fmaxf(m, mc);
+        const float mu = mn == kDecNegInf ? 0.f : mn;
+        const float alpha = exp2_fast(m - mu);
+        l *= alpha;
 #pragma unroll
-    for (int off = LPK; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    const float mu = m == kDecNegInf ? 0.f : m;
-    float l = 0.f;
+        for (int e = 0; e < 8; ++e) o[e] *= alpha;
+        m = mn;
 #pragma unroll
-    for (int s = 0; s < NS; ++s) {
-        sc[s] = exp2_fast(sc[s] - mu);  // exp2(-inf) = 0
-        l += sc[s];
-    }
-    // pass 2: o = sum_j p_j v_j over this lane's key group, 8 outputs per lane
-    float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s0 = 0; s0 < NS; s0 += kDecBatch) {
-        uint4 vv[kDecBatch];
-#pragma unroll
-        for (int u = 0; u < kDecBatch; ++u) {
-            const int j = j0 + (s0 + u) * KPI + kg;
-            vv[u] = j < len ? ld16(vb + (int64_t)j * a.vst) : make_uint4(0u, 0u, 0u, 0u);
-        }
-#pragma unroll
-        for (int u = 0; u < kDecBatch; ++u) {
+        for (int s = 0; s < NS; ++s) {
+            const float p = exp2_fast(sc[s] - mu);  // exp2(-inf) = 0
+            l += p;
             float vf[8];
-            unpack8(vv[u], vf);
+            unpack8(vv[s], vf);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) o[e] = fmaf(sc[s0 + u], vf[e], o[e]);
+            for (int e = 0; e < 8; ++e) o[e] = fmaf(p, vf[e], o[e]);
         }
     }
-    // sum over the key groups: every lane of slice dl ends with the chunk's o slice
+    // key groups of the wave: lanes kg and kg ^ (off / LPK) merge, every lane of slice dl
+    // ends with the wave's (m, l, o)
 #pragma unroll
     for (int off = LPK; off < 64; off <<= 1) {
-        l += __shfl_xor(l, off, 64);
+        float o2[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] += __shfl_xor(o[e], off, 64);
+        for (int e = 0; e < 8; ++e) o2[e] = __shfl_xor(o[e], off, 64);
+        const float m2 = __shfl_xor(m, off, 64), l2 = __shfl_xor(l, off, 64);
+        dec_merge(m, l, o, m2, l2, o2);
     }
-    if (kg != 0) return;
-    if (nchunks == 1) {  // the only chunk: final output
-        const float inv = l > 0.f ? 1.f / l : 0.f;
+    if (kg == 0) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] *= inv;
-        st16(a.o + (int64_t)bh * D + dl * 8, pack8(o));
-        if (a.lse && dl == 0) a.lse[bh] = l > 0.f ? (m + log2_fast(l)) * kLn2 : kDecNegInf;
-        return;
+        for (int e = 0; e < 8; ++e) red[w][dl * 8 + e] = o[e];
+        if (dl == 0) {
+            red[w][D] = m;
+            red[w][D + 1] = l;
+        }
     }
-    // partial of chunk c: (max, sum, o[D]) at work + (bh * nchunks + c) * (D + 4)
-    float* w = a.work + ((int64_t)bh * nchunks + c) * (D + 4);
-    *reinterpret_cast<float4*>(w + 4 + dl * 8) = make_float4(o[0], o[1], o[2], o[3]);
-    *reinterpret_cast<float4*>(w + 8 + dl * 8) = make_float4(o[4], o[5], o[6], o[7]);
-    if (dl == 0) *reinterpret_cast<float2*>(w) = make_float2(m, l);
+    __syncthreads();
+    // waves in order: one thread per output dimension
+    for (int t = threadIdx.x; t < D; t += blockDim.x) {
+        float M = kDecNegInf;
+        for (int v = 0; v < nw; ++v) M = fmaxf(M, red[v][D]);
+        const float mu = M == kDecNegInf ? 0.f : M;
+        float L = 0.f, O = 0.f;
+        for (int v = 0; v < nw; ++v) {
+            const float f = exp2_fast(red[v][D] - mu);
+            L += red[v][D + 1] * f;
+            O += red[v][t] * f;
+        }
+        if (nseg == 1) {
+            a.o[(int64_t)bh * D + t] = f32_to_bf16(L > 0.f ? O / L : 0.f);
+            if (a.lse && t == 0) a.lse[bh] = L > 0.f ? (M + log2_fast(L)) * kLn2 : kDecNegInf;
+        } else {
+            // segment partial (max, sum, o[D]) at work + (bh * nseg + seg) * (D + 4)
+            float* pw = a.work + ((int64_t)bh * nseg + seg) * (D + 4);
+            pw[4 + t] = O;
+            if (t == 0) {
+                pw[0] = M;
+                pw[1] = L;
+            }
+        }
+    }
 }
 
-// merge the chunk partials of one (sequence, head) per wave, over the chunks that hold
-// keys (c CH < len): M = max m_c, L = sum l_c 2^(m_c - M), o = sum o_c 2^(m_c - M) / L,
-// lse = (M + log2 L) ln 2
-template <int D, int CH>
-__global__ void __launch_bounds__(64) attn_decode_merge_kernel(fxAttnDecodeArgs a, int nchunks) {
+// merge the segment partials of one (sequence, head) per wave, over the segments that
+// hold keys (s * seglen < len): M = max m_s, L = sum l_s 2^(m_s - M),
+// o = sum o_s 2^(m_s - M) / L, lse = (M + log2 L) ln 2
+template <int D>
+__global__ void __launch_bounds__(64) attn_decode_merge_kernel(fxAttnDecodeArgs a, int nseg, int seglen) {
     constexpr int EPL = D / 64;  // outputs per lane
     const int lane = threadIdx.x;
     const int bh = blockIdx.x;
     int len = a.lens[bh / a.H];
     len = len < 0 ? 0 : (len > a.Tmax ? a.Tmax : len);
-    const int nc = (len + CH - 1) / CH;  // <= nchunks
-    const float* w = a.work + (int64_t)bh * nchunks * (D + 4);
+    const int ns = (len + seglen - 1) / seglen;  // <= nseg
+    const float* w = a.work + (int64_t)bh * nseg * (D + 4);
     float M = kDecNegInf;
-    for (int c = 0; c < nc; ++c) M = fmaxf(M, w[(int64_t)c * (D + 4)]);
+    for (int c = 0; c < ns; ++c) M = fmaxf(M, w[(int64_t)c * (D + 4)]);
     const float mu = M == kDecNegInf ? 0.f : M;
     float L = 0.f, o[EPL];
 #pragma unroll
     for (int e = 0; e < EPL; ++e) o[e] = 0.f;
-    for (int c = 0; c < nc; ++c) {
+    for (int c = 0; c < ns; ++c) {
         const float* p = w + (int64_t)c * (D + 4);
         const float f = exp2_fast(p[0] - mu);
         L += p[1] * f;
@@ -157,24 +185,39 @@ __global__ void __launch_bounds__(64) attn_decode_merge_kernel(fxAttnDecodeArgs 
     if (a.lse && lane == 0) a.lse[bh] = L > 0.f ? (M + log2_fast(L)) * kLn2 : kDecNegInf;
 }
 
-// keys per chunk: the largest of 256, 128, 64 whose grid reaches kDecWaves waves
-static int decode_chunk(int32_t B, int32_t H, int32_t Tmax) {
-    for (int ch = 256; ch > 64; ch >>= 1)
-        if ((int64_t)B * H * ((Tmax + ch - 1) / ch) >= kDecWaves) return ch;
-    return 64;
-}
-static int decode_chunks(int32_t B, int32_t H, int32_t Tmax) {
-    const int ch = decode_chunk(B, H, Tmax);
-    return (Tmax + ch - 1) / ch;
+// Launch shape: segments, waves per workgroup and keys per segment.  One segment per
+// (sequence, head) once those fill half the CUs; else enough segments for about one
+// workgroup per CU, each at least two sub-chunks long.
+struct DecodeShape {
+    int nseg, nw, seglen;
+};
+
+static DecodeShape decode_shape(int32_t B, int32_t H, int32_t Tmax, int32_t D) {
+    const int ch = D == 64 ? 64 : 32;
+    const int64_t nbh = (int64_t)B * H;
+    const int nsub = (Tmax + ch - 1) / ch;
+    const int64_t cus = device_cus();
+    int nseg = 1;
+    if (nbh < cus / 2) {
+        const int64_t want = (cus + nbh - 1) / nbh;
+        const int64_t most = (nsub + 1) / 2;
+        nseg = (int)(want < most ? want : most);
+        if (nseg < 1) nseg = 1;
+    }
+    const int per = (nsub + nseg - 1) / nseg;  // sub-chunks per segment
+    nseg = (nsub + per - 1) / per;             // no empty trailing segment
+    return {nseg, per < kDecMaxWaves ? per : kDecMaxWaves, per * ch};
 }
 
-template <int D, int CH>
-static int decode_launch(const fxAttnDecodeArgs& a, int nc, hipStream_t st) {
+template <int D>
+static int decode_launch(const fxAttnDecodeArgs& a, const DecodeShape& s, hipStream_t st) {
+    constexpr int CH = D == 64 ? 64 : 32;
     const unsigned nbh = (unsigned)(a.B * a.H);
-    hipLaunchKernelGGL((attn_decode_kernel<D, CH>), dim3(nbh * nc), dim3(64), 0, st, a, nc);
+    hipLaunchKernelGGL((attn_decode_kernel<D, CH>), dim3(nbh * s.nseg), dim3(64 * s.nw), 0, st, a, s.nseg,
+                       s.seglen);
     if (int e = check_launch("attn_decode")) return e;
-    if (nc == 1) return 0;
-    hipLaunchKernelGGL((attn_decode_merge_kernel<D, CH>), dim3(nbh), dim3(64), 0, st, a, nc);
+    if (s.nseg == 1) return 0;
+    hipLaunchKernelGGL((attn_decode_merge_kernel<D>), dim3(nbh), dim3(64), 0, st, a, s.nseg, s.seglen);
     return check_launch("attn_decode_merge");
 }
 
@@ -183,9 +226,9 @@ static int decode_launch(const fxAttnDecodeArgs& a, int nc, hipStream_t st) {
 using namespace fx;
 
 extern "C" int64_t fx_attn_decode_workspace(int32_t B, int32_t H, int32_t Tmax, int32_t D) {
-    if (B <= 0 || H <= 0 || Tmax <= 0 || D <= 0) return 0;
-    const int nc = decode_chunks(B, H, Tmax);
-    return nc > 1 ? (int64_t)B * H * nc * (D + 4) * (int64_t)sizeof(float) : 0;
+    if (B <= 0 || H <= 0 || Tmax <= 0 || (D != 64 && D != 128)) return 0;
+    const DecodeShape s = decode_shape(B, H, Tmax, D);
+    return s.nseg > 1 ? (int64_t)B * H * s.nseg * (D + 4) * (int64_t)sizeof(float) : 0;
 }
 
 extern "C" int fx_attn_decode(const fxAttnDecodeArgs* args, void* stream) {
@@ -194,7 +237,7 @@ extern "C" int fx_attn_decode(const fxAttnDecodeArgs* args, void* stream) {
     FX_REQUIRE(a.D == 64 || a.D == 128, "fx_attn_decode: head_dim %d not supported (64 or 128)", a.D);
     FX_REQUIRE(a.B >= 1 && a.H >= 1 && a.Tmax >= 1, "fx_attn_decode: bad shape B=%d H=%d Tmax=%d", a.B, a.H,
                a.Tmax);
-    FX_REQUIRE((int64_t)a.B * a.H * ((a.Tmax + 63) / 64) < 0x7fffffffLL, "fx_attn_decode: grid too large");
+    FX_REQUIRE((int64_t)a.B * a.H * ((a.Tmax + 31) / 32) < 0x7fffffffLL, "fx_attn_decode: grid too large");
     FX_REQUIRE(a.q && a.k && a.v && a.lens && a.o, "fx_attn_decode: null pointer");
     FX_REQUIRE(a.scale > 0.f && a.scale < __builtin_huge_valf(), "fx_attn_decode: scale %g must be positive and finite",
                (double)a.scale);
@@ -202,15 +245,8 @@ extern "C" int fx_attn_decode(const fxAttnDecodeArgs* args, void* stream) {
     for (int64_t x : s) FX_REQUIRE(x % 8 == 0, "fx_attn_decode: strides must be multiples of 8 elements");
     FX_REQUIRE((((uintptr_t)a.q | (uintptr_t)a.k | (uintptr_t)a.v | (uintptr_t)a.o | (uintptr_t)a.work) & 15) == 0,
                "fx_attn_decode: q, k, v, o and work must be 16-byte aligned");
-    const int ch = decode_chunk(a.B, a.H, a.Tmax);
-    const int nc = (a.Tmax + ch - 1) / ch;
-    FX_REQUIRE(nc == 1 || a.work != nullptr, "fx_attn_decode: null workspace (%d chunks)", nc);
+    const DecodeShape sh = decode_shape(a.B, a.H, a.Tmax, a.D);
+    FX_REQUIRE(sh.nseg == 1 || a.work != nullptr, "fx_attn_decode: null workspace (%d segments)", sh.nseg);
     hipStream_t st = (hipStream_t)stream;
-    if (a.D == 64)
-        return ch == 256 ? decode_launch<64, 256>(a, nc, st)
-             : ch == 128 ? decode_launch<64, 128>(a, nc, st)
-                         : decode_launch<64, 64>(a, nc, st);
-    return ch == 256 ? decode_launch<128, 256>(a, nc, st)
-         : ch == 128 ? decode_launch<128, 128>(a, nc, st)
-                     : decode_launch<128, 64>(a, nc, st);
+    return a.D == 64 ? decode_launch<64>(a, sh, st) : decode_launch<128>(a, sh, st);
 }

@@ -111,16 +111,18 @@ def test_cfg2_full_size(dev):
 
 # ---- decode attention (KV cache) ------------------------------------------------------
 
-# the chunk is the largest of 256 / 128 / 64 keys whose grid B H ceil(Tmax / chunk)
-# reaches 2048 waves; chunks at or past a sequence's length are skipped
+# one workgroup per (sequence, head) of up to 16 waves streaming 64-key sub-chunks
+# (32 at D = 128) once B H >= half the CUs; fewer pairs split the keys into segments
+# merged by a second kernel, and segments at or past a sequence's length are skipped
 @pytest.mark.parametrize("B,Tmax,H,D,lens", [
-    (2, 1024, 12, 64, [1024, 513]),        # sixteen 64-key chunks, ragged second sequence
-    (3, 300, 4, 128, [1, 64, 65]),         # chunk boundaries at D = 128
-    (1, 64, 2, 64, [50]),                  # one chunk: written without the merge
+    (2, 1024, 12, 64, [1024, 513]),        # 8 segments of 2 waves, ragged second sequence
+    (3, 300, 4, 128, [1, 64, 65]),         # segment boundaries at D = 128
+    (1, 64, 2, 64, [50]),                  # one wave, one segment: no merge
     (4, 2048, 8, 64, [2048, 1, 1500, 0]),  # an empty sequence
-    (16, 1024, 16, 64, [1024 - 61 * i for i in range(16)]),   # 128-key chunks
-    (32, 300, 64, 64, [300 - 9 * i for i in range(32)]),      # 256-key chunks
-    (16, 256, 128, 128, [256 - 16 * i for i in range(16)]),   # one 256-key chunk, D = 128
+    (16, 1024, 16, 64, [1024 - 61 * i for i in range(16)]),   # one segment, 16 waves
+    (32, 300, 64, 64, [300 - 9 * i for i in range(32)]),      # 5 waves, ragged tails
+    (16, 256, 128, 128, [256 - 16 * i for i in range(16)]),   # one segment at D = 128
+    (8, 2048, 16, 64, [2048 - 97 * i for i in range(8)]),     # waves loop over 2 sub-chunks
 ])
 def test_decode_against_oracle(dev, B, Tmax, H, D, lens):
     from fxlm.attention import decode_attention

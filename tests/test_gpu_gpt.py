@@ -214,3 +214,40 @@ def test_checkpoint_resume_continues_identically(dev, tmp_path):
     for (n1, p1), (n2, p2) in zip(m.named_parameters(), m2.named_parameters()):
         assert torch.equal(p1, p2), n1
     assert torch.equal(opt.master, opt2.master) and torch.equal(opt.v, opt2.v)
+
+
+def test_head_dim_128_model(dev):
+    # 128-wide heads through the GPT: the D = 128 attention forward / backward against the
+    # SDPA path, and cached decoding against the full forward
+    from fxlm.model import GPT, GPTConfig
+    torch.manual_seed(0)
+    kw = dict(vocab_size=256, seq_len=64, n_layer=2, n_head=2, d_model=256)
+    torch_cfg = dict(attn_impl="sdpa", norm_impl="torch", ce_impl="torch", mlp_impl="torch", linear_impl="torch")
+    m_f = GPT(GPTConfig(**kw)).to(dev)
+    m_t = GPT(GPTConfig(**kw, **torch_cfg))
+    m_r = GPT(GPTConfig(**kw, **torch_cfg))
+    m_t.load_state_dict(m_f.state_dict())
+    m_r.load_state_dict(m_f.state_dict())
+    m_f.bfloat16()
+    m_t.bfloat16()
+    idx = torch.randint(0, 256, (4, 64))
+    tgt = torch.randint(0, 256, (4, 64))
+    l_f = m_f(idx.to(dev), tgt.to(dev), grad_scale=1.0)
+    l_t, l_r = m_t(idx, tgt), m_r(idx, tgt)
+    for l in (l_f, l_t, l_r):
+        l.backward()
+    # the reference's rule, as in test_fused_vs_torch_paths: error <= 2 x torch bf16's + 1e-3
+    assert abs(float(l_f) - float(l_r)) <= 2 * abs(float(l_t) - float(l_r)) + 1e-3
+    rp, tp = dict(m_r.named_parameters()), dict(m_t.named_parameters())
+    for name, p in m_f.named_parameters():
+        ef = float((p.grad.float().cpu() - rp[name].grad).abs().max())
+        et = float((tp[name].grad.float() - rp[name].grad).abs().max())
+        assert ef <= 2 * et + 1e-3, name
+    m_f.eval()
+    x = torch.randint(0, 256, (2, 40), device=dev)
+    cache = m_f.init_cache(2, 40)
+    with torch.no_grad():
+        got = [m_f.prefill(x[:, :30], cache)] + [m_f.decode_step(x[:, t], cache, t) for t in range(30, 39)]
+        ref = [m_f(x[:, :t + 1])[:, -1, :].float() for t in range(29, 39)]
+    for a, r in zip(got, ref):
+        assert float((a - r).abs().max()) <= 3e-2 * max(1.0, float(r.abs().max()))
