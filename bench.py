@@ -1,10 +1,10 @@
 """Benchmark: the fxlm GPT 12L-d768 training step on one MI355X, plus the hot-path kernels.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-    python bench.py --only {attention,ce,norm,adamw,linear,step,copy}   (profiling runs)
+    python bench.py --only {attention,ce,norm,adamw,linear,step,copy,decode}   (profiling runs)
     python bench.py --pmc-summary FETCH.csv WRITE.csv COPY_FETCH.csv COPY_WRITE.csv
 
-Workload: GPT with 12 layers, d_model 768, 12 heads of
+Workload (the headline metric's fifth config): GPT with 12 layers, d_model 768, 12 heads of
 64, RMSNorm (fused), fused-linear GELU MLP 3072, vocab 50304, causal S=1024,
 batch 16, tied head; all bf16 with FlatAdamW (fp32 master, lr 6e-4, betas
 (0.9, 0.95), eps 1e-8, wd 0.1, clip 1.0).  Tokens are uniform random from a
@@ -408,7 +408,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): the fxlm hot path is "
-              "single-GPU; see DESIGN.md for how it would shard.", file=sys.stderr)
+              "measured on a single GPU; multi-GPU sharding is designed, not built.", file=sys.stderr)
         sys.exit(2)
     import torch
     from fxgpu.abi import lib

@@ -24,7 +24,7 @@ extern "C" {
 #endif
 
 #define FX_EINVAL (-1)
-#define FX_ABI_VERSION 1
+#define FX_ABI_VERSION 2
 
 /* ---- library ------------------------------------------------------------ */
 
@@ -228,13 +228,20 @@ typedef struct fxAttnDecodeArgs {
     int64_t qsb, qsh, ksb, kst, ksh, vsb, vst, vsh;
     int32_t B, H, Tmax, D;    /* D in {64, 128} */
     float scale;              /* > 0 and finite */
+    /* Optional (both or neither): the new token's key and value, knew[b*knb + h*knh + d]
+     * (vnew likewise).  Key lens[b] - 1 is then taken from them and written into the
+     * caches at that row in the same pass (no separate cache write).  NULL: every key
+     * comes from the caches. */
+    const uint16_t* knew;
+    const uint16_t* vnew;
+    int64_t knb, knh, vnb, vnh;
 } fxAttnDecodeArgs;
 
 int64_t fx_attn_decode_workspace(int32_t B, int32_t H, int32_t Tmax, int32_t D);
 
 /* No counterpart in the reference, whose sampler re-runs the whole context through the
- * model for every new token (ml/fxlm/sample.py:62-73); this is the KV-cache step that
- * SURVEY ranks next for the inference path (bf16 in and out, fp32 softmax).  All
+ * model for every new token (ml/fxlm/sample.py:62-73); this is the attention of a
+ * KV-cache decoding step (bf16 in and out, fp32 softmax).  All
  * vectors 16-byte aligned, strides multiples of 8 elements. */
 int fx_attn_decode(const fxAttnDecodeArgs* args, void* stream);
 

@@ -14,7 +14,9 @@
 // group; the key groups of a wave combine with lane exchanges at the end, the waves
 // through LDS in wave order.  With one segment the workgroup writes the output; with
 // several it writes (max, sum, o) per segment and a second kernel merges them by the
-// forward's lse rule, reading only the segments below the sequence's length.
+// forward's lse rule, reading only the segments below the sequence's length.  Given
+// the new token's key and value (knew / vnew), the wave that reaches key len - 1 reads
+// it from there and writes it into the caches: the step needs no separate cache write.
 #include <math.h>
 
 #include "fx_device.h"
@@ -65,6 +67,11 @@ __global__ void __launch_bounds__(64 * kDecMaxWaves) attn_decode_kernel(fxAttnDe
     }
     const uint16_t* kb = a.k + b * a.ksb + h * a.ksh + dl * 8;
     const uint16_t* vb = a.v + b * a.vsb + h * a.vsh + dl * 8;
+    // the new token's key / value (row len - 1) when given: read from knew / vnew and
+    // stored into the caches by the lanes that load it (no other lane reads that row)
+    const int jnew = a.knew ? len - 1 : -1;
+    const uint16_t* kn = a.knew ? a.knew + b * a.knb + h * a.knh + dl * 8 : nullptr;
+    const uint16_t* vn = a.vnew ? a.vnew + b * a.vnb + h * a.vnh + dl * 8 : nullptr;
 
     float m = kDecNegInf, l = 0.f;
     float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -74,8 +81,15 @@ __global__ void __launch_bounds__(64 * kDecMaxWaves) attn_decode_kernel(fxAttnDe
         for (int s = 0; s < NS; ++s) {
             const int j = j0 + s * KPI + kg;
             const bool ok = j < k1;
-            kv[s] = ok ? ld16(kb + (int64_t)j * a.kst) : make_uint4(0u, 0u, 0u, 0u);
-            vv[s] = ok ? ld16(vb + (int64_t)j * a.vst) : make_uint4(0u, 0u, 0u, 0u);
+            if (j == jnew) {
+                kv[s] = ld16(kn);
+                vv[s] = ld16(vn);
+                st16(const_cast<uint16_t*>(kb) + (int64_t)j * a.kst, kv[s]);
+                st16(const_cast<uint16_t*>(vb) + (int64_t)j * a.vst, vv[s]);
+            } else {
+                kv[s] = ok ? ld16(kb + (int64_t)j * a.kst) : make_uint4(0u, 0u, 0u, 0u);
+                vv[s] = ok ? ld16(vb + (int64_t)j * a.vst) : make_uint4(0u, 0u, 0u, 0u);
+            }
         }
         float sc[NS];
         float mc = kDecNegInf;
@@ -241,10 +255,12 @@ extern "C" int fx_attn_decode(const fxAttnDecodeArgs* args, void* stream) {
     FX_REQUIRE(a.q && a.k && a.v && a.lens && a.o, "fx_attn_decode: null pointer");
     FX_REQUIRE(a.scale > 0.f && a.scale < __builtin_huge_valf(), "fx_attn_decode: scale %g must be positive and finite",
                (double)a.scale);
-    const int64_t s[] = {a.qsb, a.qsh, a.ksb, a.kst, a.ksh, a.vsb, a.vst, a.vsh};
+    const int64_t s[] = {a.qsb, a.qsh, a.ksb, a.kst, a.ksh, a.vsb, a.vst, a.vsh, a.knb, a.knh, a.vnb, a.vnh};
     for (int64_t x : s) FX_REQUIRE(x % 8 == 0, "fx_attn_decode: strides must be multiples of 8 elements");
-    FX_REQUIRE((((uintptr_t)a.q | (uintptr_t)a.k | (uintptr_t)a.v | (uintptr_t)a.o | (uintptr_t)a.work) & 15) == 0,
-               "fx_attn_decode: q, k, v, o and work must be 16-byte aligned");
+    FX_REQUIRE((a.knew == nullptr) == (a.vnew == nullptr), "fx_attn_decode: knew and vnew go together");
+    FX_REQUIRE((((uintptr_t)a.q | (uintptr_t)a.k | (uintptr_t)a.v | (uintptr_t)a.o | (uintptr_t)a.work |
+                 (uintptr_t)a.knew | (uintptr_t)a.vnew) & 15) == 0,
+               "fx_attn_decode: q, k, v, o, work, knew and vnew must be 16-byte aligned");
     const DecodeShape sh = decode_shape(a.B, a.H, a.Tmax, a.D);
     FX_REQUIRE(sh.nseg == 1 || a.work != nullptr, "fx_attn_decode: null workspace (%d segments)", sh.nseg);
     hipStream_t st = (hipStream_t)stream;

@@ -14,7 +14,7 @@ LIB_PATH = os.path.join(_PKG_ROOT, "libfxforge.so")
 HEADER_PATH = os.path.join(os.path.dirname(_PKG_ROOT), "include", "fx_abi.h")
 
 FX_EINVAL = -1
-FX_ABI_VERSION = 1
+FX_ABI_VERSION = 2
 MAX_TENSORS = 64
 
 c_void_p = ctypes.c_void_p
@@ -83,6 +83,8 @@ class fxAttnDecodeArgs(ctypes.Structure):
         ("vsb", c_int64), ("vst", c_int64), ("vsh", c_int64),
         ("B", c_int32), ("H", c_int32), ("Tmax", c_int32), ("D", c_int32),
         ("scale", c_float),
+        ("knew", c_void_p), ("vnew", c_void_p),
+        ("knb", c_int64), ("knh", c_int64), ("vnb", c_int64), ("vnh", c_int64),
     ]
 
 

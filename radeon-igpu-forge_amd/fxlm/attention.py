@@ -153,13 +153,15 @@ def attention_fwd_raw(q, k, v, causal=True, scale=None):
     return _fwd(q, k, v, causal, float(scale))
 
 
-def decode_attention(q, k_cache, v_cache, lens, scale=None, return_lse=False):
+def decode_attention(q, k_cache, v_cache, lens, scale=None, return_lse=False, k_new=None, v_new=None):
     """One new query per (sequence, head) against a KV cache (inference).
 
     q (B, H, Dh) bf16; k_cache, v_cache (B, Tmax, H, Dh) bf16 (unit stride along Dh,
     b/t/h strides multiples of 8); lens (B,) int32 cuda: the number of valid cached keys
     of each sequence (the new token's own key included).  Returns o (B, H, Dh) bf16 =
     softmax(scale q K[:lens]^T) V[:lens], and the fp32 logsumexp (B, H) if asked.
+    k_new, v_new (B, H, Dh), both or neither: the new token's key and value; the kernel
+    uses them as key lens[b] - 1 and writes them into the caches at that row.
     """
     if q.dim() != 3 or k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
         raise ValueError(f"q (B,H,Dh) and caches (B,Tmax,H,Dh): {tuple(q.shape)} "
@@ -179,6 +181,18 @@ def decode_attention(q, k_cache, v_cache, lens, scale=None, return_lse=False):
                              "elements and the base 16-byte aligned")
     if lens.dtype != torch.int32 or not lens.is_cuda or lens.shape != (B,):
         raise TypeError(f"lens must be an int32 cuda tensor of shape ({B},)")
+    if (k_new is None) != (v_new is None):
+        raise ValueError("k_new and v_new go together")
+    for nm, t in (("k_new", k_new), ("v_new", v_new)):
+        if t is None:
+            continue
+        if tuple(t.shape) != (B, H, Dh):
+            raise ValueError(f"{nm} {tuple(t.shape)} must be (B, H, Dh) = {(B, H, Dh)}")
+        if t.dtype != torch.bfloat16 or not t.is_cuda:
+            raise TypeError(f"{nm} must be a bfloat16 cuda tensor")
+        if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:-1]) or t.data_ptr() % 16:
+            raise ValueError(f"{nm}: last dim must be contiguous, other strides multiples of 8 "
+                             "elements and the base 16-byte aligned")
     if scale is None:
         scale = 1.0 / math.sqrt(Dh)
     lens = lens.contiguous()
@@ -195,5 +209,9 @@ def decode_attention(q, k_cache, v_cache, lens, scale=None, return_lse=False):
     a.vsb, a.vst, a.vsh = _strides3(v_cache)
     a.B, a.H, a.Tmax, a.D = B, H, Tmax, Dh
     a.scale = float(scale)
+    if k_new is not None:
+        a.knew, a.vnew = k_new.data_ptr(), v_new.data_ptr()
+        a.knb, a.knh = k_new.stride(0), k_new.stride(1)
+        a.vnb, a.vnh = v_new.stride(0), v_new.stride(1)
     call("fx_attn_decode", ctypes.byref(a), stream_of(q))
     return (o, lse) if return_lse else o

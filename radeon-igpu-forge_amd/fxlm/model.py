@@ -101,16 +101,16 @@ class Block(nn.Module):
         return self._mlp(x)
 
     def step(self, x, kv, pos, lens):
-        """One new token per sequence: x (B, 1, D) at the position held by the device
-        tensor pos (1,) int64; its key and value go into the caches there, then attention
-        over the first lens[b] cached keys.  No host value depends on the position, so a
-        step can be captured once in a HIP graph and replayed for every token."""
+        """One new token per sequence: x (B, 1, D) at position lens[b] - 1 (lens (B,) int32
+        on the device, pos (1,) int64 the same position); attention over the first
+        lens[b] keys, the new key and value written into the caches by the attention
+        kernel.  No host value depends on the position, so a step can be captured once in
+        a HIP graph and replayed for every token."""
         B, _, D = x.shape
         h = self._norm(x, self.ln1_w)
         qkv = self._lin(h, self.qkv).view(B, 1, 3, self.n_head, self.head_dim)
-        kv[0].index_copy_(1, pos, qkv[:, :, 1])
-        kv[1].index_copy_(1, pos, qkv[:, :, 2])
-        y = decode_attention(qkv[:, 0, 0], kv[0], kv[1], lens)          # (B, H, Dh)
+        # the attention kernel writes the new key and value into the caches at lens - 1
+        y = decode_attention(qkv[:, 0, 0], kv[0], kv[1], lens, k_new=qkv[:, 0, 1], v_new=qkv[:, 0, 2])
         x = x + self._lin(y.reshape(B, 1, D), self.proj)
         return self._mlp(x)
 

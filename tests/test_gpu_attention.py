@@ -166,3 +166,28 @@ def test_decode_rejects_bad_arguments(dev):
                          torch.zeros(1, 8, 2, 96, device=dev).bfloat16(),
                          torch.zeros(1, 8, 2, 96, device=dev).bfloat16(),
                          torch.ones(1, dtype=torch.int32, device=dev))
+
+
+@pytest.mark.parametrize("B,Tmax,H,D", [(2, 1024, 12, 64), (16, 512, 12, 64), (3, 300, 4, 128)])
+def test_decode_writes_new_key_value(dev, B, Tmax, H, D):
+    # k_new / v_new as key lens - 1: the same output, bit for bit, as writing them into
+    # the caches first, and the caches hold them afterwards (split segments and one
+    # workgroup per (sequence, head) alike)
+    from fxlm.attention import decode_attention
+    g = torch.Generator(device=dev).manual_seed(B + Tmax + D)
+    q = torch.randn(B, H, D, device=dev, generator=g).bfloat16()
+    k = torch.randn(B, Tmax, H, D, device=dev, generator=g).bfloat16()
+    v = torch.randn(B, Tmax, H, D, device=dev, generator=g).bfloat16()
+    qkv_new = torch.randn(B, 3, H, D, device=dev, generator=g).bfloat16()   # strided views
+    lens = torch.randint(1, Tmax + 1, (B,), device=dev, generator=g, dtype=torch.int32)
+    k2, v2 = k.clone(), v.clone()
+    o, lse = decode_attention(q, k, v, lens, return_lse=True, k_new=qkv_new[:, 1], v_new=qkv_new[:, 2])
+    rows = (lens.long() - 1)
+    bi = torch.arange(B, device=dev)
+    k2[bi, rows] = qkv_new[:, 1]
+    v2[bi, rows] = qkv_new[:, 2]
+    o2, lse2 = decode_attention(q, k2, v2, lens, return_lse=True)
+    assert torch.equal(o, o2) and torch.equal(lse, lse2)
+    assert torch.equal(k, k2) and torch.equal(v, v2)
+    with pytest.raises(ValueError):
+        decode_attention(q, k, v, lens, k_new=qkv_new[:, 1])
