@@ -260,6 +260,34 @@ int fx_linear_fwd(const uint16_t* X, int64_t ldx, const int32_t* idx, int64_t F,
                   const uint16_t* W, const uint16_t* bias, uint16_t* Y, uint16_t* H,
                   uint16_t* Xg, int64_t M, int64_t N, int64_t K, int32_t act, void* stream);
 
+/* Dense-row form of fx_linear_fwd with two fusions for inference:
+ *   Y = act(norm(X) W^T + bias) + res
+ * norm(X) = X * rsqrt(mean(X^2, row) + eps) * norm_w, rounded to bf16 as the RMSNorm
+ * forward writes it, when norm_w (K,) is given (M <= 64 rows: the few-row kernel
+ * computes the rows' rstd itself); res (M, N) row stride ldres, when given, is added
+ * after the activation.  X (M, K) row stride ldx, W (N, K) contiguous, bias (N,) or
+ * NULL, Y (M, N) contiguous, H (M, N) or NULL receives the pre-activation (before the
+ * residual).  X, W and norm_w 16-byte aligned, K % 8 == 0.
+ * No counterpart in the reference: it folds the RMSNorm before a block's qkv / fc and
+ * the residual sum after its proj / fc2 (ml/fxlm/model.py:60-71) into the projection,
+ * for decoding steps whose few rows make every extra kernel launch count. */
+typedef struct fxLinearArgs {
+    const uint16_t* X;
+    int64_t ldx;
+    const uint16_t* W;
+    const uint16_t* bias;
+    const uint16_t* res;
+    int64_t ldres;
+    const uint16_t* norm_w;
+    uint16_t* Y;
+    uint16_t* H;
+    int64_t M, N, K;
+    float eps;
+    int32_t act;
+} fxLinearArgs;
+
+int fx_linear_fwd_ex(const fxLinearArgs* args, void* stream);
+
 /* dh = dy * gelu_tanh'(h), elementwise over n bf16 values (16-byte aligned buffers).
  * The activation half of the fused linear's backward (the reference's torch autograd
  * of F.gelu(approximate="tanh"), ml/fxlm/model.py:71). */

@@ -54,6 +54,10 @@ struct GemmArgs {
     int64_t ldxg;
     int M, N, K;
     int act;   // 0: identity, 1: GELU (tanh approximation)
+    const uint16_t* res;  // residual (M, N) added to the output after the activation, or null
+    int64_t ldres;
+    const uint16_t* nw;  // RMSNorm weight (K,) applied to the A rows first (few-row kernel), or null
+    float eps;
 };
 
 // tile t -> (row panel, column tile): with a multiple of 8 row panels, tiles with
@@ -208,7 +212,9 @@ __global__ void __launch_bounds__(kGThreads, 1) gemm_bias_act_kernel(GemmArgs a)
                     if (m < a.M) {
                         const float h = acc[j][i][e] + bn;
                         if (a.H) a.H[(int64_t)m * a.ldh + n] = f32_to_bf16(h);
-                        a.C[(int64_t)m * a.ldc + n] = f32_to_bf16(a.act == 1 ? gelu_tanh(h) : h);
+                        float y = a.act == 1 ? gelu_tanh(h) : h;
+                        if (a.res) y += bf16_to_f32(a.res[(int64_t)m * a.ldres + n]);
+                        a.C[(int64_t)m * a.ldc + n] = f32_to_bf16(y);
                     }
                 }
         }
@@ -392,7 +398,16 @@ __device__ __forceinline__ f32x4 mfma16(const uint4& a, const uint4& b, const f3
                                                    0, 0, 0);
 }
 
-template <int NT, int MT>
+// row m of A (dense or gathered; null for a window that leaves X)
+__device__ __forceinline__ const uint16_t* xrow_base(const GemmArgs& a, int m) {
+    if (a.idx) {
+        const int64_t st = a.idx[m];
+        return (st >= 0 && st * a.F + a.K <= a.R * a.F) ? a.A + st * a.F : nullptr;
+    }
+    return a.A + (int64_t)m * a.lda;
+}
+
+template <int NT, int MT, bool NORM>
 __global__ void __launch_bounds__(1024) gemm_skinny_kernel(GemmArgs a, int sw) {
     constexpr int U = NT * MT >= 4 ? 2 : 4;  // K steps per load batch
     __shared__ __attribute__((aligned(16))) float red[kSKMaxTiles * 256];
@@ -413,18 +428,34 @@ __global__ void __launch_bounds__(1024) gemm_skinny_kernel(GemmArgs a, int sw) {
 #pragma unroll
     for (int j = 0; j < MT; ++j) {
         const int m = 16 * j + r;
-        const uint16_t* row = nullptr;
-        if (m < a.M) {
-            if (a.idx) {
-                const int64_t st = a.idx[m];
-                if (st >= 0 && st * a.F + a.K <= a.R * a.F) row = a.A + st * a.F;
-            } else {
-                row = a.A + (int64_t)m * a.lda;
-            }
-        }
+        const uint16_t* row = m < a.M ? xrow_base(a, m) : nullptr;
         xrow[j] = row ? row + 8 * kg : nullptr;
     }
     const bool wxg = a.Xg != nullptr && blockIdx.x == 0;
+
+    // NORM: A rows are RMS-normalised on the fly, x * rstd[m] * nw[k] rounded to bf16 as
+    // the norm kernel writes them.  Each workgroup first computes rstd of every row: wave
+    // v sums rows v, v + sw, ... (lane partials, then a butterfly: a fixed order).
+    __shared__ float srstd[kSKMaxM];
+    float rs[MT];
+    if constexpr (NORM) {
+        for (int m = w; m < a.M; m += sw) {
+            const uint16_t* row = xrow_base(a, m);
+            float q = 0.f;
+            if (row)
+                for (int c = lane; c < a.K / 8; c += 64) {
+                    float f[8];
+                    unpack8(ld16(row + c * 8), f);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) q = fmaf(f[e], f[e], q);
+                }
+            q = group_sum<64>(q);
+            if (lane == 0) srstd[m] = 1.f / sqrtf(q / (float)a.K + a.eps);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < MT; ++j) rs[j] = 16 * j + r < a.M ? srstd[16 * j + r] : 0.f;
+    }
 
     f32x4 acc[NT][MT];
 #pragma unroll
@@ -442,6 +473,19 @@ __global__ void __launch_bounds__(1024) gemm_skinny_kernel(GemmArgs a, int sw) {
             for (int i = 0; i < NT; ++i) wv[u][i] = ok && wrow[i] ? ld16(wrow[i] + s * 32) : zero;
 #pragma unroll
             for (int j = 0; j < MT; ++j) xv[u][j] = ok && xrow[j] ? ld16(xrow[j] + s * 32) : zero;
+            if constexpr (NORM) {
+                const uint4 wn = ok ? ld16(a.nw + s * 32 + 8 * kg) : zero;
+                float fw[8];
+                unpack8(wn, fw);
+#pragma unroll
+                for (int j = 0; j < MT; ++j) {
+                    float f[8];
+                    unpack8(xv[u][j], f);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) f[e] = f[e] * rs[j] * fw[e];
+                    xv[u][j] = pack8(f);
+                }
+            }
         }
         if (wxg) {
 #pragma unroll
@@ -481,12 +525,14 @@ __global__ void __launch_bounds__(1024) gemm_skinny_kernel(GemmArgs a, int sw) {
         if (n < a.N && m < a.M) {
             const float h = sum + (a.bias ? bf16_to_f32(a.bias[n]) : 0.f);
             if (a.H) a.H[(int64_t)m * a.ldh + n] = f32_to_bf16(h);
-            a.C[(int64_t)m * a.ldc + n] = f32_to_bf16(a.act == 1 ? gelu_tanh(h) : h);
+            float y = a.act == 1 ? gelu_tanh(h) : h;
+            if (a.res) y += bf16_to_f32(a.res[(int64_t)m * a.ldres + n]);
+            a.C[(int64_t)m * a.ldc + n] = f32_to_bf16(y);
         }
     }
 }
 
-template <int NT>
+template <int NT, bool NORM>
 static int skinny_launch(const GemmArgs& a, hipStream_t st) {
     const int mt = (a.M + 15) / 16;
     const int64_t nblk = ((int64_t)a.N + 16 * NT - 1) / (16 * NT);
@@ -496,18 +542,19 @@ static int skinny_launch(const GemmArgs& a, hipStream_t st) {
     while (sw < 16 && nblk * sw < target && 2 * sw <= ks && 2 * sw * NT * mt <= kSKMaxTiles) sw *= 2;
     const dim3 grid((unsigned)nblk), block(64 * sw);
     switch (mt) {
-        case 1: hipLaunchKernelGGL((gemm_skinny_kernel<NT, 1>), grid, block, 0, st, a, sw); break;
-        case 2: hipLaunchKernelGGL((gemm_skinny_kernel<NT, 2>), grid, block, 0, st, a, sw); break;
-        case 3: hipLaunchKernelGGL((gemm_skinny_kernel<NT, 3>), grid, block, 0, st, a, sw); break;
-        default: hipLaunchKernelGGL((gemm_skinny_kernel<NT, 4>), grid, block, 0, st, a, sw); break;
+        case 1: hipLaunchKernelGGL((gemm_skinny_kernel<NT, 1, NORM>), grid, block, 0, st, a, sw); break;
+        case 2: hipLaunchKernelGGL((gemm_skinny_kernel<NT, 2, NORM>), grid, block, 0, st, a, sw); break;
+        case 3: hipLaunchKernelGGL((gemm_skinny_kernel<NT, 3, NORM>), grid, block, 0, st, a, sw); break;
+        default: hipLaunchKernelGGL((gemm_skinny_kernel<NT, 4, NORM>), grid, block, 0, st, a, sw); break;
     }
     return check_launch("gemm_skinny");
 }
 
 // two W row tiles per workgroup once there are enough workgroups (fewer re-reads of X)
 static int linear_skinny(const GemmArgs& a, hipStream_t st) {
-    if ((a.N + 31) / 32 >= 2LL * device_cus()) return skinny_launch<2>(a, st);
-    return skinny_launch<1>(a, st);
+    const bool two = (a.N + 31) / 32 >= 2LL * device_cus();
+    if (a.nw) return two ? skinny_launch<2, true>(a, st) : skinny_launch<1, true>(a, st);
+    return two ? skinny_launch<2, false>(a, st) : skinny_launch<1, false>(a, st);
 }
 
 __global__ void __launch_bounds__(256)
@@ -525,6 +572,18 @@ gelu_bwd_kernel(const uint16_t* __restrict__ dy, const uint16_t* __restrict__ h,
     }
     for (int64_t i = n8 * 8 + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride)
         dh[i] = f32_to_bf16(bf16_to_f32(dy[i]) * gelu_tanh_grad(bf16_to_f32(h[i])));
+}
+
+// the few-row kernel for M <= kSKMaxM, else the persistent tiled kernel
+static int linear_fwd(const GemmArgs& a, hipStream_t stream) {
+    if (a.M <= kSKMaxM) return linear_skinny(a, stream);
+    const int64_t tiles = ((int64_t)(a.M + kGBM - 1) / kGBM) * ((a.N + kGBN - 1) / kGBN);
+    FX_REQUIRE(tiles < 0x7fffffffLL, "fx_linear_fwd: too many tiles");
+    // persistent grid: one workgroup per CU (the LDS of one is 147 KB)
+    const int64_t cus = device_cus();
+    const int64_t grid = tiles < cus ? tiles : cus;
+    hipLaunchKernelGGL(gemm_bias_act_kernel, dim3((unsigned)grid), dim3(kGThreads), 0, stream, a);
+    return check_launch("gemm_bias_act");
 }
 
 }  // namespace fx
@@ -550,7 +609,7 @@ extern "C" int fx_linear_fwd(const uint16_t* X, int64_t ldx, const int32_t* idx,
     FX_REQUIRE(((((uintptr_t)X) | ((uintptr_t)W) | ((uintptr_t)Xg)) & 15) == 0,
                "fx_linear_fwd: X, W, Xg must be 16-byte aligned");
     if (M == 0) return 0;
-    GemmArgs a;
+    GemmArgs a{};
     a.A = X;
     a.lda = ldx;
     a.idx = idx;
@@ -569,14 +628,46 @@ extern "C" int fx_linear_fwd(const uint16_t* X, int64_t ldx, const int32_t* idx,
     a.N = (int)N;
     a.K = (int)K;
     a.act = act;
-    if (M <= kSKMaxM) return linear_skinny(a, (hipStream_t)stream);
-    const int64_t tiles =((M + kGBM - 1) / kGBM) * ((N + kGBN - 1) / kGBN);
-    FX_REQUIRE(tiles < 0x7fffffffLL, "fx_linear_fwd: too many tiles");
-    // persistent grid: one workgroup per CU (the LDS of one is 147 KB)
-    const int64_t cus = device_cus();
-    const int64_t grid = tiles < cus ? tiles : cus;
-    hipLaunchKernelGGL(gemm_bias_act_kernel, dim3((unsigned)grid), dim3(kGThreads), 0, (hipStream_t)stream, a);
-    return check_launch("gemm_bias_act");
+    return linear_fwd(a, (hipStream_t)stream);
+}
+
+extern "C" int fx_linear_fwd_ex(const fxLinearArgs* args, void* stream) {
+    FX_REQUIRE(args != nullptr, "fx_linear_fwd_ex: null args");
+    const fxLinearArgs& p = *args;
+    FX_REQUIRE(p.X && p.W && p.Y, "fx_linear_fwd_ex: null pointer");
+    FX_REQUIRE(p.M >= 0 && p.N >= 1 && p.K >= 8 && p.K % 8 == 0,
+               "fx_linear_fwd_ex: bad shape M=%lld N=%lld K=%lld (K a multiple of 8)", (long long)p.M,
+               (long long)p.N, (long long)p.K);
+    FX_REQUIRE(p.M < 0x7fffffffLL && p.N < 0x7fffffffLL && p.K < 0x7fffffffLL, "fx_linear_fwd_ex: size too large");
+    FX_REQUIRE(p.act == 0 || p.act == 1, "fx_linear_fwd_ex: act=%d (0 identity, 1 gelu_tanh)", p.act);
+    FX_REQUIRE(p.ldx >= p.K && p.ldx % 8 == 0, "fx_linear_fwd_ex: ldx=%lld", (long long)p.ldx);
+    FX_REQUIRE(p.res == nullptr || p.ldres >= p.N, "fx_linear_fwd_ex: ldres=%lld < N", (long long)p.ldres);
+    FX_REQUIRE(p.norm_w == nullptr || p.M <= kSKMaxM,
+               "fx_linear_fwd_ex: the input RMSNorm needs M <= %d rows (M=%lld)", kSKMaxM, (long long)p.M);
+    FX_REQUIRE(p.norm_w == nullptr || (p.eps >= 0.f && p.eps < __builtin_huge_valf()),
+               "fx_linear_fwd_ex: eps %g", (double)p.eps);
+    FX_REQUIRE(((((uintptr_t)p.X) | ((uintptr_t)p.W) | ((uintptr_t)p.norm_w)) & 15) == 0,
+               "fx_linear_fwd_ex: X, W and norm_w must be 16-byte aligned");
+    if (p.M == 0) return 0;
+    GemmArgs a{};
+    a.A = p.X;
+    a.lda = p.ldx;
+    a.B = p.W;
+    a.ldb = p.K;
+    a.bias = p.bias;
+    a.C = p.Y;
+    a.ldc = p.N;
+    a.H = p.H;
+    a.ldh = p.N;
+    a.M = (int)p.M;
+    a.N = (int)p.N;
+    a.K = (int)p.K;
+    a.act = p.act;
+    a.res = p.res;
+    a.ldres = p.ldres;
+    a.nw = p.norm_w;
+    a.eps = p.eps;
+    return linear_fwd(a, (hipStream_t)stream);
 }
 
 // K steps of 64 tokens per slice at least 4, at most 32 slices, and no more workgroups

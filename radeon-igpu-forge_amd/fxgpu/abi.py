@@ -88,6 +88,16 @@ class fxAttnDecodeArgs(ctypes.Structure):
     ]
 
 
+class fxLinearArgs(ctypes.Structure):
+    _fields_ = [
+        ("X", c_void_p), ("ldx", c_int64), ("W", c_void_p), ("bias", c_void_p),
+        ("res", c_void_p), ("ldres", c_int64), ("norm_w", c_void_p),
+        ("Y", c_void_p), ("H", c_void_p),
+        ("M", c_int64), ("N", c_int64), ("K", c_int64),
+        ("eps", c_float), ("act", c_int32),
+    ]
+
+
 _P = c_void_p
 # name -> (restype, argtypes); must list exactly the functions of fx_abi.h
 SIGNATURES = {
@@ -111,6 +121,7 @@ SIGNATURES = {
     "fx_attn_decode": (c_int32, [ctypes.POINTER(fxAttnDecodeArgs), _P]),
     "fx_linear_fwd": (c_int32, [_P, c_int64, _P, c_int64, c_int64, _P, _P, _P, _P, _P,
                                 c_int64, c_int64, c_int64, c_int32, _P]),
+    "fx_linear_fwd_ex": (c_int32, [_P, _P]),
     "fx_gelu_bwd": (c_int32, [_P, _P, _P, c_int64, _P]),
     "fx_linear_wgrad_workspace": (c_int64, [c_int64, c_int64, c_int64]),
     "fx_linear_wgrad": (c_int32, [_P, c_int64, _P, c_int64, _P, c_int64, _P, c_int64, c_int64, c_int64,
@@ -146,9 +157,16 @@ def lib():
     return _LIB
 
 
+_FUNCS = {}
+
+
 def call(name, *args):
-    """Call ``fx_<name>``; a non-zero return raises RuntimeError with the library message."""
-    rc = getattr(lib(), name)(*args)
+    """Call ``fx_<name>``; a non-zero return raises RuntimeError with the library message.
+    The bound functions are looked up once (the GPT step makes ~400 calls)."""
+    f = _FUNCS.get(name)
+    if f is None:
+        f = _FUNCS[name] = getattr(lib(), name)
+    rc = f(*args)
     if rc != 0:
         msg = lib().fx_last_error().decode(errors="replace")
         if rc == FX_EINVAL:
@@ -157,11 +175,13 @@ def call(name, *args):
 
 
 def ptr(t):
-    """Device pointer of a tensor (None -> NULL)."""
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+    """Device pointer of a tensor as an int (None -> NULL); the argtypes convert it."""
+    return None if t is None else t.data_ptr()
 
 
 def stream_of(t):
-    """The current torch stream on t's device, as a hipStream_t handle."""
+    """The current torch stream on t's device, as a hipStream_t handle (an int): torch's
+    raw-stream query, without building a Stream object (2.2 -> 0.1 us per call)."""
     import torch
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+    return torch._C._cuda_getCurrentRawStream(t.device.index if t.device.index is not None
+                                              else torch.cuda.current_device())

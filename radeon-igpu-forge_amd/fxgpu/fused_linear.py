@@ -16,10 +16,15 @@
   GEMM.
 * ``linear_wgrad(dy, x)`` -- dW = dy^T x for dy (T, N) and x (T, K): the weight
   gradient that ml/fxgpu/fused_linear.py:90-101 computes with rocBLAS.
+* ``linear_ex(x, W, bias, residual, norm_weight, eps, activation)`` -- inference
+  forward with the input RMSNorm and the output residual folded into the GEMM
+  (decoding steps).
 """
+import ctypes
+
 import torch
 
-from fxgpu.abi import call, lib, ptr, stream_of
+from fxgpu.abi import call, fxLinearArgs, lib, ptr, stream_of
 
 _ACTS = {None: 0, "none": 0, "identity": 0, "gelu_tanh": 1}
 
@@ -216,3 +221,50 @@ class FusedLinear(torch.autograd.Function):
 def fused_linear(x, weight, bias=None, activation="gelu_tanh"):
     """y = activation(x @ weight.T + bias) with the activation fused into the GEMM."""
     return FusedLinear.apply(x, weight, bias, activation)
+
+
+def linear_ex(x, weight, bias=None, residual=None, norm_weight=None, eps=1e-6, activation=None):
+    """Inference forward y = act(norm(x) @ weight.T + bias) + residual in one launch
+    (fx_linear_fwd_ex): norm is an RMSNorm of the rows of x with norm_weight (only for
+    at most FEW_ROWS rows), residual a tensor shaped like y.  No autograd."""
+    if activation not in _ACTS:
+        raise ValueError(f"activation {activation!r} not in {sorted(k for k in _ACTS if k)}")
+    for nm, t in (("x", x), ("weight", weight), ("bias", bias), ("residual", residual),
+                  ("norm_weight", norm_weight)):
+        if t is not None and (t.dtype != torch.bfloat16 or not t.is_cuda):
+            raise TypeError(f"{nm} must be a bfloat16 cuda tensor")
+    K = x.shape[-1]
+    if weight.dim() != 2 or weight.shape[1] != K or not weight.is_contiguous():
+        raise ValueError(f"weight must be a contiguous (N, {K}), got {tuple(weight.shape)}")
+    if K % 8:
+        raise ValueError(f"in_features={K} must be a multiple of 8")
+    N = weight.shape[0]
+    x2 = _rows(x)
+    M = x2.shape[0]
+    if norm_weight is not None:
+        if norm_weight.shape != (K,) or not norm_weight.is_contiguous():
+            raise ValueError(f"norm_weight must be a contiguous ({K},)")
+        if M > FEW_ROWS:
+            raise ValueError(f"the fused input norm takes at most {FEW_ROWS} rows, got {M}")
+    if bias is not None and (bias.shape != (N,) or not bias.is_contiguous()):
+        raise ValueError(f"bias must be a contiguous ({N},)")
+    r2 = None
+    if residual is not None:
+        if tuple(residual.shape[:-1]) != tuple(x.shape[:-1]) or residual.shape[-1] != N:
+            raise ValueError(f"residual {tuple(residual.shape)} must be shaped like the output")
+        r2 = residual.reshape(-1, N)
+        if r2.stride(1) != 1:
+            r2 = r2.contiguous()
+    y = torch.empty(M, N, device=x.device, dtype=torch.bfloat16)
+    a = fxLinearArgs()
+    a.X, a.ldx, a.W = x2.data_ptr(), x2.stride(0), weight.data_ptr()
+    a.bias = bias.data_ptr() if bias is not None else None
+    if r2 is not None:
+        a.res, a.ldres = r2.data_ptr(), r2.stride(0)
+    a.norm_w = norm_weight.data_ptr() if norm_weight is not None else None
+    a.Y = y.data_ptr()
+    a.M, a.N, a.K = M, N, K
+    a.eps = float(eps)
+    a.act = _ACTS[activation]
+    call("fx_linear_fwd_ex", ctypes.byref(a), stream_of(x))
+    return y.view(*x.shape[:-1], N)

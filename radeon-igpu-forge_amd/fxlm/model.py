@@ -16,7 +16,7 @@ import torch
 import torch.nn.functional as Fn
 from torch import nn
 
-from fxgpu.fused_linear import fused_linear, linear
+from fxgpu.fused_linear import FEW_ROWS, fused_linear, linear, linear_ex
 
 from .attention import decode_attention, flash_attention_qkv
 from .cross_entropy import linear_cross_entropy
@@ -107,12 +107,25 @@ class Block(nn.Module):
         kernel.  No host value depends on the position, so a step can be captured once in
         a HIP graph and replayed for every token."""
         B, _, D = x.shape
+        if self._fused_step(B):
+            # four projections and the attention: the norms run inside qkv / fc, the
+            # residual sums inside proj / fc2
+            qkv = linear_ex(x, self.qkv.weight, norm_weight=self.ln1_w, eps=self.eps)
+            qkv = qkv.view(B, 1, 3, self.n_head, self.head_dim)
+            y = decode_attention(qkv[:, 0, 0], kv[0], kv[1], lens, k_new=qkv[:, 0, 1], v_new=qkv[:, 0, 2])
+            x = linear_ex(y.reshape(B, 1, D), self.proj.weight, residual=x)
+            u = linear_ex(x, self.fc.weight, norm_weight=self.ln2_w, eps=self.eps, activation="gelu_tanh")
+            return linear_ex(u, self.fc2.weight, residual=x)
         h = self._norm(x, self.ln1_w)
         qkv = self._lin(h, self.qkv).view(B, 1, 3, self.n_head, self.head_dim)
         # the attention kernel writes the new key and value into the caches at lens - 1
         y = decode_attention(qkv[:, 0, 0], kv[0], kv[1], lens, k_new=qkv[:, 0, 1], v_new=qkv[:, 0, 2])
         x = x + self._lin(y.reshape(B, 1, D), self.proj)
         return self._mlp(x)
+
+    def _fused_step(self, rows):
+        return (self.norm_impl == "fused" and self.linear_impl == "fused" and self.mlp_impl == "fused"
+                and rows <= FEW_ROWS)
 
 
 class GPT(nn.Module):
@@ -211,6 +224,8 @@ class GPT(nn.Module):
         x = self.tok_emb(tok.view(B, 1)) + self.pos_emb.index_select(0, pos)
         for blk, kv in zip(self.blocks, cache):
             x = blk.step(x, kv, pos, lens)
+        if self.blocks and self.blocks[0]._fused_step(B):   # final norm inside the head GEMM
+            return linear_ex(x[:, 0], self._head_w(), norm_weight=self.lnf_w, eps=self.cfg.eps).float()
         x = self._norm_f(x)
         return self._head(x[:, 0]).float()
 

@@ -47,7 +47,7 @@ def test_library_exports_every_symbol(abi):
     assert lib.fx_abi_version() == abi.FX_ABI_VERSION
 
 
-STRUCTS = ["fxCEArgs", "fxTensorList", "fxAdamWState", "fxAttnArgs", "fxAttnDecodeArgs"]
+STRUCTS = ["fxCEArgs", "fxTensorList", "fxAdamWState", "fxAttnArgs", "fxAttnDecodeArgs", "fxLinearArgs"]
 
 
 def test_struct_layout_matches_c(abi, tmp_path):

@@ -283,3 +283,47 @@ def test_few_rows_gather_writes_windows(dev):
     assert float(Xg[7].abs().max()) == 0.0
     rdW = gout.double().cpu().t() @ Xg
     assert max_abs(W.grad, rdW) <= _rel_tol(rdW)
+
+
+# ---- inference forward with the input norm and output residual folded in -----------
+
+@pytest.mark.parametrize("M,K,N,norm,res,act", [
+    (16, 768, 2304, True, False, None),        # a decode step's qkv: norm inside
+    (16, 768, 3072, True, False, "gelu_tanh"),  # fc: norm + GELU
+    (16, 768, 768, False, True, None),          # proj: residual inside
+    (1, 3072, 768, False, True, None),          # fc2 of one sequence
+    (64, 200, 129, True, True, "gelu_tanh"),    # everything, ragged K / N, 64 rows
+    (300, 256, 520, False, True, None),         # residual on the tiled kernel (M > 64)
+])
+def test_linear_ex_against_oracle(dev, M, K, N, norm, res, act):
+    from fxgpu.fused_linear import linear_ex
+    from oracle import norm as onorm
+    # outputs stay below 8 in magnitude, where the bf16 rounding of the result alone
+    # (half an ulp, 1/64 in [4, 8)) fits the 2e-2 bound
+    torch.manual_seed(M + K + N)
+    x = torch.randn(M, K).bfloat16()
+    W = (torch.randn(N, K) * K ** -0.5).bfloat16()
+    b = (torch.randn(N) * 0.1).bfloat16()
+    nw = (torch.randn(K) * 0.1 + 1).bfloat16() if norm else None
+    r = (torch.randn(M, N) * 0.5).bfloat16() if res else None
+    y = linear_ex(x.to(dev), W.to(dev), bias=b.to(dev), residual=r.to(dev) if res else None,
+                  norm_weight=nw.to(dev) if norm else None, eps=1e-6, activation=act)
+    # reference: the norm's bf16 output (as the RMSNorm forward writes it), then the GEMM
+    h = onorm.rms_norm_fwd(x, nw, 1e-6)[0].to(torch.bfloat16) if norm else x
+    z = h.double() @ W.double().t() + b.double()
+    if act:
+        z = olin.gelu_tanh(z)
+    if res:
+        z = z + r.double()
+    assert float(z.abs().max()) < 8.0
+    assert max_abs(y, z) <= ATOL_BF16
+
+
+def test_linear_ex_rejects(dev):
+    from fxgpu.fused_linear import linear_ex
+    x = torch.zeros(65, 64, device=dev, dtype=torch.bfloat16)
+    W = torch.zeros(32, 64, device=dev, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="at most"):
+        linear_ex(x, W, norm_weight=torch.ones(64, device=dev, dtype=torch.bfloat16))
+    with pytest.raises(ValueError):
+        linear_ex(x, W, residual=torch.zeros(65, 31, device=dev, dtype=torch.bfloat16))
