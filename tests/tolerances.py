@@ -1,4 +1,4 @@
-"""Parity tolerances (north star of this build, stated once for every test).
+"""Parity tolerances of this build's kernels against the oracle, stated once for every test.
 
 * Attention and linear outputs / gradients (bf16 results of bf16 inputs):
   max |ours - fp32 oracle| <= 2e-2.
