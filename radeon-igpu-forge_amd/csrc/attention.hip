@@ -332,6 +332,9 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dq_kern
     dma.init(a.kst, a.vst);
     dma.issue(kbase, vbase, T, sk0, sv0);
 
+    // this lane's lse, read before the Delta store below (a load after a store to
+    // another fp32 array may not be moved above it: one more memory round trip)
+    const float lse2 = qok ? a.lse[(int64_t)bh * T + qi] * kLog2e : 0.f;
     // Q^T and dO^T operands, Delta = rowsum(dO * O) for this lane's query
     bf16x8 qop[DC], dop[DC];
     float delta = 0.f;
@@ -357,7 +360,6 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dq_kern
         delta = pair_sum(delta);
         if (qok && g == 0) a.delta[(int64_t)bh * T + qi] = delta;
     }
-    const float lse2 = qok ? a.lse[(int64_t)bh * T + qi] * kLog2e : 0.f;
     const float sl2 = a.scale * kLog2e;
 
     f32x16 acc[DT];
