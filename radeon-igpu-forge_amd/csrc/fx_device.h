@@ -77,6 +77,14 @@ __device__ __forceinline__ void st16_nt(void* p, const uint4& v) {
     u32x4 r = {v.x, v.y, v.z, v.w};
     __builtin_nontemporal_store(r, reinterpret_cast<u32x4*>(p));
 }
+__device__ __forceinline__ float4 ldf4_nt(const float* p) {
+    const f32x4 r = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+    return make_float4(r.x, r.y, r.z, r.w);
+}
+__device__ __forceinline__ void stf4_nt(float* p, const float4& v) {
+    const f32x4 r = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(r, reinterpret_cast<f32x4*>(p));
+}
 
 // butterfly reductions over groups of W consecutive lanes (W a power of two <= 64)
 template <int W>

@@ -55,7 +55,7 @@ __global__ void __launch_bounds__(kOptThreads) adamw_sumsq_kernel(ChunkList L, f
         const int64_t e = base + ((int64_t)u * kOptThreads + threadIdx.x) * 8;
         gv[u] = make_uint4(0u, 0u, 0u, 0u);
         if (e + 8 <= n) {
-            gv[u] = ld16_nt(g + e);  // streamed: measured ~8 us faster per 124M step
+            gv[u] = ld16(g + e);  // cached: the update kernel re-reads it
         } else if (e < n) {
             uint16_t tmp[8] = {0, 0, 0, 0, 0, 0, 0, 0};
             for (int j = 0; j < 8 && e + j < n; ++j) tmp[j] = g[e + j];
@@ -142,6 +142,12 @@ __device__ __forceinline__ void adamw_elem(float g, float& w, float& m, float& v
 // fp32, 512 B of bf16).  The block's g/master/m/v loads are issued before the
 // step's scalars (clip factor, skip flag, bias corrections) are read, so no block
 // waits on them before its data is in flight.
+// Cache policy: master, m and v are loaded and stored non-temporally, while the
+// gradient (read just before by adamw_sumsq with ordinary loads) is loaded normally.
+// The bf16 gradient of a 124M-parameter model (249 MB) then stays in the GPU's 256 MB
+// memory-side cache between the two passes instead of being evicted by the 3 GB fp32
+// stream, and its second read is served from there: 699 -> 627-639 us per step at
+// 124,373,760 parameters, bitwise-identical results.
 __global__ void __launch_bounds__(kOptThreads)
 adamw_update_kernel(ChunkList L, const float* __restrict__ work, float* __restrict__ master,
                     float* __restrict__ mom, float* __restrict__ var, uint16_t* __restrict__ p16,
@@ -163,9 +169,9 @@ adamw_update_kernel(ChunkList L, const float* __restrict__ work, float* __restri
         for (int h = 0; h < 2; ++h) {
             const int64_t e = e0 + 256 * h;
             gq[h] = *reinterpret_cast<const uint2*>(g + e);
-            w[h] = *reinterpret_cast<const float4*>(master + off + e);
-            m[h] = *reinterpret_cast<const float4*>(mom + off + e);
-            v[h] = *reinterpret_cast<const float4*>(var + off + e);
+            w[h] = ldf4_nt(master + off + e);
+            m[h] = ldf4_nt(mom + off + e);
+            v[h] = ldf4_nt(var + off + e);
         }
         const float4 sc = *reinterpret_cast<const float4*>(work);  // clip/scale, skip, 1/bc1, 1/bc2
         if (sc.y != 0.f) return;  // non-finite gradients: skip the step
@@ -179,9 +185,9 @@ adamw_update_kernel(ChunkList L, const float* __restrict__ work, float* __restri
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 adamw_elem(gf[j] * sc.x, wf[j], mf[j], vf[j], lr, lrwd, b1, b2, b1c, b2c, sc.z, sc.w, eps, wd_on);
-            *reinterpret_cast<float4*>(master + off + e) = make_float4(wf[0], wf[1], wf[2], wf[3]);
-            *reinterpret_cast<float4*>(mom + off + e) = make_float4(mf[0], mf[1], mf[2], mf[3]);
-            *reinterpret_cast<float4*>(var + off + e) = make_float4(vf[0], vf[1], vf[2], vf[3]);
+            stf4_nt(master + off + e, make_float4(wf[0], wf[1], wf[2], wf[3]));
+            stf4_nt(mom + off + e, make_float4(mf[0], mf[1], mf[2], mf[3]));
+            stf4_nt(var + off + e, make_float4(vf[0], vf[1], vf[2], vf[3]));
             uint2 o;
             o.x = pack_bf16x2(wf[0], wf[1]);
             o.y = pack_bf16x2(wf[2], wf[3]);
