@@ -81,6 +81,27 @@ def test_qkv_variant(dev, causal):
         assert max_abs(x.grad[:, :, i], r) <= ATOL_BF16
 
 
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("T,Dh", [(77, 64), (45, 128)])
+def test_free_strides(dev, causal, T, Dh):
+    # ml/fxlm/attention.py:57-79 accepts any b/t/h strides with a unit-stride last dim:
+    # q is a (B,H,T,Dh) buffer seen through transpose(1, 2), k is contiguous, v takes
+    # every other head of a (B,T,2H,Dh) buffer, and dO is non-contiguous too
+    torch.manual_seed(T + Dh)
+    B, H = 2, 3
+    qb = torch.randn(B, H, T, Dh).bfloat16()
+    k = torch.randn(B, T, H, Dh).bfloat16()
+    vb = torch.randn(B, T, 2 * H, Dh).bfloat16()
+    dob = torch.randn(B, H, T, Dh).bfloat16()
+    q, v, do = qb.transpose(1, 2), vb[:, :, ::2], dob.transpose(1, 2)
+    assert not (q.is_contiguous() or v.is_contiguous() or do.is_contiguous())
+    got = _fwd_bwd(qb.to(dev).transpose(1, 2), k.to(dev), vb.to(dev)[:, :, ::2], dob.to(dev).transpose(1, 2),
+                   causal, 1.0 / math.sqrt(Dh))
+    ro, rl = oatt.attn_fwd(q, k, v, causal)
+    rdq, rdk, rdv = oatt.attn_bwd(q, k, v, got[0].cpu(), rl, do, causal)
+    _check(got, (ro, rl, rdq, rdk, rdv))
+
+
 def test_single_key_closed_form(dev):
     from fxlm.attention import flash_attention
     torch.manual_seed(2)
