@@ -16,6 +16,42 @@ def test_loader_smoke(dev):
     assert bool((y == 3.5).all())
 
 
+_TWO_KERNELS = r"""
+extern "C" __global__ void scale_rev(float* p, float s, int n) {
+    extern __shared__ float tile[];
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    tile[threadIdx.x] = i < n ? p[i] : 0.f;
+    __syncthreads();
+    if (i < n) p[i] = tile[blockDim.x - 1 - threadIdx.x] * s;
+}
+extern "C" __global__ void add_one(float* p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] += 1.f;
+}
+"""
+
+
+def test_hiprtc_module_shared_memory_and_streams(dev):
+    # ml/fxgpu/hip_kernel.py:88-145: one compile for several kernels, dynamic shared
+    # memory, an explicit stream, and stream=None meaning the current torch stream
+    import ctypes
+    from fxgpu import hip_kernel
+    fns = hip_kernel.compile_module(_TWO_KERNELS, ["scale_rev", "add_one"])
+    n = 1024  # whole 256-thread blocks: every reversed index stays inside its block
+    x = torch.arange(n, device=dev, dtype=torch.float32)
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        hip_kernel.launch(fns["scale_rev"], (n // 256, 1, 1), (256, 1, 1),
+                          [ctypes.c_void_p(x.data_ptr()), ctypes.c_float(2.0), ctypes.c_int(n)],
+                          shared=256 * 4, stream=side.cuda_stream)
+        hip_kernel.launch(fns["add_one"], (n // 256, 1, 1), (256, 1, 1),
+                          [ctypes.c_void_p(x.data_ptr()), ctypes.c_int(n)])
+    side.synchronize()
+    want = torch.arange(n, dtype=torch.float32).view(-1, 256).flip(1).reshape(-1) * 2 + 1
+    assert torch.equal(x.cpu(), want)
+
+
 def _cfg(**kw):
     from fxlm.model import GPTConfig
     return GPTConfig(vocab_size=256, seq_len=64, n_layer=2, n_head=2, d_model=128, **kw)

@@ -67,6 +67,17 @@ def test_hip_kernel_surface():
         assert hasattr(hip_kernel, name)
 
 
+def test_hiprtc_compile_error_raises_with_log(capsys):
+    # ml/fxgpu/hip_kernel.py:59-69: the compiler log is printed with a "[hiprtc log]"
+    # prefix and a failed compile raises RuntimeError before anything is loaded
+    from fxgpu import hip_kernel
+    src = 'extern "C" __global__ void bad(float* p) { p[0] = undeclared_name; }'
+    with pytest.raises(RuntimeError, match="hiprtcCompileProgram failed"):
+        hip_kernel.compile_module(src, ["bad"])
+    out = capsys.readouterr().out
+    assert "[hiprtc log]" in out and "undeclared_name" in out
+
+
 def test_lazy_exports():
     import fxgpu
     import fxlm
