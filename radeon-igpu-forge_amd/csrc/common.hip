@@ -24,15 +24,14 @@ int check_launch(const char* what) {
 }
 
 int device_cus() {
-    static int s_cus = 0;
-    if (s_cus == 0) {
+    // initialised once, thread-safely (host threads such as autograd's may call first)
+    static const int s_cus = [] {
         int dev = 0, cus = 0;
         if (hipGetDevice(&dev) == hipSuccess &&
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
-            s_cus = cus;
-        else
-            s_cus = 256;
-    }
+            return cus;
+        return 256;
+    }();
     return s_cus;
 }
 
