@@ -24,7 +24,7 @@ extern "C" {
 #endif
 
 #define FX_EINVAL (-1)
-#define FX_ABI_VERSION 2
+#define FX_ABI_VERSION 3
 
 /* ---- library ------------------------------------------------------------ */
 
@@ -70,6 +70,14 @@ int fx_rms_norm_bwd(const uint16_t* x, const uint16_t* dy, const uint16_t* w,
 int fx_rms_norm_bwd_add(const uint16_t* x, const uint16_t* dy, const uint16_t* dres,
                         const uint16_t* w, const float* rstd, uint16_t* dx, float* dw_f32,
                         uint16_t* dw, float* work, int64_t N, int32_t D, void* stream);
+
+/* xsum = x + r (fp32 sum rounded to bf16, as a bf16 tensor add rounds it) and
+ * fx_rms_norm_fwd of xsum, in one pass: (N, D) bf16 x, r, xsum, y, 16-byte aligned;
+ * y and rstd are bit for bit those of the add followed by fx_rms_norm_fwd.  No
+ * counterpart in the reference: it fuses the residual sums of ml/fxlm/model.py:69,71
+ * (x = x + proj(...), x = x + fc2(...)) into the next norm that reads them. */
+int fx_rms_norm_fwd_add(const uint16_t* x, const uint16_t* r, const uint16_t* w, uint16_t* xsum,
+                        uint16_t* y, float* rstd, int64_t N, int32_t D, float eps, void* stream);
 
 /* ---- softmax cross-entropy ---------------------------------------------- */
 

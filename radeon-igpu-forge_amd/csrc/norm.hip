@@ -14,10 +14,13 @@
 
 namespace fx {
 
-template <int LPR, int NV>
+// ADD: the row is x + radd instead (fp32 sum rounded to bf16, as a bf16 tensor add
+// rounds it), written to xsum and normalised from those rounded values.
+template <int LPR, int NV, bool ADD = false>
 __global__ void __launch_bounds__(256)
 rms_fwd_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-               uint16_t* __restrict__ y, float* __restrict__ rstd, int64_t N, int D, float eps) {
+               uint16_t* __restrict__ y, float* __restrict__ rstd, int64_t N, int D, float eps,
+               const uint16_t* __restrict__ radd, uint16_t* __restrict__ xsum) {
     constexpr int G = 256 / LPR;
     const int lane = threadIdx.x % LPR;
     const int64_t row = (int64_t)blockIdx.x * G + threadIdx.x / LPR;
@@ -27,15 +30,48 @@ rms_fwd_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
 
     uint4 xv[NV];
     float ss = 0.f;
+    if constexpr (ADD) {
+        const uint16_t* rr = radd + row * D;
+        uint16_t* sr = xsum + row * D;
+        uint4 rv[NV];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int c = i * LPR + lane;
-        xv[i] = make_uint4(0u, 0u, 0u, 0u);
-        if (c < V8) xv[i] = ld16_nt(xr + (int64_t)c * 8);
-        float f[8];
-        unpack8(xv[i], f);
+        for (int i = 0; i < NV; ++i) {
+            const int c = i * LPR + lane;
+            xv[i] = make_uint4(0u, 0u, 0u, 0u);
+            rv[i] = xv[i];
+            if (c < V8) {
+                xv[i] = ld16_nt(xr + (int64_t)c * 8);
+                rv[i] = ld16_nt(rr + (int64_t)c * 8);
+            }
+        }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
+        for (int i = 0; i < NV; ++i) {
+            const int c = i * LPR + lane;
+            if (c < V8) {
+                float f[8], q[8];
+                unpack8(xv[i], f);
+                unpack8(rv[i], q);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) f[j] += q[j];
+                xv[i] = pack8(f);
+                st16_nt(sr + (int64_t)c * 8, xv[i]);
+            }
+            float f[8];
+            unpack8(xv[i], f);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int c = i * LPR + lane;
+            xv[i] = make_uint4(0u, 0u, 0u, 0u);
+            if (c < V8) xv[i] = ld16_nt(xr + (int64_t)c * 8);
+            float f[8];
+            unpack8(xv[i], f);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ss += f[j] * f[j];
+        }
     }
     ss = group_sum<LPR>(ss);
     const float r = rsqrtf(ss / (float)D + eps);
@@ -358,10 +394,30 @@ extern "C" int fx_rms_norm_fwd(const uint16_t* x, const uint16_t* w, uint16_t* y
     FX_REQUIRE(blocks <= 0x7fffffff, "fx_rms_norm_fwd: N=%lld too large", (long long)N);
 #define FX_CALL(L, V)                                                                       \
     hipLaunchKernelGGL((rms_fwd_kernel<L, V>), dim3((unsigned)blocks), dim3(256), 0,        \
-                       (hipStream_t)stream, x, w, y, rstd, N, (int)D, eps)
+                       (hipStream_t)stream, x, w, y, rstd, N, (int)D, eps, nullptr, nullptr)
     FX_NORM_DISPATCH(s, FX_CALL)
 #undef FX_CALL
     return check_launch("rms_norm_fwd");
+}
+
+extern "C" int fx_rms_norm_fwd_add(const uint16_t* x, const uint16_t* r, const uint16_t* w, uint16_t* xsum,
+                                   uint16_t* y, float* rstd, int64_t N, int32_t D, float eps, void* stream) {
+    if (int e = norm_check(x, w, N, D, "fx_rms_norm_fwd_add")) return e;
+    if (N == 0) return 0;
+    FX_REQUIRE(r != nullptr && xsum != nullptr && y != nullptr && rstd != nullptr,
+               "fx_rms_norm_fwd_add: null pointer");
+    FX_REQUIRE(((((uintptr_t)x) | ((uintptr_t)r) | ((uintptr_t)xsum) | ((uintptr_t)y)) & 15) == 0,
+               "fx_rms_norm_fwd_add: x, r, xsum and y must be 16-byte aligned");
+    const RowShape s = pick_shape(D);
+    const int G = 256 / s.lpr;
+    const int64_t blocks = (N + G - 1) / G;
+    FX_REQUIRE(blocks <= 0x7fffffff, "fx_rms_norm_fwd_add: N=%lld too large", (long long)N);
+#define FX_CALL(L, V)                                                                       \
+    hipLaunchKernelGGL((rms_fwd_kernel<L, V, true>), dim3((unsigned)blocks), dim3(256), 0,  \
+                       (hipStream_t)stream, x, w, y, rstd, N, (int)D, eps, r, xsum)
+    FX_NORM_DISPATCH(s, FX_CALL)
+#undef FX_CALL
+    return check_launch("rms_norm_fwd_add");
 }
 
 extern "C" int64_t fx_rms_norm_bwd_workspace(int64_t N, int32_t D) {

@@ -14,7 +14,7 @@ LIB_PATH = os.path.join(_PKG_ROOT, "libfxforge.so")
 HEADER_PATH = os.path.join(os.path.dirname(_PKG_ROOT), "include", "fx_abi.h")
 
 FX_EINVAL = -1
-FX_ABI_VERSION = 2
+FX_ABI_VERSION = 3
 MAX_TENSORS = 64
 
 c_void_p = ctypes.c_void_p
@@ -105,6 +105,7 @@ SIGNATURES = {
     "fx_last_error": (ctypes.c_char_p, []),
     "fx_fill_f32": (c_int32, [_P, c_int64, c_float, _P]),
     "fx_rms_norm_fwd": (c_int32, [_P, _P, _P, _P, c_int64, c_int32, c_float, _P]),
+    "fx_rms_norm_fwd_add": (c_int32, [_P, _P, _P, _P, _P, _P, c_int64, c_int32, c_float, _P]),
     "fx_rms_norm_bwd_workspace": (c_int64, [c_int64, c_int32]),
     "fx_rms_norm_bwd": (c_int32, [_P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int32, _P]),
     "fx_rms_norm_bwd_add": (c_int32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, c_int64, c_int32, _P]),

@@ -20,7 +20,7 @@ from fxgpu.fused_linear import FEW_ROWS, fused_linear, linear, linear_ex
 
 from .attention import decode_attention, flash_attention_qkv
 from .cross_entropy import linear_cross_entropy
-from .norm import pre_norm, rms_norm
+from .norm import add_pre_norm, pre_norm, rms_norm
 
 
 @dataclass
@@ -82,11 +82,28 @@ class Block(nn.Module):
             u = Fn.gelu(self.fc(h), approximate="tanh")
         return x + self._lin(u, self.fc2)
 
+    def _add_prenorm(self, x, r, w):
+        """(x + r, norm(x + r)); the fused form adds inside the norm's own pass."""
+        if self.norm_impl == "fused":
+            return add_pre_norm(x, r, w, self.eps)
+        x = x + r
+        return x, self._norm(x, w)
+
     def forward(self, x, kv=None):
         """kv: optional (k_cache, v_cache) (B, Tmax, H, Dh) that receive this block's
         keys and values at positions 0..T-1 (the prompt of a cached generation)."""
+        x, out = self.forward_pair(x, None, kv)
+        return x + out
+
+    def forward_pair(self, x, branch=None, kv=None):
+        """(x', out) with the block's output x' + out (ml/fxlm/model.py:65-72), the last
+        residual sum left to the next norm that reads it; `branch`, the previous block's
+        `out`, is added to x inside this block's first norm."""
         B, T, D = x.shape
-        x, h = self._prenorm(x, self.ln1_w)
+        if branch is None:
+            x, h = self._prenorm(x, self.ln1_w)
+        else:
+            x, h = self._add_prenorm(x, branch, self.ln1_w)
         qkv = self._lin(h, self.qkv).view(B, T, 3, self.n_head, self.head_dim)
         if kv is not None:
             kv[0][:, :T].copy_(qkv[:, :, 1])
@@ -97,8 +114,12 @@ class Block(nn.Module):
             q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))   # (B,H,T,Dh)
             y = Fn.scaled_dot_product_attention(q, k, v, is_causal=True)
             y = y.transpose(1, 2)
-        x = x + self._lin(y.reshape(B, T, D), self.proj)
-        return self._mlp(x)
+        x, h = self._add_prenorm(x, self._lin(y.reshape(B, T, D), self.proj), self.ln2_w)
+        if self.mlp_impl == "fused":
+            u = fused_linear(h, self.fc.weight, None, "gelu_tanh")
+        else:
+            u = Fn.gelu(self.fc(h), approximate="tanh")
+        return x, self._lin(u, self.fc2)
 
     def step(self, x, kv, pos, lens):
         """One new token per sequence: x (B, 1, D) at position lens[b] - 1 (lens (B,) int32
@@ -164,6 +185,12 @@ class GPT(nn.Module):
             return rms_norm(x, self.lnf_w, self.cfg.eps)
         return Fn.rms_norm(x, (x.shape[-1],), self.lnf_w, self.cfg.eps)
 
+    def _norm_f_add(self, x, r):
+        """Final norm of x + r (the last block's residual sum, added in the norm's pass)."""
+        if self.cfg.norm_impl == "fused":
+            return add_pre_norm(x, r, self.lnf_w, self.cfg.eps)[1]
+        return self._norm_f(x + r)
+
     def _head_w(self):
         return self.tok_emb.weight if self.cfg.tie_embeddings else self.head.weight
 
@@ -175,9 +202,10 @@ class GPT(nn.Module):
         if T > self.cfg.seq_len:
             raise ValueError(f"T={T} > seq_len={self.cfg.seq_len}")
         x = self.tok_emb(idx) + self.pos_emb[:T]
+        branch = None
         for blk in self.blocks:
-            x = blk(x)
-        x = self._norm_f(x)
+            x, branch = blk.forward_pair(x, branch)
+        x = self._norm_f_add(x, branch)
         if targets is None:
             return Fn.linear(x, self._head_w())
         if self.cfg.ce_impl == "fused":

@@ -111,6 +111,45 @@ def pre_norm(x, weight, eps=1e-6):
     return _PreNorm.apply(x, weight, float(eps))
 
 
+class _AddPreNorm(torch.autograd.Function):
+    """(s, rms_norm(s)) for s = x + r: the residual sum of ml/fxlm/model.py:69,71 done in
+    the pass of the norm that reads it (fx_rms_norm_fwd_add; s, y and rstd are bit for
+    bit those of the bf16 add followed by the norm).  Both inputs get the gradient of s,
+    formed as in _PreNorm."""
+
+    @staticmethod
+    def forward(ctx, x, r, w, eps):
+        D = _check(x, w)
+        if r.shape != x.shape or r.dtype != x.dtype or not r.is_contiguous():
+            raise ValueError(f"r must be a contiguous {tuple(x.shape)} {x.dtype} tensor")
+        N = x.numel() // D
+        x2 = x.view(N, D)
+        s = torch.empty_like(x2)
+        y = torch.empty_like(x2)
+        rstd = torch.empty(N, device=x.device, dtype=torch.float32)
+        call("fx_rms_norm_fwd_add", ptr(x2), ptr(r), ptr(w), ptr(s), ptr(y), ptr(rstd), N, D, float(eps),
+             stream_of(x))
+        ctx.save_for_backward(s, w, rstd)
+        ctx.oshape = x.shape
+        ctx.set_materialize_grads(False)
+        return s.view(x.shape), y.view(x.shape)
+
+    @staticmethod
+    def backward(ctx, ds, dy):
+        s, w, rstd = ctx.saved_tensors
+        if dy is None:
+            return ds, ds, None, None
+        dx, dw = _bwd_into(s, dy, w, rstd, ds)
+        dx = dx.view(ctx.oshape)
+        return dx, dx, dw, None
+
+
+def add_pre_norm(x, r, weight, eps=1e-6):
+    """(x + r, rms_norm(x + r, weight, eps)) in one pass over x and r; the backward is
+    pre_norm's, with the gradient of the sum going to both x and r."""
+    return _AddPreNorm.apply(x, r, weight, float(eps))
+
+
 def rms_norm_fwd_stats(x, weight, eps=1e-6):
     """Forward only, returning (y, rstd): the fp32 per-row rstd for parity checks."""
     D = _check(x, weight)

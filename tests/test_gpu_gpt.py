@@ -287,3 +287,28 @@ def test_head_dim_128_model(dev):
         ref = [m_f(x[:, :t + 1])[:, -1, :].float() for t in range(29, 39)]
     for a, r in zip(got, ref):
         assert float((a - r).abs().max()) <= 3e-2 * max(1.0, float(r.abs().max()))
+
+
+def test_deferred_residual_sums_bitwise(dev):
+    # GPT.forward adds each block's last residual sum inside the next norm
+    # (fx_rms_norm_fwd_add); loss and gradients equal the per-block x + out chain bit for bit
+    from fxlm.cross_entropy import linear_cross_entropy
+    from fxlm.model import GPT
+    torch.manual_seed(5)
+    model = GPT(_cfg()).to(dev).bfloat16()
+    idx = torch.randint(0, 256, (2, 64), device=dev)
+    tgt = torch.randint(0, 256, (2, 64), device=dev)
+    loss_a = model(idx, tgt)
+    loss_a.backward()
+    ga = [p.grad.clone() for p in model.parameters()]
+    model.zero_grad(set_to_none=True)
+    x = model.tok_emb(idx) + model.pos_emb[:64]
+    for blk in model.blocks:
+        x = blk(x)
+    x = model._norm_f(x)
+    loss_b = linear_cross_entropy(x.reshape(-1, x.shape[-1]), model._head_w(), tgt.reshape(-1))
+    loss_b.backward()
+    torch.cuda.synchronize()
+    assert torch.equal(loss_a, loss_b)
+    for a, p in zip(ga, model.parameters()):
+        assert torch.equal(a, p.grad)

@@ -134,3 +134,43 @@ def test_pre_norm_autograd(dev):
     x3, w3 = x0.clone().requires_grad_(), w0.clone().requires_grad_()
     rms_norm(x3, w3).backward(gy)
     assert torch.equal(x2.grad, x3.grad) and torch.equal(w2.grad, w3.grad)
+
+
+@pytest.mark.parametrize("N,D", [(129, 768), (300, 8192), (64, 2056), (5, 96)])
+def test_fwd_add_is_add_then_norm(dev, N, D):
+    # fx_rms_norm_fwd_add: the sum rounds like torch's bf16 add and y / rstd are the
+    # plain forward's on that sum, bit for bit
+    from fxlm.norm import add_pre_norm, rms_norm_fwd_stats
+    torch.manual_seed(N + D)
+    x = torch.randn(N, D, device=dev).bfloat16()
+    r = torch.randn(N, D, device=dev).bfloat16()
+    w = (1 + 0.1 * torch.randn(D, device=dev)).bfloat16()
+    s, y = add_pre_norm(x, r, w)
+    s_ref = x + r
+    y_ref, _ = rms_norm_fwd_stats(s_ref, w)
+    torch.cuda.synchronize()
+    assert torch.equal(s, s_ref) and torch.equal(y, y_ref)
+
+
+def test_add_pre_norm_autograd(dev):
+    # gradients equal those of the separate add followed by pre_norm, bit for bit
+    from fxlm.norm import add_pre_norm, pre_norm
+    torch.manual_seed(11)
+    N, D = 200, 768
+    x0 = torch.randn(N, D, device=dev).bfloat16()
+    r0 = torch.randn(N, D, device=dev).bfloat16()
+    w0 = (1 + 0.1 * torch.randn(D, device=dev)).bfloat16()
+    gs = torch.randn(N, D, device=dev).bfloat16()
+    gy = torch.randn(N, D, device=dev).bfloat16()
+    got, ref = [], []
+    for fused, out in ((True, got), (False, ref)):
+        x, r, w = (t.clone().requires_grad_() for t in (x0, r0, w0))
+        if fused:
+            s, y = add_pre_norm(x, r, w)
+        else:
+            s, y = pre_norm(x + r, w)
+        torch.autograd.backward([s, y], [gs, gy])
+        torch.cuda.synchronize()
+        out.extend([s.detach(), y.detach(), x.grad, r.grad, w.grad])
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b)
