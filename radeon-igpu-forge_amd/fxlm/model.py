@@ -96,7 +96,7 @@ class Block(nn.Module):
         return x + out
 
     def forward_pair(self, x, branch=None, kv=None):
-        """(x', out) with the block's output x' + out (ml/fxlm/model.py:65-72), the last
+        """(x', out) with the block's output x' + out (ml/fxlm/model.py:58-72), the last
         residual sum left to the next norm that reads it; `branch`, the previous block's
         `out`, is added to x inside this block's first norm."""
         B, T, D = x.shape
