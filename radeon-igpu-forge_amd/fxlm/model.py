@@ -186,7 +186,10 @@ class GPT(nn.Module):
         return Fn.rms_norm(x, (x.shape[-1],), self.lnf_w, self.cfg.eps)
 
     def _norm_f_add(self, x, r):
-        """Final norm of x + r (the last block's residual sum, added in the norm's pass)."""
+        """Final norm of x + r (the last block's residual sum, added in the norm's pass);
+        r is None when there are no blocks."""
+        if r is None:
+            return self._norm_f(x)
         if self.cfg.norm_impl == "fused":
             return add_pre_norm(x, r, self.lnf_w, self.cfg.eps)[1]
         return self._norm_f(x + r)

@@ -85,3 +85,4 @@ def test_lazy_exports():
         assert getattr(fxlm, name) is not None
     for name in ("FusedGatherLinear", "fused_gather_linear", "setup_env", "require_gpu"):
         assert getattr(fxgpu, name) is not None
+
