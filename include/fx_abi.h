@@ -126,6 +126,15 @@ int fx_ce_loss_finalize(const float* row_loss, int64_t N, const float* inv_n,
 int fx_ce_scale_grad(uint16_t* grad, int64_t numel, const float* g, float* applied,
                      int32_t src, void* stream);
 
+/* s = (*g) * (gs ? 1 / *gs : inv_value); dw_out = bf16(dw * s) for the fp32 (nw,) weight
+ * gradient and dx_out = bf16(dx * bf16(s)) for the bf16 (nx,) input gradient, in one pass; all
+ * four buffers 16-byte aligned.  Replaces _LinearCE.backward's reciprocal, products and
+ * cast (ml/fxlm/cross_entropy.py:141-148: gx = dx * (g * inv), gw = (dW * (g * inv)).to(dtype)),
+ * with the same fp32 roundings. */
+int fx_ce_lin_grad_scale(const float* dw, int64_t nw, const uint16_t* dx, int64_t nx, const float* g,
+                         const float* gs, float inv_value, uint16_t* dw_out, uint16_t* dx_out,
+                         void* stream);
+
 /* ---- FlatAdamW ---------------------------------------------------------- */
 
 #define FX_ADAMW_MAX_TENSORS 64

@@ -124,6 +124,10 @@ def _mm_f32(a, b):
         return torch.mm(a, b).float()
 
 
+# the backward's scaling in one kernel (fx_ce_lin_grad_scale); False: the torch ops
+_FUSED_LIN_GRAD_SCALE = True
+
+
 class _LinearCE(torch.autograd.Function):
     """loss = CE(x @ W.T, target); the (N, V) logits never exist beyond one chunk."""
 
@@ -157,6 +161,15 @@ class _LinearCE(torch.autograd.Function):
     def backward(ctx, g):
         dx, dW = ctx.saved_tensors
         gs = ctx.grad_scale
+        if _FUSED_LIN_GRAD_SCALE and ctx.wdtype == torch.bfloat16 and dx.dtype == torch.bfloat16:
+            # one pass: the same fp32 reciprocal, products and bf16 rounding as below
+            g32 = g.detach().float().reshape(())
+            gs_t = gs.detach().float().reshape(()) if torch.is_tensor(gs) else None
+            gx = torch.empty_like(dx)
+            gw = torch.empty(dW.shape, device=dW.device, dtype=torch.bfloat16)
+            call("fx_ce_lin_grad_scale", ptr(dW), dW.numel(), ptr(dx), dx.numel(), ptr(g32), ptr(gs_t),
+                 0.0 if gs_t is not None else 1.0 / gs, ptr(gw), ptr(gx), stream_of(dx))
+            return gx, gw, None, None, None, None
         inv = torch.reciprocal(gs.float()) if torch.is_tensor(gs) else 1.0 / gs
         gx = dx * (g * inv)
         gw = (dW * (g * inv)).to(ctx.wdtype)

@@ -138,3 +138,28 @@ def test_linear_ce_no_grad_path(dev):
     with torch.no_grad():
         ln = linear_cross_entropy(x, W, tg)
     assert ln.grad_fn is None and abs(float(ln) - float(lg)) < 1e-6
+
+
+@pytest.mark.parametrize("gs", ["tensor", 3.0])
+def test_linear_ce_backward_scaling_is_bitwise_torch(dev, gs):
+    # fx_ce_lin_grad_scale against the torch ops it replaces (ml/fxlm/cross_entropy.py:141-148),
+    # with a device or Python grad_scale and an incoming gradient other than 1
+    import fxlm.cross_entropy as ce
+    torch.manual_seed(8)
+    N, D, V = 301, 256, 1003
+    x0 = (torch.randn(N, D, device=dev) * 0.5).bfloat16()
+    w0 = (torch.randn(V, D, device=dev) * 0.05).bfloat16()
+    t = torch.randint(0, V, (N,), device=dev)
+    scale = torch.tensor(8.0, device=dev) if gs == "tensor" else gs
+    outs = []
+    for fused in (True, False):
+        ce._FUSED_LIN_GRAD_SCALE = fused
+        try:
+            x, w = x0.clone().requires_grad_(), w0.clone().requires_grad_()
+            loss = ce.linear_cross_entropy(x, w, t, grad_scale=scale)
+            loss.backward(torch.tensor(0.37, device=dev))
+            torch.cuda.synchronize()
+            outs.append((x.grad, w.grad))
+        finally:
+            ce._FUSED_LIN_GRAD_SCALE = True
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
