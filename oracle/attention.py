@@ -62,11 +62,6 @@ def attn_bwd(q, k, v, o, lse, do, causal=True, scale=None, dtype=torch.float64):
     return f(dq), f(dk), f(dv)
 
 
-def delta(o, do, dtype=torch.float64):
-    """Delta (B,H,T) = rowsum(dO * O)."""
-    return (_bhtd(do, dtype) * _bhtd(o, dtype)).sum(-1)
-
-
 def attn_decode(q, k_cache, v_cache, lens, scale=None, dtype=torch.float64):
     """Decode step: q (B, H, D) against the first lens[b] rows of k_cache / v_cache
     (B, Tmax, H, D).  Returns (o (B, H, D), lse (B, H)) in `dtype`: the last row of the

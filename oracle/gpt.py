@@ -2,7 +2,7 @@
 
 Restates fxlm's GPT with its plain-PyTorch implementations selected
 (ml/fxlm/model.py:22-130 with attn_impl="sdpa", norm_impl="torch",
-ce_impl="torch"; the configuration ml/fxlm/selftest.py:436-438 uses as its
+ce_impl="torch"; the configuration ml/fxlm/selftest.py:305-308 uses as its
 comparator) and the baseline optimiser loop of ml/bench/bench10_lm.py:92-111
 (AdamW with weight decay on ndim >= 2 parameters, clip_grad_norm_(1.0)).
 Pre-norm blocks, no biases, GELU-tanh MLP, tied LM head, init N(0, 0.02) with
@@ -56,13 +56,17 @@ class GPT(nn.Module):
             nn.init.normal_(b.proj.weight, std=s)
             nn.init.normal_(b.fc2.weight, std=s)
 
-    def forward(self, idx, targets):
+    def forward(self, idx, targets=None):
+        """Mean CE over every position, or the logits (B, T, V) without targets
+        (ml/fxlm/model.py:114-130)."""
         T = idx.shape[1]
         x = self.tok_emb(idx) + self.pos_emb[:T]
         for blk in self.blocks:
             x = blk(x)
         x = F.rms_norm(x, (x.shape[-1],), self.lnf_w, self.eps)
         logits = F.linear(x, self.tok_emb.weight)
+        if targets is None:
+            return logits
         return F.cross_entropy(logits.float().view(-1, logits.shape[-1]), targets.reshape(-1))
 
 

@@ -376,10 +376,12 @@ static int64_t bwd_blocks(int64_t ngroups) {
 
 using namespace fx;
 
+// x and w are read as 16-byte vectors: both must be 16-byte aligned
 static int norm_check(const void* x, const void* w, int64_t N, int32_t D, const char* who) {
     FX_REQUIRE((N == 0 || x != nullptr) && w != nullptr, "%s: null pointer", who);
     FX_REQUIRE(N >= 0, "%s: N=%lld < 0", who, (long long)N);
     FX_REQUIRE(D >= 8 && D <= 8192 && D % 8 == 0, "%s: D=%d needs D%%8==0 and 8<=D<=8192", who, D);
+    FX_REQUIRE(((((uintptr_t)x) | ((uintptr_t)w)) & 15) == 0, "%s: x and w must be 16-byte aligned", who);
     return 0;
 }
 
@@ -388,6 +390,7 @@ extern "C" int fx_rms_norm_fwd(const uint16_t* x, const uint16_t* w, uint16_t* y
     if (int e = norm_check(x, w, N, D, "fx_rms_norm_fwd")) return e;
     if (N == 0) return 0;
     FX_REQUIRE(y != nullptr && rstd != nullptr, "fx_rms_norm_fwd: null output");
+    FX_REQUIRE(((uintptr_t)y & 15) == 0, "fx_rms_norm_fwd: y must be 16-byte aligned");
     const RowShape s = pick_shape(D);
     const int G = 256 / s.lpr;
     const int64_t blocks = (N + G - 1) / G;
@@ -434,7 +437,8 @@ static int rms_norm_bwd(const uint16_t* x, const uint16_t* dy, const uint16_t* d
                "%s: dw_f32 and work must be 16-byte aligned, dw 8-byte aligned", who);
     FX_REQUIRE(N == 0 || (dy != nullptr && rstd != nullptr && dx != nullptr),
                "%s: null pointer", who);
-    FX_REQUIRE(((uintptr_t)dres & 15) == 0, "%s: dres must be 16-byte aligned", who);
+    FX_REQUIRE(((((uintptr_t)dy) | ((uintptr_t)dx) | ((uintptr_t)dres)) & 15) == 0,
+               "%s: dy, dx and dres must be 16-byte aligned", who);
     if (N == 0) {
         // dw of an empty batch is zero
         hipLaunchKernelGGL(rms_dw_reduce_kernel, dim3((D + 7) / 8), dim3(256), 0,

@@ -90,19 +90,31 @@ class _FusedCE(torch.autograd.Function):
             grad = torch.empty(N, V, device=dev, dtype=torch.bfloat16)
         _ce_rows(logits, target, grad, row_loss, mul, ignore_index)
         ctx.save_for_backward(grad)
-        # multiplier already in grad: slot ctx.src of two (the kernel writes the other)
+        # applied[0] = 1: the multiplier in grad as written; the first backward's kernel
+        # stores its g in applied[1]
         ctx.applied = torch.ones(2, device=dev, dtype=torch.float32)
-        ctx.src = 0
+        ctx.calls = 0
         return _finalize(row_loss, inv_n)
 
     @staticmethod
     def backward(ctx, g):
         (grad,) = ctx.saved_tensors
         g32 = g.detach().to(torch.float32).reshape(()).contiguous()
-        call("fx_ce_scale_grad", ptr(grad), grad.numel(), ptr(g32), ptr(ctx.applied), ctx.src,
-             stream_of(grad))
-        ctx.src ^= 1
-        return grad, None, None
+        ctx.calls += 1
+        if ctx.calls == 1:
+            # the usual single backward: scale the saved dlogits in place (no pass at all
+            # when g == 1) and hand them over
+            call("fx_ce_scale_grad", ptr(grad), grad.numel(), ptr(g32), ptr(ctx.applied), 0,
+                 stream_of(grad))
+            return grad, None, None
+        # a further backward through a retained graph: a fresh tensor, so the gradient the
+        # first backward returned stays as it was
+        prev = float(ctx.applied[1])
+        if prev == 0.0:
+            raise RuntimeError("fused_cross_entropy: the first backward of this graph had an "
+                               "incoming gradient of 0, which zeroed the saved dlogits; run the "
+                               "forward again")
+        return (grad.float() * (g32 / prev)).to(torch.bfloat16), None, None
 
 
 def fused_cross_entropy(logits, target, ignore_index=-100):
@@ -111,17 +123,16 @@ def fused_cross_entropy(logits, target, ignore_index=-100):
 
 
 def _auto_chunk(D, V):
-    """Rows per chunk so that one chunk's bf16 logits stay within _CHUNK_BYTES."""
+    """Rows per chunk so that one chunk's bf16 logits stay within _CHUNK_BYTES.
+
+    The reference sizes chunks for a shared-memory iGPU: at most 4096 rows and
+    2.5e10 / (D V) (ml/fxlm/cross_entropy.py:102-104; 512 rows at D 768, V 50304).
+    With 288 GB of HBM the limit here is 2 GiB of logits (21,248 rows at V 50304), so
+    the 16,384-row batch of the 12-layer model is one chunk: 1.65 GB of logits, three
+    large GEMMs, and one pass over the fp32 (V, D) weight-gradient accumulator instead
+    of 32 passes (154 MB each) at the reference's chunking."""
     c = (_CHUNK_BYTES // (2 * max(1, V))) // 256 * 256
     return max(256, c)
-
-
-def _mm_f32(a, b):
-    """a @ b with fp32 output from bf16 operands (fp32 accumulation in the GEMM)."""
-    try:
-        return torch.mm(a, b, out_dtype=torch.float32)
-    except (RuntimeError, TypeError):
-        return torch.mm(a, b).float()
 
 
 # the backward's scaling in one kernel (fx_ce_lin_grad_scale); False: the torch ops
@@ -147,8 +158,10 @@ class _LinearCE(torch.autograd.Function):
             lg = torch.mm(xc, weight.t())                       # (C, V) bf16
             _ce_rows(lg, target[r0:r1], lg, row_loss[r0:r1], mul, ignore_index)  # in place
             torch.mm(lg, weight, out=dx[r0:r1])                 # dx_c
-            part = _mm_f32(lg.t(), xc)                          # (V, D) fp32
-            dW = part if dW is None else dW.add_(part)
+            # the reference's dW.add_(torch.mm(dl.t(), xc).float()): a bf16 product,
+            # accumulated over the chunks in fp32 (ml/fxlm/cross_entropy.py:135)
+            part = torch.mm(lg.t(), xc)                         # (V, D) bf16
+            dW = part.float() if dW is None else dW.add_(part)
             del lg
         if dW is None:
             dW = torch.zeros(V, D, device=dev, dtype=torch.float32)

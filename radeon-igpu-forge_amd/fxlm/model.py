@@ -325,9 +325,11 @@ class _DecodeGraph:
         with torch.no_grad():
             # warm-up off the capture (library handles, workspaces), as torch requires;
             # position 0 only rewrites a cache row the real prompt fills again
+            # copies of the cache rows the warm-up writes, queued before the side stream
+            # waits on the current one: the warm-up then runs after them
+            saved = [(k[:, :1].clone(), v[:, :1].clone()) for k, v in cache]
             s = torch.cuda.Stream(device=dev)
             s.wait_stream(torch.cuda.current_stream(dev))
-            saved = [(k[:, :1].clone(), v[:, :1].clone()) for k, v in cache]
             with torch.cuda.stream(s):
                 for _ in range(2):
                     model._decode(self.tok, cache, self.pos, self.lens)

@@ -26,12 +26,20 @@ def _check(x, w):
     return D
 
 
+def _al(t):
+    """t itself when its data is 16-byte aligned (the kernels read 16-byte vectors), else
+    an aligned copy: a contiguous view at an odd storage offset is accepted, as the
+    reference accepts any contiguous tensor."""
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 class _RMSNorm(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, w, eps):
         D = _check(x, w)
+        w = _al(w)
         N = x.numel() // D
-        x2 = x.view(N, D)
+        x2 = _al(x.view(N, D))
         y = torch.empty_like(x2)
         rstd = torch.empty(N, device=x.device, dtype=torch.float32)
         call("fx_rms_norm_fwd", ptr(x2), ptr(w), ptr(y), ptr(rstd), N, D, float(eps),
@@ -56,7 +64,7 @@ def rms_norm(x, weight, eps=1e-6):
 def _bwd_into(x2, dy, w, rstd, dres=None):
     """(dx, dw) of the norm for x2 (N, D); dx += dres in the same pass when given."""
     N, D = x2.shape
-    dy2 = dy.contiguous().view(N, D)
+    dy2 = _al(dy.contiguous().view(N, D))
     if dy2.dtype != torch.bfloat16:
         dy2 = dy2.to(torch.bfloat16)
     dx = torch.empty_like(x2)
@@ -68,7 +76,7 @@ def _bwd_into(x2, dy, w, rstd, dres=None):
         call("fx_rms_norm_bwd", ptr(x2), ptr(dy2), ptr(w), ptr(rstd), ptr(dx), ptr(dw32),
              ptr(dw), ptr(work), N, D, stream_of(x2))
     else:
-        r2 = dres.contiguous().view(N, D)
+        r2 = _al(dres.contiguous().view(N, D))
         if r2.dtype != torch.bfloat16:
             r2 = r2.to(torch.bfloat16)
         call("fx_rms_norm_bwd_add", ptr(x2), ptr(dy2), ptr(r2), ptr(w), ptr(rstd), ptr(dx),
@@ -85,8 +93,9 @@ class _PreNorm(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, w, eps):
         D = _check(x, w)
+        w = _al(w)
         N = x.numel() // D
-        x2 = x.view(N, D)
+        x2 = _al(x.view(N, D))
         y = torch.empty_like(x2)
         rstd = torch.empty(N, device=x.device, dtype=torch.float32)
         call("fx_rms_norm_fwd", ptr(x2), ptr(w), ptr(y), ptr(rstd), N, D, float(eps),
@@ -122,8 +131,9 @@ class _AddPreNorm(torch.autograd.Function):
         D = _check(x, w)
         if r.shape != x.shape or r.dtype != x.dtype or not r.is_contiguous():
             raise ValueError(f"r must be a contiguous {tuple(x.shape)} {x.dtype} tensor")
+        w, r = _al(w), _al(r)
         N = x.numel() // D
-        x2 = x.view(N, D)
+        x2 = _al(x.view(N, D))
         s = torch.empty_like(x2)
         y = torch.empty_like(x2)
         rstd = torch.empty(N, device=x.device, dtype=torch.float32)
@@ -153,8 +163,9 @@ def add_pre_norm(x, r, weight, eps=1e-6):
 def rms_norm_fwd_stats(x, weight, eps=1e-6):
     """Forward only, returning (y, rstd): the fp32 per-row rstd for parity checks."""
     D = _check(x, weight)
+    weight = _al(weight)
     N = x.numel() // D
-    x2 = x.view(N, D)
+    x2 = _al(x.view(N, D))
     y = torch.empty_like(x2)
     rstd = torch.empty(N, device=x.device, dtype=torch.float32)
     call("fx_rms_norm_fwd", ptr(x2), ptr(weight), ptr(y), ptr(rstd), N, D, float(eps),
@@ -165,8 +176,9 @@ def rms_norm_fwd_stats(x, weight, eps=1e-6):
 def rms_norm_bwd_raw(x, dy, weight, rstd):
     """Backward only, returning (dx, dw_f32, dw_bf16) for parity checks."""
     D = _check(x, weight)
+    weight = _al(weight)
     N = x.numel() // D
-    x2, dy2 = x.view(N, D), dy.contiguous().view(N, D)
+    x2, dy2 = _al(x.view(N, D)), _al(dy.contiguous().view(N, D))
     dx = torch.empty_like(x2)
     dw32 = torch.empty(D, device=x.device, dtype=torch.float32)
     dw = torch.empty(D, device=x.device, dtype=torch.bfloat16)

@@ -100,6 +100,24 @@ def test_argument_checks_reject_before_launch(abi):
     assert lib.fx_rms_norm_bwd_workspace(0, 768) == 0
 
 
+def test_rms_norm_rejects_misaligned_vectors(abi):
+    # x / w / y / dy / dx are read and written as 16-byte vectors: an address that is
+    # only 2-byte aligned is rejected before any launch (never dereferenced)
+    lib = abi.lib()
+    ok, odd = ctypes.c_void_p(4096), ctypes.c_void_p(4096 + 2)
+    for args in ((odd, ok, ok), (ok, odd, ok), (ok, ok, odd)):
+        x, w, y = args
+        assert lib.fx_rms_norm_fwd(x, w, y, ok, 4, 64, 1e-6, None) == abi.FX_EINVAL
+        assert b"16-byte aligned" in lib.fx_last_error()
+    for i in range(4):   # x, dy, w, dx
+        p = [ok, ok, ok, ok]
+        p[i] = odd
+        x, dy, w, dx = p
+        assert lib.fx_rms_norm_bwd(x, dy, w, ok, dx, ok, ok, ok, 4, 64, None) == abi.FX_EINVAL
+        assert b"16-byte aligned" in lib.fx_last_error()
+        assert lib.fx_rms_norm_bwd_add(x, dy, ok, w, ok, dx, ok, ok, ok, 4, 64, None) == abi.FX_EINVAL
+
+
 def test_adamw_workspace_counts_chunks(abi):
     tl = abi.fxTensorList()
     tl.count = 3

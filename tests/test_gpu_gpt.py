@@ -1,5 +1,7 @@
 """End-to-end GPT on the GPU: fused kernels vs the plain-PyTorch paths, and learning
 with FlatAdamW (ml/fxlm/selftest.py:301-352), plus the loader smoke kernels."""
+import math
+
 import pytest
 import torch
 
@@ -86,6 +88,85 @@ def test_fused_vs_torch_paths(dev):
         ef = float((p.grad.float().cpu() - rp[name].grad).abs().max())
         et = float((tp[name].grad.float() - rp[name].grad).abs().max())
         assert ef <= 2 * et + 1e-3, name
+
+
+def _rule_ok(ours, ref32, torch16):
+    """The reference's parity rule (ml/fxlm/selftest.py:49-53): our error against fp32 is at
+    most twice the plain-PyTorch half-precision error plus 1e-3."""
+    e_our = float((ours.float().cpu() - ref32.float()).abs().max())
+    e_t16 = float((torch16.float().cpu() - ref32.float()).abs().max())
+    return e_our <= 2 * e_t16 + 1e-3, e_our, e_t16
+
+
+def _parity_vs_oracle(dev, V, T, L, H, D, B, seed):
+    """The HIP GPT in bf16 on the GPU, the oracle's naive-PyTorch GPT in fp32 (reference)
+    and in bf16 (error bar) on the CPU, on one state_dict and one batch; loss and every
+    parameter gradient under the reference's rule."""
+    from fxlm.model import GPT, GPTConfig
+    from oracle import gpt as ogpt
+    torch.manual_seed(seed)
+    m_f = GPT(GPTConfig(vocab_size=V, seq_len=T, n_layer=L, n_head=H, d_model=D))
+    m_r = ogpt.GPT(vocab_size=V, seq_len=T, n_layer=L, n_head=H, d_model=D)
+    m_t = ogpt.GPT(vocab_size=V, seq_len=T, n_layer=L, n_head=H, d_model=D)
+    m_r.load_state_dict(m_f.state_dict())
+    m_t.load_state_dict(m_f.state_dict())
+    m_f = m_f.to(dev).bfloat16()
+    m_t = m_t.bfloat16()
+    idx = torch.randint(0, V, (B, T))
+    tgt = torch.randint(0, V, (B, T))
+    l_f = m_f(idx.to(dev), tgt.to(dev), grad_scale=1.0)
+    l_f.backward()
+    l_r, l_t = m_r(idx, tgt), m_t(idx, tgt)
+    l_r.backward()
+    l_t.backward()
+    ok, e, et = _rule_ok(l_f.detach(), l_r.detach(), l_t.detach())
+    assert ok, ("loss", e, et)
+    assert abs(float(l_r) - math.log(V)) < 0.5        # N(0, 0.02) init: near-uniform logits
+    rp, tp = dict(m_r.named_parameters()), dict(m_t.named_parameters())
+    for name, p in m_f.named_parameters():
+        assert bool(torch.isfinite(p.grad).all()), name
+        ok, e, et = _rule_ok(p.grad, rp[name].grad, tp[name].grad)
+        assert ok, (name, e, et)
+
+
+def test_cfg1_gpt_vs_oracle(dev):
+    # cfg1: 4 layers, d_model 256, 4 heads of 64, V 256, T 256, batch 32
+    _parity_vs_oracle(dev, V=256, T=256, L=4, H=4, D=256, B=32, seed=1)
+
+
+def test_cfg5_gpt_vs_oracle_batch2(dev):
+    # the 12-layer cfg5 model (V 50304, D 768, H 12, T 1024) at batch 2, full width and depth
+    _parity_vs_oracle(dev, V=50304, T=1024, L=12, H=12, D=768, B=2, seed=5)
+
+
+def test_cfg5_train_step(dev):
+    # one cfg5 step as bench.py times it (B 16, T 1024, FlatAdamW of the cfg4 settings):
+    # initial loss near ln V, no skipped step, finite gradients, and a second step on the
+    # same batch lowers the loss
+    from fxlm.model import GPT, GPTConfig
+    from fxlm.optim import FlatAdamW
+    torch.manual_seed(0)
+    V = 50304
+    m = GPT(GPTConfig(vocab_size=V, seq_len=1024, n_layer=12, n_head=12, d_model=768)).to(dev)
+    opt = FlatAdamW(m, lr=6e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+    assert opt.master.numel() == 124_373_760
+    g = torch.Generator(device=dev).manual_seed(1234)
+    idx = torch.randint(0, V, (16, 1024), device=dev, generator=g)
+    tgt = torch.randint(0, V, (16, 1024), device=dev, generator=g)
+    losses = []
+    for _ in range(2):
+        loss = m(idx, tgt, grad_scale=opt.scale)
+        opt.backward(loss)
+        for name, p in m.named_parameters():
+            assert p.grad is not None and bool(torch.isfinite(p.grad).all()), name
+        stats = opt.step(lr=6e-4)
+        opt.zero_grad()
+        assert float(stats["found_inf"]) == 0.0
+        assert math.isfinite(float(stats["grad_norm"])) and float(stats["grad_norm"]) > 0
+        losses.append(float(loss.detach()))
+    assert abs(losses[0] - math.log(V)) < 0.3
+    assert losses[1] < losses[0]
+    assert torch.equal(opt.flat16, opt.master.bfloat16())
 
 
 def test_twenty_steps_learn(dev):
@@ -194,6 +275,23 @@ def test_decode_graph_replays_match_eager(dev):
             assert torch.equal(k[:, :t + 1], rk[:, :t + 1]) and torch.equal(v[:, :t + 1], rv[:, :t + 1])
     with pytest.raises(ValueError):
         step(x[:, 0], T0 + n)
+
+
+def test_decode_graph_capture_keeps_the_prefilled_cache(dev):
+    # the capture's warm-up writes cache row 0; decode_graph() restores it, so the prefilled
+    # cache is bitwise unchanged afterwards
+    m = _bf16_model(dev)
+    g = torch.Generator(device=dev).manual_seed(12)
+    B, T0 = 4, 17
+    x = torch.randint(0, 512, (B, T0), device=dev, generator=g)
+    cache = m.init_cache(B, T0 + 4)
+    with torch.no_grad():
+        m.prefill(x, cache)
+    before = [(k[:, :T0].clone(), v[:, :T0].clone()) for k, v in cache]
+    m.decode_graph(cache, B)
+    torch.cuda.synchronize()
+    for (k, v), (k0, v0) in zip(cache, before):
+        assert torch.equal(k[:, :T0], k0) and torch.equal(v[:, :T0], v0)
 
 
 def test_generate_graph_equals_eager(dev):

@@ -174,3 +174,27 @@ def test_add_pre_norm_autograd(dev):
         out.extend([s.detach(), y.detach(), x.grad, r.grad, w.grad])
     for a, b in zip(got, ref):
         assert torch.equal(a, b)
+
+
+def test_misaligned_views_are_accepted(dev):
+    # contiguous views at a 2-byte storage offset (the reference accepts any contiguous
+    # tensor): the wrappers hand the kernels aligned copies; results equal the aligned run
+    from fxlm.norm import add_pre_norm, rms_norm
+    torch.manual_seed(21)
+    N, D = 37, 256
+    base = torch.randn(N * D + 1, device=dev).bfloat16()
+    x_odd = base[1:].view(N, D)
+    assert x_odd.is_contiguous() and x_odd.data_ptr() % 16 != 0
+    wbase = (torch.randn(D + 1, device=dev) * 0.3 + 1).bfloat16()
+    w_odd = wbase[1:]
+    dy = torch.randn(N, D, device=dev).bfloat16()
+    outs = []
+    for x, w in ((x_odd, w_odd), (x_odd.clone(), w_odd.clone())):
+        xr, wr = x.detach().requires_grad_(), w.detach().requires_grad_()
+        y = rms_norm(xr, wr)
+        y.backward(dy)
+        s, y2 = add_pre_norm(x, x, w)
+        outs.append((y, xr.grad, wr.grad, s, y2))
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)

@@ -279,6 +279,154 @@ def test_linear_gelu_matches_autograd():
 
 # ---------------------------------------------------------------- GPT (CPU baseline model)
 
+def _tiny_gpt(V=64, T=16, L=2, H=2, D=32, seed=0, dtype=f64):
+    torch.manual_seed(seed)
+    return ogpt.GPT(vocab_size=V, seq_len=T, n_layer=L, n_head=H, d_model=D).to(dtype)
+
+
+def _rms(x, w, eps=1e-6):
+    """RMSNorm from its definition: x / sqrt(mean(x^2) + eps) * w."""
+    return x / torch.sqrt((x * x).mean(-1, keepdim=True) + eps) * w
+
+
+def _gelu_tanh(u):
+    """GELU with the tanh approximation, from its formula."""
+    return 0.5 * u * (1.0 + torch.tanh(math.sqrt(2.0 / math.pi) * (u + 0.044715 * u ** 3)))
+
+
+@pytest.mark.parametrize("V,T,L,H,D", [(256, 256, 4, 4, 256), (50304, 1024, 12, 12, 768)])
+def test_cpu_gpt_param_count_closed_form(V, T, L, H, D):
+    # tied head, no biases: V*D (embedding = head) + T*D (positions) + L*(2D norms +
+    # 3D^2 qkv + D^2 proj + 4D^2 fc + 4D^2 fc2) + D (final norm); an untied head adds V*D
+    with torch.device("meta"):
+        m = ogpt.GPT(vocab_size=V, seq_len=T, n_layer=L, n_head=H, d_model=D)
+    n = sum(p.numel() for p in m.parameters())
+    assert n == V * D + T * D + L * (2 * D + 12 * D * D) + D
+    if V == 50304:
+        assert n == 124_373_760
+
+
+def test_cpu_gpt_init_scales():
+    # ml/fxlm/model.py:88-99: N(0, 0.02) everywhere, proj / fc2 at 0.02 / sqrt(2 L);
+    # norm weights one, positions zero
+    L = 4
+    m = ogpt.GPT(vocab_size=512, seq_len=64, n_layer=L, n_head=4, d_model=256)
+    small = 0.02 / math.sqrt(2 * L)
+    for name, p in m.named_parameters():
+        if name.endswith(("proj.weight", "fc2.weight")):
+            want = small
+        elif name.endswith(("qkv.weight", "fc.weight")) or name == "tok_emb.weight":
+            want = 0.02
+        elif name == "pos_emb":
+            assert float(p.detach().abs().max()) == 0.0
+            continue
+        else:
+            assert torch.equal(p, torch.ones_like(p)), name
+            continue
+        assert abs(float(p.std()) / want - 1) < 0.03, name
+        assert abs(float(p.mean())) < 0.1 * want, name
+
+
+def test_cpu_gpt_block_from_definitions():
+    # one block restated from its definitions: pre-norm, causal attention (the pinned
+    # attention oracle), both residual sums, GELU-tanh MLP (ml/fxlm/model.py:58-72)
+    m = _tiny_gpt(L=1)
+    blk = m.blocks[0]
+    for p in blk.parameters():
+        torch.nn.init.normal_(p, std=0.3)
+    x = torch.randn(3, 16, 32, dtype=f64)
+    H, Dh = 2, 16
+    h = _rms(x, blk.ln1_w)
+    qkv = (h @ blk.qkv.weight.T).view(3, 16, 3, H, Dh)
+    o, _ = oatt.attn_fwd(qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], True, Dh ** -0.5)
+    x1 = x + o.reshape(3, 16, 32) @ blk.proj.weight.T
+    want = x1 + _gelu_tanh(_rms(x1, blk.ln2_w) @ blk.fc.weight.T) @ blk.fc2.weight.T
+    with torch.no_grad():
+        got = blk(x)
+    assert torch.allclose(got, want, atol=1e-12, rtol=1e-12)
+
+
+def test_cpu_gpt_zero_branches_are_identity():
+    # with proj and fc2 at zero every block returns its input exactly, and the logits are
+    # rms_norm(emb + pos) * lnf_w times the (tied) embedding
+    m = _tiny_gpt()
+    with torch.no_grad():
+        for b in m.blocks:
+            b.proj.weight.zero_()
+            b.fc2.weight.zero_()
+        torch.nn.init.normal_(m.pos_emb, std=0.5)
+        torch.nn.init.normal_(m.lnf_w, mean=1.0, std=0.2)
+        idx = torch.randint(0, 64, (2, 16))
+        x = m.tok_emb(idx) + m.pos_emb[:16]
+        for b in m.blocks:
+            assert torch.equal(b(x), x)
+        want = _rms(x, m.lnf_w) @ m.tok_emb.weight.T
+        assert torch.allclose(m(idx), want, atol=1e-12, rtol=1e-12)
+
+
+def test_cpu_gpt_is_causal():
+    # changing the tokens after position t leaves the logits at positions <= t unchanged,
+    # and changing the token at t changes the logits at t
+    m = _tiny_gpt(L=2)
+    idx = torch.randint(0, 64, (2, 16))
+    with torch.no_grad():
+        base = m(idx)
+        for t in (0, 5, 14):
+            alt = idx.clone()
+            alt[:, t + 1:] = (alt[:, t + 1:] + 7) % 64
+            out = m(alt)
+            assert torch.allclose(out[:, :t + 1], base[:, :t + 1], atol=1e-12, rtol=0)
+            if t + 1 < 16:
+                assert not torch.allclose(out[:, t + 1], base[:, t + 1])
+            alt2 = idx.clone()
+            alt2[:, t] = (alt2[:, t] + 3) % 64
+            assert not torch.allclose(m(alt2)[:, t], base[:, t])
+
+
+def test_cpu_gpt_gradients_match_finite_differences():
+    # fp64 gradcheck of the logits over every parameter of a tiny model (the loss path
+    # casts the logits to fp32, as the reference does, so it is checked through them)
+    m = _tiny_gpt(V=16, T=6, L=1, H=2, D=8, seed=3)
+    with torch.no_grad():
+        for p in m.parameters():
+            p.copy_(torch.randn_like(p) * 0.4 + (1.0 if p.dim() == 1 else 0.0))
+    idx = torch.randint(0, 16, (2, 6))
+    names = [n for n, _ in m.named_parameters()]
+    params = tuple(p.detach().clone().requires_grad_() for p in m.parameters())
+
+    def logits_of(*ps):
+        return torch.func.functional_call(m, dict(zip(names, ps)), (idx,))
+
+    assert torch.autograd.gradcheck(logits_of, params, eps=1e-6, atol=1e-7, rtol=1e-5)
+
+
+def test_cpu_gpt_matches_fxlm_torch_path():
+    # the oracle and fxlm.model.GPT with the reference's torch comparator switches
+    # (ml/fxlm/selftest.py:305-308) on one state_dict: equal fp32 loss and gradients
+    from fxlm.model import GPT as FxGPT, GPTConfig
+    cfg = GPTConfig(vocab_size=96, seq_len=24, n_layer=2, n_head=2, d_model=64,
+                    attn_impl="sdpa", norm_impl="torch", ce_impl="torch", mlp_impl="torch",
+                    linear_impl="torch")
+    torch.manual_seed(11)
+    fx = FxGPT(cfg)
+    m = ogpt.GPT(vocab_size=96, seq_len=24, n_layer=2, n_head=2, d_model=64)
+    m.load_state_dict(fx.state_dict())
+    with torch.no_grad():
+        for p in fx.parameters():       # larger branches than the init gives
+            p.add_(torch.randn_like(p) * 0.05)
+        m.load_state_dict(fx.state_dict())
+    idx = torch.randint(0, 96, (3, 24))
+    tgt = torch.randint(0, 96, (3, 24))
+    l_fx, l_o = fx(idx, tgt), m(idx, tgt)
+    l_fx.backward()
+    l_o.backward()
+    assert abs(float(l_fx) - float(l_o)) <= 1e-6 * abs(float(l_o))
+    op = dict(m.named_parameters())
+    for name, p in fx.named_parameters():
+        r = op[name].grad
+        assert torch.allclose(p.grad, r, atol=1e-6 * float(r.abs().max()) + 1e-9, rtol=1e-4), name
+
+
 def test_cpu_gpt_initial_loss_and_learning():
     torch.manual_seed(0)
     m = ogpt.GPT(vocab_size=256, seq_len=32, n_layer=2, n_head=2, d_model=64)
