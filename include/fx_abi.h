@@ -7,7 +7,8 @@
  *   - bf16 tensors are passed as uint16_t* holding IEEE bfloat16 bit patterns.
  *   - `stream` is a hipStream_t passed as void* (torch.cuda.current_stream().cuda_stream).
  *   - Every entry point only enqueues work on `stream`; none synchronises and none
- *     allocates device memory.  Workspace buffers are owned by the caller.
+ *     allocates device memory.  Workspace buffers are owned by the caller, except for
+ *     fx_adamw_step_noalloc, whose workspace is a fixed buffer inside the library.
  *   - Return value: 0 on success, FX_EINVAL when an argument check fails, otherwise
  *     the hipError_t of the failed HIP call.  fx_last_error() gives a message.
  *
@@ -184,6 +185,22 @@ int64_t fx_adamw_workspace(const fxTensorList* lists, int32_t nlists);
  * ml/fxlm/kernels/optim.hip:25-162). */
 int fx_adamw_step(const fxAdamWState* state, const fxTensorList* lists, int32_t nlists,
                   void* stream);
+
+/* Bytes of the buffer inside the library that fx_adamw_step_noalloc uses as its workspace:
+ * 16 bytes of header plus 4 bytes per 8192-element chunk, so at most
+ * (FX_ADAMW_NOALLOC_SCRATCH_BYTES / 4 - 4) * 8192 = 2,147,450,880 parameters per call. */
+#define FX_ADAMW_NOALLOC_SCRATCH_BYTES (1 << 20)
+
+/* fx_adamw_step with no workspace argument and no allocation: state->work is ignored and
+ * the step's partial sums live in a device buffer inside the library, one per GPU (held
+ * until the process ends; FX_ADAMW_NOALLOC_SCRATCH_BYTES).  Lists needing more return
+ * FX_EINVAL before any launch.  Calls that overlap on one GPU (concurrent streams or host
+ * threads) share that buffer and race; calls in stream order do not.  The buffer's device
+ * address is looked up on the first call on each device.
+ * No counterpart in the reference: it is for callers that cannot allocate device memory
+ * (HIP graph capture of a training step, serving loops, allocation-free harnesses). */
+int fx_adamw_step_noalloc(const fxAdamWState* state, const fxTensorList* lists, int32_t nlists,
+                          void* stream);
 
 /* ---- flash attention ------------------------------------------------------ */
 

@@ -13,6 +13,8 @@
 // reference's separate flag word did (ml/fxlm/kernels/optim.hip:44-51, :85-91).
 #include <math.h>
 
+#include <mutex>
+
 #include "fx_device.h"
 
 namespace fx {
@@ -235,6 +237,37 @@ static int build_chunks(const fxTensorList& in, int32_t pbase, ChunkList& out, i
     return 0;
 }
 
+// Workspace of fx_adamw_step_noalloc: a file-scope device array (one copy per GPU, held
+// until the process ends).  In host code `scratch` names a host-side stand-in, not device
+// memory: the kernels get the device address hipGetSymbolAddress returns for the
+// current device, looked up once per device and kept.  The step writes every word it
+// reads (the sum-of-squares kernel writes each chunk's partial, the final kernel the
+// header) before reading it, so nothing needs clearing between calls.
+static __device__ __align__(256) float scratch[FX_ADAMW_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static float* g_scratch[kMaxDevices];
+
+static int scratch_ptr(float** out, const char* who) {
+    int dev = -1;
+    const hipError_t e = hipGetDevice(&dev);
+    FX_REQUIRE(e == hipSuccess, "%s: hipGetDevice failed (%s)", who, hipGetErrorString(e));
+    FX_REQUIRE(dev >= 0 && dev < kMaxDevices, "%s: device %d beyond the %d supported", who, dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch[dev] == nullptr) {
+        void* p = nullptr;
+        const hipError_t r = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (r != hipSuccess || p == nullptr)
+            return set_error(r != hipSuccess ? (int)r : FX_EINVAL,
+                             "%s: hipGetSymbolAddress(scratch) failed on device %d (%s)", who, dev,
+                             hipGetErrorString(r));
+        g_scratch[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch[dev];
+    return 0;
+}
+
 }  // namespace fx
 
 using namespace fx;
@@ -247,20 +280,21 @@ extern "C" int64_t fx_adamw_workspace(const fxTensorList* lists, int32_t nlists)
     return (kWorkHead + parts) * (int64_t)sizeof(float);
 }
 
-extern "C" int fx_adamw_step(const fxAdamWState* st, const fxTensorList* lists, int32_t nlists,
-                             void* stream) {
-    FX_REQUIRE(st != nullptr, "fx_adamw_step: null state");
-    FX_REQUIRE(nlists >= 0 && (nlists == 0 || lists != nullptr), "fx_adamw_step: bad lists");
+// The step's launches with `work` as the workspace (null: the per-device scratch below,
+// whose size is checked against the lists first).
+static int adamw_step(const fxAdamWState* st, const fxTensorList* lists, int32_t nlists, float* work,
+                      void* stream, const char* who) {
+    FX_REQUIRE(st != nullptr, "%s: null state", who);
+    FX_REQUIRE(nlists >= 0 && (nlists == 0 || lists != nullptr), "%s: bad lists", who);
     FX_REQUIRE(st->master && st->m && st->v && st->p16 && st->step && st->found_inf && st->grad_norm &&
-                   st->scale && st->growth && st->work,
-               "fx_adamw_step: null state pointer");
+                   st->scale && st->growth,
+               "%s: null state pointer", who);
     FX_REQUIRE(((uintptr_t)st->master & 31) == 0 && ((uintptr_t)st->m & 31) == 0 &&
                    ((uintptr_t)st->v & 31) == 0 && ((uintptr_t)st->p16 & 15) == 0,
-               "fx_adamw_step: flat buffers must be 32-byte (fp32) / 16-byte (bf16) aligned");
-    FX_REQUIRE(((uintptr_t)st->work & 15) == 0, "fx_adamw_step: work must be 16-byte aligned");
+               "%s: flat buffers must be 32-byte (fp32) / 16-byte (bf16) aligned", who);
     hipStream_t s = (hipStream_t)stream;
     // At most a few lists: keep their chunk tables on the host stack.
-    FX_REQUIRE(nlists <= 64, "fx_adamw_step: %d lists (max 64)", nlists);
+    FX_REQUIRE(nlists <= 64, "%s: %d lists (max 64)", who, nlists);
     ChunkList cl[64];
     int64_t nch[64];
     int64_t total = 0;
@@ -268,21 +302,42 @@ extern "C" int fx_adamw_step(const fxAdamWState* st, const fxTensorList* lists, 
         if (int e = build_chunks(lists[i], (int32_t)total, cl[i], nch[i])) return e;
         total += nch[i];
     }
+    if (work == nullptr) {
+        const int64_t need = (kWorkHead + total) * (int64_t)sizeof(float);
+        FX_REQUIRE(need <= FX_ADAMW_NOALLOC_SCRATCH_BYTES,
+                   "%s: %lld chunks of %lld elements need %lld bytes of scratch, more than its %lld "
+                   "(at most %lld parameters)", who, (long long)total, (long long)kChunk, (long long)need,
+                   (long long)FX_ADAMW_NOALLOC_SCRATCH_BYTES,
+                   (long long)((FX_ADAMW_NOALLOC_SCRATCH_BYTES / (int64_t)sizeof(float) - kWorkHead) * kChunk));
+        if (int e = scratch_ptr(&work, who)) return e;
+    }
+    FX_REQUIRE(((uintptr_t)work & 15) == 0, "%s: work must be 16-byte aligned", who);
     for (int i = 0; i < nlists; ++i) {
         if (nch[i] == 0) continue;
-        hipLaunchKernelGGL(adamw_sumsq_kernel, dim3((unsigned)nch[i]), dim3(kOptThreads), 0, s, cl[i], st->work);
+        hipLaunchKernelGGL(adamw_sumsq_kernel, dim3((unsigned)nch[i]), dim3(kOptThreads), 0, s, cl[i], work);
         if (int e = check_launch("adamw_sumsq")) return e;
     }
-    hipLaunchKernelGGL(adamw_final_kernel, dim3(1), dim3(1024), 0, s, st->work, total, st->step,
+    hipLaunchKernelGGL(adamw_final_kernel, dim3(1), dim3(1024), 0, s, work, total, st->step,
                        st->found_inf, st->grad_norm, st->scale, st->growth, st->max_grad_norm,
                        st->growth_factor, st->backoff_factor, st->growth_interval, st->beta1, st->beta2);
     if (int e = check_launch("adamw_final")) return e;
     for (int i = 0; i < nlists; ++i) {
         if (nch[i] == 0) continue;
         hipLaunchKernelGGL(adamw_update_kernel, dim3((unsigned)(nch[i] * kOptVec)), dim3(kOptThreads), 0, s,
-                           cl[i], (const float*)st->work, st->master, st->m, st->v, st->p16, st->lr,
+                           cl[i], (const float*)work, st->master, st->m, st->v, st->p16, st->lr,
                            st->beta1, st->beta2, st->eps, st->weight_decay);
         if (int e = check_launch("adamw_update")) return e;
     }
     return 0;
+}
+
+extern "C" int fx_adamw_step(const fxAdamWState* st, const fxTensorList* lists, int32_t nlists,
+                             void* stream) {
+    FX_REQUIRE(st != nullptr && st->work != nullptr, "fx_adamw_step: null state or workspace");
+    return adamw_step(st, lists, nlists, st->work, stream, "fx_adamw_step");
+}
+
+extern "C" int fx_adamw_step_noalloc(const fxAdamWState* st, const fxTensorList* lists, int32_t nlists,
+                                     void* stream) {
+    return adamw_step(st, lists, nlists, nullptr, stream, "fx_adamw_step_noalloc");
 }

@@ -16,6 +16,7 @@ HEADER_PATH = os.path.join(os.path.dirname(_PKG_ROOT), "include", "fx_abi.h")
 FX_EINVAL = -1
 FX_ABI_VERSION = 3
 MAX_TENSORS = 64
+ADAMW_NOALLOC_SCRATCH_BYTES = 1 << 20   # FX_ADAMW_NOALLOC_SCRATCH_BYTES
 
 c_void_p = ctypes.c_void_p
 c_int32 = ctypes.c_int32
@@ -117,6 +118,8 @@ SIGNATURES = {
     "fx_adamw_workspace": (c_int64, [ctypes.POINTER(fxTensorList), c_int32]),
     "fx_adamw_step": (c_int32, [ctypes.POINTER(fxAdamWState), ctypes.POINTER(fxTensorList),
                                 c_int32, _P]),
+    "fx_adamw_step_noalloc": (c_int32, [ctypes.POINTER(fxAdamWState), ctypes.POINTER(fxTensorList),
+                                        c_int32, _P]),
     "fx_attn_fwd": (c_int32, [ctypes.POINTER(fxAttnArgs), _P]),
     "fx_attn_bwd": (c_int32, [ctypes.POINTER(fxAttnArgs), _P]),
     "fx_attn_decode_workspace": (c_int64, [c_int32, c_int32, c_int32, c_int32]),

@@ -109,6 +109,12 @@ class FlatAdamW:
         need = lib().fx_adamw_workspace(lists, nl) // 4
         if self._work.numel() < need:
             self._work = torch.empty(need, device=self.master.device, dtype=torch.float32)
+        st = self._state(lr_v, self._work.data_ptr())
+        call("fx_adamw_step", ctypes.byref(st), lists, nl, stream_of(self.master))
+        return {"grad_norm": self._norm, "found_inf": self._found_inf, "scale": self.scale}
+
+    def _state(self, lr_v, work):
+        """The fxAdamWState of this optimiser for one step at learning rate lr_v."""
         st = fxAdamWState()
         st.master, st.m, st.v = self.master.data_ptr(), self.m.data_ptr(), self.v.data_ptr()
         st.p16 = self.flat16.data_ptr()
@@ -117,14 +123,13 @@ class FlatAdamW:
         st.grad_norm = self._norm.data_ptr()
         st.scale = self.scale.data_ptr()
         st.growth = self._growth.data_ptr()
-        st.work = self._work.data_ptr()
+        st.work = work
         st.lr, st.beta1, st.beta2 = lr_v, float(self.betas[0]), float(self.betas[1])
         st.eps, st.weight_decay = float(self.eps), float(self.weight_decay)
         st.max_grad_norm = float(self.max_grad_norm)
         st.growth_factor, st.backoff_factor = 2.0, 0.5
         st.growth_interval = self.growth_interval
-        call("fx_adamw_step", ctypes.byref(st), lists, nl, stream_of(self.master))
-        return {"grad_norm": self._norm, "found_inf": self._found_inf, "scale": self.scale}
+        return st
 
     def zero_grad(self):
         for _n, p, _o, _el, _w in self._info:
