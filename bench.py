@@ -1,7 +1,9 @@
 """Benchmark: the fxlm GPT 12L-d768 training step on one MI355X, plus the hot-path kernels.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-    python bench.py --only {attention,ce,norm,adamw,linear,step,copy,decode}   (profiling runs)
+    python bench.py --only {attention,ce,norm,adamw,linear,step,copy,decode,cpu}   (profiling runs)
+    python bench.py --counter-table p_counter_collection.csv [...]   (per-kernel counter table)
+    python bench.py --traffic-table FETCH.csv WRITE.csv COPY_FETCH.csv COPY_WRITE.csv
     python bench.py --pmc-summary FETCH.csv WRITE.csv COPY_FETCH.csv COPY_WRITE.csv
 
 Workload (the headline metric's fifth config): GPT with 12 layers, d_model 768, 12 heads of
@@ -27,6 +29,7 @@ import gc
 import json
 import math
 import os
+import subprocess
 import sys
 import time
 
@@ -281,34 +284,52 @@ def gpu_step_bench(torch, steps, warmup):
             "params": model.num_params(), "found_inf": float(opt._found_inf)}
 
 
+def _lscpu():
+    """CPU model, sockets, physical cores and threads per core from lscpu (host facts for the
+    baseline's report)."""
+    info = {}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if ":" in line:
+                k, v = line.split(":", 1)
+                info[k.strip()] = v.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+
+    def num(k):
+        try:
+            return int(info.get(k, ""))
+        except ValueError:
+            return None
+    sockets, per_socket, tpc = num("Socket(s)"), num("Core(s) per socket"), num("Thread(s) per core")
+    return {"cpu_model": info.get("Model name", ""),
+            "physical_cores": sockets * per_socket if sockets and per_socket else None,
+            "threads_per_core": tpc, "logical_cpus": num("CPU(s)")}
+
+
 def cpu_baseline(torch):
-    """The reference's naive-PyTorch fp32 step (oracle/gpt.py) on the host cores."""
+    """The reference's naive-PyTorch fp32 step (oracle/gpt.py) on the host cores: the cfg5
+    model at the cfg5 batch (16 x 1024 tokens, 1 warm-up + 2 timed steps) and cfg1."""
     from oracle import gpt as ogpt
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    host = _lscpu()
     c = CFG5
     torch.manual_seed(0)
     m = ogpt.GPT(c["vocab_size"], c["seq_len"], c["n_layer"], c["n_head"], c["d_model"])
     opt = ogpt.make_optimizer(m, lr=6e-4)
-    Bc, T = 1, c["seq_len"]
+    Bc, T = c["batch"], c["seq_len"]
     gen = torch.Generator().manual_seed(1234)
     data = torch.randint(0, c["vocab_size"], (Bc, T + 1), generator=gen)
     x, y = data[:, :-1], data[:, 1:]
     ogpt.cpu_train_step(m, opt, x, y)          # warm-up
-    n, t0 = 0, time.perf_counter()
-    while n < 2 or (time.perf_counter() - t0 < 10.0 and n < 6):
+    n = 2
+    t0 = time.perf_counter()
+    for _ in range(n):
         ogpt.cpu_train_step(m, opt, x, y)
-        n += 1
     dt = (time.perf_counter() - t0) / n
-    cpu_model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu_model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
+    del m, opt, data, x, y
     # cfg1, the reference's CPU-runnable case: 4L-d256 H4 V256, T256, batch 32, lr 3e-4
     torch.manual_seed(0)
     m1 = ogpt.GPT(256, 256, 4, 4, 256)
@@ -321,13 +342,14 @@ def cpu_baseline(torch):
         ogpt.cpu_train_step(m1, opt1, x1, y1)
         n1 += 1
     dt1 = (time.perf_counter() - t1) / n1
-    return {"value": round(Bc * T / dt, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+    return {"value": round(Bc * T / dt, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": (f"oracle/gpt.py naive-PyTorch fp32 GPT 12L-d768 V50304 (SDPA, F.rms_norm, "
-                       f"F.cross_entropy, AdamW + clip 1.0) at batch {Bc} x {T} tokens, "
-                       f"1 warm-up + {n} timed steps ({dt:.2f} s/step) on {cores} threads, {cpu_model}"),
+                       f"F.cross_entropy, AdamW + clip 1.0) at the cfg5 batch {Bc} x {T} tokens, "
+                       f"1 warm-up + {n} timed steps ({dt:.2f} s/step) on {threads} threads"),
+            "host": host,
             "cfg1_tok_s": round(32 * 256 / dt1, 1),
             "cfg1_sample": (f"cfg1 4L-d256 H4 V256 T256 B32 fp32 step, 1 warm-up + {n1} timed steps "
-                            f"({dt1:.3f} s/step) on {cores} threads")}
+                            f"({dt1:.3f} s/step) on {threads} threads")}
 
 
 def bench_copy(torch):
@@ -379,6 +401,90 @@ def pmc_summary(fetch_csv, write_csv, copy_fetch_csv, copy_write_csv):
     return out
 
 
+def counter_table(csv_paths, top=12):
+    """Per-kernel averages per dispatch from rocprofv3 --pmc counter_collection.csv files,
+    as a markdown table: MFMA busy % of the SIMDs (SQ_VALU_MFMA_BUSY_CYCLES over the
+    dispatch's active cycles x 1024 SIMDs; the csv's GRBM_GUI_ACTIVE is summed over the 8
+    XCDs, so one XCD's count is an eighth of it), issued bf16 MFMA TFLOP/s
+    (SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 flops over the dispatch time), or FETCH_SIZE /
+    WRITE_SIZE in KiB, whichever the files hold."""
+    import csv
+    agg = {}
+    for path in csv_paths:
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                k = r["Kernel_Name"]
+                d = agg.setdefault(k, {})
+                disp = d.setdefault(r["Dispatch_Id"], {"_t": (int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))})
+                disp[r["Counter_Name"]] = disp.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    rows = []
+    for k, disps in agg.items():
+        n = len(disps)
+        avg = {}
+        for dd in disps.values():
+            for c, v in dd.items():
+                avg[c] = avg.get(c, 0.0) + v / n
+        rows.append((k, n, avg))
+    rows.sort(key=lambda r: -r[2]["_t"] * r[1])
+    names = sorted({c for _, _, a in rows for c in a if c != "_t"})
+    hdr = ["kernel", "dispatches", "avg µs"] + names
+    mf = "SQ_VALU_MFMA_BUSY_CYCLES" in names and "GRBM_GUI_ACTIVE" in names
+    bf = "SQ_INSTS_VALU_MFMA_MOPS_BF16" in names
+    if mf:
+        hdr.append("MFMA busy %")
+    if bf:
+        hdr.append("issued bf16 TFLOP/s")
+    lines = ["| " + " | ".join(hdr) + " |", "|" + "---|" * len(hdr)]
+    for k, n, a in rows[:top]:
+        kn = k if len(k) < 70 else k[:67] + "..."
+        cells = [f"`{kn}`", str(n), f"{a['_t'] / 1e3:.1f}"] + [f"{a.get(c, 0):.0f}" for c in names]
+        if mf:
+            cells.append(f"{100 * a['SQ_VALU_MFMA_BUSY_CYCLES'] / max(1.0, a['GRBM_GUI_ACTIVE'] / 8 * 1024):.1f}")
+        if bf:
+            cells.append(f"{a['SQ_INSTS_VALU_MFMA_MOPS_BF16'] * 512 / max(1.0, a['_t']) / 1e3:.1f}")
+        lines.append("| " + " | ".join(cells) + " |")
+    return "\n".join(lines)
+
+
+def traffic_table(fetch_csv, write_csv, copy_fetch_csv, copy_write_csv, top=12):
+    """HBM bytes per dispatch of every kernel in a FETCH_SIZE and a WRITE_SIZE pass, each
+    scaled by what the same counter reads for torch's 1 GiB copy (bench.py --only copy), as a
+    markdown table with the achieved GB/s over the dispatch time of the FETCH pass."""
+    import csv
+    known = 1 << 30
+    cf, _ = _pmc_per_dispatch(copy_fetch_csv, "FETCH_SIZE", "copy")
+    cw, _ = _pmc_per_dispatch(copy_write_csv, "WRITE_SIZE", "copy")
+    sf, sw = known / (cf * 1024.0), known / (cw * 1024.0)
+    per = {}
+    for path, ctr in ((fetch_csv, "FETCH_SIZE"), (write_csv, "WRITE_SIZE")):
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                if r["Counter_Name"] != ctr:
+                    continue
+                d = per.setdefault(r["Kernel_Name"], {}).setdefault(ctr, {})
+                e = d.setdefault(r["Dispatch_Id"], [0.0, int(r["End_Timestamp"]) - int(r["Start_Timestamp"])])
+                e[0] += float(r["Counter_Value"])
+    lines = [f"Calibration: FETCH_SIZE x{sf:.4f}, WRITE_SIZE x{sw:.4f} (torch copy of 1 GiB).", "",
+             "| kernel | dispatches | fetch MB | write MB | total MB | µs (fetch pass) | GB/s |",
+             "|---|---|---|---|---|---|---|"]
+    rows = []
+    for k, d in per.items():
+        if "FETCH_SIZE" not in d or "WRITE_SIZE" not in d:
+            continue
+        fv = list(d["FETCH_SIZE"].values())
+        wv = list(d["WRITE_SIZE"].values())
+        fb = sum(v for v, _ in fv) / len(fv) * 1024 * sf
+        wb = sum(v for v, _ in wv) / len(wv) * 1024 * sw
+        us = sum(t for _, t in fv) / len(fv) / 1e3
+        rows.append((k, len(fv), fb, wb, us))
+    rows.sort(key=lambda r: -(r[2] + r[3]) * r[1])
+    for k, n, fb, wb, us in rows[:top]:
+        kn = k if len(k) < 70 else k[:67] + "..."
+        lines.append(f"| `{kn}` | {n} | {fb / 1e6:.1f} | {wb / 1e6:.1f} | {(fb + wb) / 1e6:.1f} | {us:.1f} | "
+                     f"{(fb + wb) / max(us, 1e-9) / 1e3:.0f} |")
+    return "\n".join(lines)
+
+
 def _traffic():
     try:
         with open(TRAFFIC_JSON) as f:
@@ -396,12 +502,24 @@ def main():
     # counts, so a batch's first step can allocate; 42 ms once when it fell in the timed steps)
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU baseline")
-    ap.add_argument("--only", choices=["attention", "ce", "norm", "adamw", "linear", "step", "copy", "decode"],
+    ap.add_argument("--only", choices=["attention", "ce", "norm", "adamw", "linear", "step", "copy", "decode",
+                                       "cpu"],
                     help="run one workload and print its figures (for profiling runs)")
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV",
                                                        "COPY_WRITE_CSV"),
                     help="write the fx_attn_bwd HBM traffic from rocprofv3 --pmc csv files")
+    ap.add_argument("--counter-table", nargs="+", metavar="CSV",
+                    help="print per-kernel counter averages from rocprofv3 --pmc csv files")
+    ap.add_argument("--traffic-table", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV",
+                                                         "COPY_WRITE_CSV"),
+                    help="print per-kernel HBM bytes from FETCH_SIZE / WRITE_SIZE passes")
     args = ap.parse_args()
+    if args.counter_table:
+        print(counter_table(args.counter_table))
+        return
+    if args.traffic_table:
+        print(traffic_table(*args.traffic_table))
+        return
     if args.pmc_summary:
         res = pmc_summary(*args.pmc_summary)
         with open(TRAFFIC_JSON, "w") as f:
@@ -417,7 +535,7 @@ def main():
     lib()
     if args.only:
         fn = {"attention": bench_attention, "ce": bench_ce, "norm": bench_norm, "adamw": bench_adamw,
-              "linear": bench_linear, "copy": bench_copy, "decode": bench_decode,
+              "linear": bench_linear, "copy": bench_copy, "decode": bench_decode, "cpu": cpu_baseline,
               "step": lambda t: gpu_step_bench(t, args.steps, args.warmup)}[args.only]
         r = fn(torch)
         print(json.dumps({k: v for k, v in r.items() if not k.startswith("flop")}))
