@@ -58,17 +58,24 @@ struct GemmArgs {
     int64_t ldres;
     const uint16_t* nw;  // RMSNorm weight (K,) applied to the A rows first (few-row kernel), or null
     float eps;
+    bool vec_c, vec_h;   // C / H rows start 16-byte aligned (16-byte epilogue stores)
 };
 
-// tile t -> (row panel, column tile): with a multiple of 8 row panels, tiles with
-// t % 8 == c (run by the workgroups on XCD c) cover panels c, c+8, ... and walk all
-// column tiles of one panel in a row, so a panel's A rows are shared in that XCD's L2
+// tile t -> (row panel, column tile).  Workgroups are dealt round-robin to the 8 XCDs, so
+// tiles with t % 8 == x run on XCD x.  With a multiple of 8 row panels, XCD x owns panels
+// x, x + 8, ... and walks them in groups of (up to) 4 panels, the column tiles outer: the
+// 32 tiles an XCD runs at once then share 4 A row panels and 8 W column panels in its L2
+// (one A panel and 32 W panels with the panels outer: measured 7 % slower at the cfg5 fc).
 __device__ __forceinline__ void gemm_tile(int t, int nm, int nn, int& m0, int& n0, int& nt) {
     int mt;
     if ((nm & 7) == 0) {
-        const int c = t & 7, s = t >> 3;
-        mt = (s / nn) * 8 + c;
-        nt = s - (s / nn) * nn;
+        const int x = t & 7, sq = t >> 3;
+        const int per = nm >> 3;
+        const int gm = per < 4 ? per : 4;
+        const int grp = sq / (gm * nn), w = sq - grp * (gm * nn);
+        const int rows = min(gm, per - grp * gm);  // panels in this (possibly last, smaller) group
+        mt = (grp * gm + w % rows) * 8 + x;
+        nt = w / rows;
     } else {
         mt = t / nn;
         nt = t - mt * nn;
@@ -77,10 +84,45 @@ __device__ __forceinline__ void gemm_tile(int t, int nm, int nn, int& m0, int& n
     n0 = nt * kGBN;
 }
 
+// A 32 x 32 bf16 block of C leaves through the wave's LDS region `tmp`: lane l writes its
+// row (l%32) 4 columns at a time (epi_put: columns 8 q + 4 g + 0..3, g = l/32), then
+// epi_flush sends 16-byte row chunks out, two per lane (rows r = ch / 4, columns 8 (ch % 4)).
+// `vec`: every row start of `out` is 16-byte aligned (ld % 8 == 0, aligned base), so a
+// chunk is one store; otherwise element by element.  LDS operations of one wave complete
+// in order: the next block's writes cannot overtake these reads.
+constexpr int kEpiLD = 40;  // LDS row stride of the staging block (elements)
+static_assert((kGWaves / 2) * 32 * kEpiLD <= kGBM * kGLD, "eight waves' staging blocks fill one operand stage");
+__device__ __forceinline__ void epi_put(uint16_t* tmp, int q, const float (&v)[4], int lane) {
+    *reinterpret_cast<uint2*>(tmp + (lane & 31) * kEpiLD + 8 * q + 4 * (lane >> 5)) =
+        make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+}
+__device__ __forceinline__ void epi_flush(const uint16_t* tmp, uint16_t* out, int64_t ld, int mb, int nb, int M,
+                                          int N, bool vec, int lane) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int ch = h * 64 + lane;
+        const int r = ch >> 2, c = (ch & 3) * 8;
+        const uint4 u = *reinterpret_cast<const uint4*>(tmp + r * kEpiLD + c);
+        const int m = mb + r, n = nb + c;
+        if (m >= M || n >= N) continue;
+        uint16_t* o = out + (int64_t)m * ld + n;
+        if (vec && n + 8 <= N) {
+            st16(o, u);
+        } else {
+            const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+            for (int e = 0; e < 8 && n + e < N; ++e) o[e] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+        }
+    }
+}
+
 // Persistent: each workgroup walks tiles blockIdx.x, blockIdx.x + gridDim.x, ...; the
 // stage pipeline runs on across tiles, so the next tile's first K stage loads during
 // the current tile's last MFMAs and epilogue.
+// EPI selects the epilogue at compile time (fewer live registers than runtime switches):
+// bit 0 GELU, bit 1 pre-activation H out, bit 2 bias, bit 3 residual
+template <int EPI>
 __global__ void __launch_bounds__(kGThreads, 1) gemm_bias_act_kernel(GemmArgs a) {
+    constexpr bool kGelu = EPI & 1, kH = EPI & 2, kBias = EPI & 4, kRes = EPI & 8;
     __shared__ __attribute__((aligned(16))) uint16_t sa[2][kGBM * kGLD];
     __shared__ __attribute__((aligned(16))) uint16_t sb[2][kGBN * kGLD];
 
@@ -193,30 +235,53 @@ __global__ void __launch_bounds__(kGThreads, 1) gemm_bias_act_kernel(GemmArgs a)
 #pragma unroll
                 for (int j = 0; j < kGTJ; ++j)
 #pragma unroll
-                    for (int i = 0; i < kGTI; ++i) acc[j][i] = mfma32(av[i], bv[j], acc[j][i]);
+                    for (int i = 0; i < kGTI; ++i) acc[j][i] = mfma32(bv[j], av[i], acc[j][i]);
             }
         }
 
-        // epilogue (standard orientation): lane holds column n = cn0 + wn + 32 j + lane%32
-        // and rows cm0 + wm + 32 i + 8 (e/4) + 4 g + e%4; a half-wave stores 64 contiguous bytes
+        // epilogue.  The accumulators hold C^T: lane l has row m = cm0 + wm + 32 i + l%32 and,
+        // for q = 0..3, the columns cn0 + wn + 32 j + 8 q + 4 g + 0..3 (g = l/32).  Bias,
+        // activation and residual are applied in fp32 in registers; each 32 x 32 block then
+        // goes through the wave's private 32 x kEpiLD LDS region (8-byte writes) and leaves
+        // as 16-byte row chunks, 8 columns per lane (2-byte stores straight from the
+        // accumulators measured 8 % slower).  `st` now names the next tile's first stage
+        // (its loads are in flight): the stage just consumed, st ^ 1, is the scratch once
+        // every wave is done reading it.
+        __syncthreads();
+        uint16_t* tmp = (wave < 8 ? sa[st ^ 1] : sb[st ^ 1]) + (wave & 7) * (32 * kEpiLD);
 #pragma unroll
         for (int j = 0; j < kGTJ; ++j) {
-            const int n = cn0 + wn + 32 * j + (lane & 31);
-            if (n >= a.N) continue;
-            const float bn = a.bias ? bf16_to_f32(a.bias[n]) : 0.f;
+            const int nb = cn0 + wn + 32 * j;  // first column of the block
 #pragma unroll
-            for (int i = 0; i < kGTI; ++i)
+            for (int i = 0; i < kGTI; ++i) {
+                const int mb = cm0 + wm + 32 * i;  // first row of the block
+                const int m = mb + (lane & 31);
+                // pre-activation h = acc + bias (H, when wanted), then y = act(h) (+ residual)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int m = cm0 + wm + 32 * i + 8 * (e >> 2) + 4 * g + (e & 3);
-                    if (m < a.M) {
-                        const float h = acc[j][i][e] + bn;
-                        if (a.H) a.H[(int64_t)m * a.ldh + n] = f32_to_bf16(h);
-                        float y = a.act == 1 ? gelu_tanh(h) : h;
-                        if (a.res) y += bf16_to_f32(a.res[(int64_t)m * a.ldres + n]);
-                        a.C[(int64_t)m * a.ldc + n] = f32_to_bf16(y);
+                for (int pass = 0; pass < 2; ++pass) {
+                    if (pass == 0 && !kH) continue;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        float v[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int n = nb + 8 * q + 4 * g + e;
+                            float h = acc[j][i][4 * q + e];
+                            if (kBias && n < a.N) h += bf16_to_f32(a.bias[n]);
+                            if (pass == 1) {
+                                if (kGelu) h = gelu_tanh(h);
+                                if (kRes && m < a.M && n < a.N) h += bf16_to_f32(a.res[(int64_t)m * a.ldres + n]);
+                            }
+                            v[e] = h;
+                        }
+                        epi_put(tmp, q, v, lane);
                     }
+                    if (pass == 0)
+                        epi_flush(tmp, a.H, a.ldh, mb, nb, a.M, a.N, a.vec_h, lane);
+                    else
+                        epi_flush(tmp, a.C, a.ldc, mb, nb, a.M, a.N, a.vec_c, lane);
                 }
+            }
         }
     }
 }
@@ -575,14 +640,24 @@ gelu_bwd_kernel(const uint16_t* __restrict__ dy, const uint16_t* __restrict__ h,
 }
 
 // the few-row kernel for M <= kSKMaxM, else the persistent tiled kernel
-static int linear_fwd(const GemmArgs& a, hipStream_t stream) {
+static int linear_fwd(GemmArgs a, hipStream_t stream) {
     if (a.M <= kSKMaxM) return linear_skinny(a, stream);
+    a.vec_c = a.ldc % 8 == 0 && ((uintptr_t)a.C & 15) == 0;
+    a.vec_h = a.H && a.ldh % 8 == 0 && ((uintptr_t)a.H & 15) == 0;
     const int64_t tiles = ((int64_t)(a.M + kGBM - 1) / kGBM) * ((a.N + kGBN - 1) / kGBN);
     FX_REQUIRE(tiles < 0x7fffffffLL, "fx_linear_fwd: too many tiles");
     // persistent grid: one workgroup per CU (the LDS of one is 147 KB)
     const int64_t cus = device_cus();
     const int64_t grid = tiles < cus ? tiles : cus;
-    hipLaunchKernelGGL(gemm_bias_act_kernel, dim3((unsigned)grid), dim3(kGThreads), 0, stream, a);
+    const int epi = (a.act == 1 ? 1 : 0) | (a.H ? 2 : 0) | (a.bias ? 4 : 0) | (a.res ? 8 : 0);
+#define FX_GEMM_EPI(E) \
+    case E: hipLaunchKernelGGL(gemm_bias_act_kernel<E>, dim3((unsigned)grid), dim3(kGThreads), 0, stream, a); break;
+    switch (epi) {
+        FX_GEMM_EPI(0) FX_GEMM_EPI(1) FX_GEMM_EPI(2) FX_GEMM_EPI(3) FX_GEMM_EPI(4) FX_GEMM_EPI(5) FX_GEMM_EPI(6)
+        FX_GEMM_EPI(7) FX_GEMM_EPI(8) FX_GEMM_EPI(9) FX_GEMM_EPI(10) FX_GEMM_EPI(11) FX_GEMM_EPI(12)
+        FX_GEMM_EPI(13) FX_GEMM_EPI(14) FX_GEMM_EPI(15)
+    }
+#undef FX_GEMM_EPI
     return check_launch("gemm_bias_act");
 }
 
