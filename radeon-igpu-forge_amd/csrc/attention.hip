@@ -102,22 +102,103 @@ __device__ __forceinline__ void store_rows(const f32x16 (&acc)[D / 32], float mu
 }
 
 // ---------------------------------------------------------------------------
+// LDS layout of a streamed R x D tile.
+//
+// D = 64: unpadded 128-byte rows whose eight 16-byte chunks are permuted per row: logical
+// chunk c of row r sits at chunk c ^ swz(r), swz(r) = bits 1, 2, 3 of r reversed.  Rows
+// r and r + 1 differ in bank half, so among any 16 consecutive rows the 8 even ones (and
+// the 8 odd ones) cover all 8 chunk positions: a row read (16 lanes, 16 consecutive rows,
+// one chunk) is conflict-free; bit 2 of swz follows bit 1 of r, so the 4 rows of a
+// transposed read (4 rows x 4 chunks per 32 lanes) fall in disjoint banks as well.
+// Against the padded layout this drops one slot in nine from every tile load (the loads'
+// cost grows faster than their byte count: half the loads measured a third of their cost)
+// and the 2-way conflicts of the transposed reads.
+// D = 128: row stride D + 8 elements (the pad keeps the operand reads conflict-free).
+template <int D, bool SW>
+struct TileLayout {
+    static constexpr int LD = D + 8;       // row stride (elements)
+    static constexpr int SPR = D / 8 + 1;  // 16-byte slots per row, the last one padding
+    __device__ __forceinline__ static int off(int row, int col) { return row * LD + col; }
+    // logical chunk held by slot `slot` of row `row` (the pad slot: any in-row chunk)
+    __device__ __forceinline__ static int chunk(int row, int slot) { return slot == SPR - 1 ? SPR - 2 : slot; }
+};
+template <>
+struct TileLayout<64, true> {
+    static constexpr int LD = 64;
+    static constexpr int SPR = 8;
+    __device__ __forceinline__ static int swz(int row) {
+        return (((row >> 1) & 1) << 2) | (((row >> 2) & 1) << 1) | ((row >> 3) & 1);
+    }
+    __device__ __forceinline__ static int off(int row, int col) {
+        return row * 64 + ((((col >> 3) ^ swz(row)) << 3) | (col & 7));
+    }
+    __device__ __forceinline__ static int chunk(int row, int slot) { return slot ^ swz(row); }
+};
+
+// MFMA operands from a tile in this layout (see fx_mfma.h for the lane mappings): K along a
+// row (8 contiguous elements of row r0 + l%32 at column c0 + 8 (l/32)), or K down the rows
+// (two ds_read_b64_tr_b16; a lane's 4 columns never cross a 16-byte chunk).  The kernels
+// only read at r0, k0 multiples of 16 (which leave swz unchanged) and c0, m0 multiples of
+// 16 and 32, so for D = 64 each lane's offsets are a per-lane table plus a compile-time
+// row offset (a per-lane swizzle computed at every read cost 10 VGPRs in the forward).
+template <int D, bool SW>
+struct TileLane {
+    __device__ __forceinline__ void init(int) {}
+    __device__ __forceinline__ int row(int r0, int c0, int lane) const {
+        return TileLayout<D, SW>::off(r0 + (lane & 31), c0 + 8 * (lane >> 5));
+    }
+    __device__ __forceinline__ int tr(int k0, int m0, int h, int lane) const {
+        const int grp = lane >> 4, s = lane & 15;
+        return TileLayout<D, SW>::off(k0 + 4 * (grp >> 1) + (s >> 2) + 8 * h, m0 + 16 * (grp & 1) + 4 * (s & 3));
+    }
+};
+template <>
+struct TileLane<64, true> {
+    int ro[4];     // row reads at c0 = 16 c, rows 0..31
+    int to[2][2];  // transposed reads at m0 = 32 m, rows 0..7 (h = 0) or 8..15 (h = 1)
+    __device__ __forceinline__ void init(int lane) {
+        const int g = lane >> 5, l32 = lane & 31;
+        const int p = g ^ TileLayout<64, true>::swz(l32);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) ro[c] = l32 * 64 + (((2 * c) ^ p) << 3);
+        const int grp = lane >> 4, s = lane & 15;
+        const int rb = 4 * (grp >> 1) + (s >> 2);
+        const int cl = 2 * (grp & 1) + ((s & 3) >> 1);
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                to[m][h] = (rb + 8 * h) * 64 + ((((4 * m) ^ cl ^ TileLayout<64, true>::swz(rb) ^ h)) << 3) + 4 * (s & 1);
+    }
+    __device__ __forceinline__ int row(int r0, int c0, int) const { return r0 * 64 + ro[c0 >> 4]; }
+    __device__ __forceinline__ int tr(int k0, int m0, int h, int) const { return k0 * 64 + to[m0 >> 5][h]; }
+};
+template <int D, bool SW>
+__device__ __forceinline__ bf16x8 tile_op_row(const TileLane<D, SW>& tl, const uint16_t* tile, int r0, int c0, int lane) {
+    if constexpr (SW) return *reinterpret_cast<const bf16x8*>(tile + tl.row(r0, c0, lane));
+    else return lds_op_row(tile, TileLayout<D, SW>::LD, r0, c0, lane);
+}
+template <int D, bool SW>
+__device__ __forceinline__ bf16x8 tile_op_t(const TileLane<D, SW>& tl, const uint16_t* tile, int k0, int m0, int lane) {
+    if constexpr (SW) return cat8(lds_tr16(tile + tl.tr(k0, m0, 0, lane)), lds_tr16(tile + tl.tr(k0, m0, 1, lane)));
+    else return lds_op_t(tile, TileLayout<D, SW>::LD, k0, m0, lane);
+}
+
+// ---------------------------------------------------------------------------
 // Tile staging by direct global -> LDS loads (global_load_lds_dwordx4).
 //
-// A tile of R rows x D columns lives in LDS with row stride D + 8 elements (the pad
-// keeps the MFMA operand reads free of bank conflicts), i.e. SPR = D/8 + 1 16-byte
-// slots per row.  A wave-wide global_load_lds writes 64 consecutive slots (lane i ->
-// slot base + i), so a tile is covered slot by slot: slot s holds row s / SPR, chunk
-// s % SPR; the pad slot re-reads the row's last chunk and rows past the end of the
+// A wave-wide global_load_lds writes 64 consecutive 16-byte LDS slots (lane i -> slot
+// base + i), so a tile is covered slot by slot: slot s is slot s % SPR of row s / SPR and
+// holds that row's logical chunk TileLayout::chunk(row, slot); rows past the end of the
 // sequence read a zero line.  The loads need no registers and no LDS stores; they are
 // complete once the issuing wave's vmcnt drains, and visible to the other waves after
 // the following barrier.
 
 // Two R x D tiles (K and V, or Q and dO) staged together: 2 * R * SPR / 64 wave
 // instructions dealt round-robin to the workgroup's waves.
-template <int D, int R>
+template <int D, int R, bool SW>
 struct TileDma2 {
-    static constexpr int SPR = D / 8 + 1;
+    static constexpr int SPR = TileLayout<D, SW>::SPR;
     static constexpr int NI = R * SPR / 64;  // wave instructions per tile
     static_assert(R * SPR % 64 == 0, "tile must be a whole number of wave loads");
     static constexpr int PW = (2 * NI + kAttWaves - 1) / kAttWaves;  // per wave, at most
@@ -127,8 +208,7 @@ struct TileDma2 {
     __device__ __forceinline__ static void slot(int i, int lane, int& r, int& c) {
         const int s = (i % NI) * 64 + lane;
         r = s / SPR;
-        c = s - r * SPR;
-        if (c == SPR - 1) c = SPR - 2;  // pad slot: any in-row chunk
+        c = TileLayout<D, SW>::chunk(r, s - r * SPR);
     }
     __device__ __forceinline__ void init(int64_t rs0, int64_t rs1) {
         wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -183,11 +263,15 @@ __device__ __forceinline__ float pair_sum(float x) {
 
 template <int D>
 __global__ void __launch_bounds__(kAttThreads) attn_fwd_kernel(fxAttnArgs a) {
-    constexpr int LD = D + 8;
+    // padded tiles: the swizzle's per-lane offset table would take the forward past 128
+    // VGPRs (3 waves per SIMD instead of 4), and its tile loads cost it little
+    constexpr bool SW = false;
+    constexpr int LD = TileLayout<D, SW>::LD;
     constexpr int DC = D / 16;  // K chunks of Q.K
     constexpr int DT = D / 32;  // 32-row tiles of O^T
     __shared__ __attribute__((aligned(16))) uint16_t sk0[kBN * LD], sk1[kBN * LD];
     __shared__ __attribute__((aligned(16))) uint16_t sv0[kBN * LD], sv1[kBN * LD];
+    static_assert(32 * (D + 8) <= kBN * LD, "a stage buffer holds one wave's output staging");
 
     const int T = a.T;
     const int nqt = (T + kBM - 1) / kBM;
@@ -197,6 +281,8 @@ __global__ void __launch_bounds__(kAttThreads) attn_fwd_kernel(fxAttnArgs a) {
     const int b = bh / a.H, h = bh - b * a.H;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 5, ln = lane & 31;
+    TileLane<D, SW> tl;
+    tl.init(lane);
     const int q0 = qt * kBM;
     const int q0w = q0 + 32 * wave;
     const int qi = q0w + ln;
@@ -206,7 +292,7 @@ __global__ void __launch_bounds__(kAttThreads) attn_fwd_kernel(fxAttnArgs a) {
     const int kend = a.causal ? min(T, q0 + kBM) : T;
     const int nblk = (kend + kBN - 1) / kBN;
 
-    TileDma2<D, kBN> dma;
+    TileDma2<D, kBN, SW> dma;
     dma.init(a.kst, a.vst);
     dma.issue(kbase, vbase, T, sk0, sv0);
 
@@ -240,7 +326,7 @@ __global__ void __launch_bounds__(kAttThreads) attn_fwd_kernel(fxAttnArgs a) {
             if (kh >= T || (a.causal && kh > q0w + 31)) continue;  // every key masked for this wave
             bf16x8 kop[DC];
 #pragma unroll
-            for (int c = 0; c < DC; ++c) kop[c] = lds_op_row(K, LD, 32 * hh, 16 * c, lane);
+            for (int c = 0; c < DC; ++c) kop[c] = tile_op_row(tl, K, 32 * hh, 16 * c, lane);
             f32x16 sc = f32x16{};
 #pragma unroll
             for (int c = 0; c < DC; ++c) sc = mfma32(kop[c], qop[c], sc);
@@ -248,7 +334,7 @@ __global__ void __launch_bounds__(kAttThreads) attn_fwd_kernel(fxAttnArgs a) {
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-                for (int kc = 0; kc < 2; ++kc) vop[dt][kc] = lds_op_t(V, LD, 32 * hh + 16 * kc, 32 * dt, lane);
+                for (int kc = 0; kc < 2; ++kc) vop[dt][kc] = tile_op_t(tl, V, 32 * hh + 16 * kc, 32 * dt, lane);
             if ((kh + 32 > T) || (a.causal && kh + 31 > q0w))  // keys past T or after the query
                 mask_rows(sc, 0, (a.causal ? min(qi, T - 1) : T - 1) - kh - 4 * g);
             float mloc = sc[0];
@@ -305,11 +391,13 @@ __global__ void __launch_bounds__(kAttThreads) attn_fwd_kernel(fxAttnArgs a) {
 
 template <int D>
 __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dq_kernel(fxAttnArgs a) {
-    constexpr int LD = D + 8;
+    constexpr bool SW = D == 64;  // swizzled tiles: 9 % fewer tile loads, no transposed-read conflicts
+    constexpr int LD = TileLayout<D, SW>::LD;
     constexpr int DC = D / 16;
     constexpr int DT = D / 32;
     __shared__ __attribute__((aligned(16))) uint16_t sk0[kBN * LD], sk1[kBN * LD];
     __shared__ __attribute__((aligned(16))) uint16_t sv0[kBN * LD], sv1[kBN * LD];
+    static_assert(32 * (D + 8) <= kBN * LD, "a stage buffer holds one wave's output staging");
 
     const int T = a.T;
     const int nqt = (T + kBM - 1) / kBM;
@@ -319,6 +407,8 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dq_kern
     const int b = bh / a.H, h = bh - b * a.H;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 5, ln = lane & 31;
+    TileLane<D, SW> tl;
+    tl.init(lane);
     const int q0 = qt * kBM;
     const int q0w = q0 + 32 * wave;
     const int qi = q0w + ln;
@@ -328,7 +418,7 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dq_kern
     const uint16_t* vbase = a.v + b * a.vsb + h * a.vsh;
     const int kend = a.causal ? min(T, q0 + kBM) : T;
     const int nblk = (kend + kBN - 1) / kBN;
-    TileDma2<D, kBN> dma;
+    TileDma2<D, kBN, SW> dma;
     dma.init(a.kst, a.vst);
     dma.issue(kbase, vbase, T, sk0, sv0);
 
@@ -380,8 +470,8 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dq_kern
             f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
             for (int c = 0; c < DC; ++c) {
-                const bf16x8 kop = lds_op_row(K, LD, 32 * hh, 16 * c, lane);
-                const bf16x8 vop = lds_op_row(V, LD, 32 * hh, 16 * c, lane);
+                const bf16x8 kop = tile_op_row(tl, K, 32 * hh, 16 * c, lane);
+                const bf16x8 vop = tile_op_row(tl, V, 32 * hh, 16 * c, lane);
                 s = mfma32(kop, qop[c], s);
                 dp = mfma32(vop, dop[c], dp);
             }
@@ -395,8 +485,8 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dq_kern
             const bf16x8 d0 = pack_op(s, 0), d1 = pack_op(s, 1);
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
-                const bf16x8 k0t = lds_op_t(K, LD, 32 * hh, 32 * dt, lane);
-                const bf16x8 k1t = lds_op_t(K, LD, 32 * hh + 16, 32 * dt, lane);
+                const bf16x8 k0t = tile_op_t(tl, K, 32 * hh, 32 * dt, lane);
+                const bf16x8 k1t = tile_op_t(tl, K, 32 * hh + 16, 32 * dt, lane);
                 acc[dt] = mfma32(k0t, d0, acc[dt]);
                 acc[dt] = mfma32(k1t, d1, acc[dt]);
             }
@@ -408,7 +498,7 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dq_kern
     }
 
     __syncthreads();  // every wave is done with the K/V stages: they become store scratch
-    store_rows<D>(acc, a.scale, (wave < 2 ? sk0 : sk1) + (wave & 1) * 32 * LD,
+    store_rows<D>(acc, a.scale, wave == 0 ? sk0 : wave == 1 ? sk1 : wave == 2 ? sv0 : sv1,
                   a.dq + b * a.dqb + h * a.dqh + (int64_t)q0w * a.dqt, a.dqt, T - q0w, lane);
 }
 
@@ -417,11 +507,13 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dq_kern
 
 template <int D>
 __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dkv_kernel(fxAttnArgs a) {
-    constexpr int LD = D + 8;
+    constexpr bool SW = D == 64;
+    constexpr int LD = TileLayout<D, SW>::LD;
     constexpr int DC = D / 16;
     constexpr int DT = D / 32;
     __shared__ __attribute__((aligned(16))) uint16_t sq0[kBQ * LD], sq1[kBQ * LD];
     __shared__ __attribute__((aligned(16))) uint16_t sdo0[kBQ * LD], sdo1[kBQ * LD];
+    static_assert(32 * (D + 8) <= kBQ * LD, "a stage buffer holds one wave's output staging");
     __shared__ __attribute__((aligned(16))) float slse[2][kBQ];
     __shared__ __attribute__((aligned(16))) float sdelta[2][kBQ];
 
@@ -432,6 +524,8 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dkv_ker
     const int b = bh / a.H, h = bh - b * a.H;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane >> 5, ln = lane & 31;
+    TileLane<D, SW> tl;
+    tl.init(lane);
     const int k0 = kt * kBK;
     const int k0w = k0 + 32 * wave;
     const int ki = k0w + ln;
@@ -447,7 +541,7 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dkv_ker
 
     // Q / dO tiles by DMA; the tile's lse and Delta through one register each
     // (threads 0..63), stored to LDS once they have arrived
-    TileDma2<D, kBQ> dma;
+    TileDma2<D, kBQ, SW> dma;
     dma.init(a.qst, dors);
     float rl = 0.f, rdl = 0.f;
     auto issue = [&](int qb, const uint16_t* nQ, const uint16_t* nDO) {
@@ -502,8 +596,8 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dkv_ker
             f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
             for (int c = 0; c < DC; ++c) {
-                const bf16x8 qa = lds_op_row(Q, LD, 32 * hh, 16 * c, lane);
-                const bf16x8 da = lds_op_row(DO, LD, 32 * hh, 16 * c, lane);
+                const bf16x8 qa = tile_op_row(tl, Q, 32 * hh, 16 * c, lane);
+                const bf16x8 da = tile_op_row(tl, DO, 32 * hh, 16 * c, lane);
                 s = mfma32(qa, kop[c], s);
                 dp = mfma32(da, vop[c], dp);
             }
@@ -530,10 +624,10 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dkv_ker
             const bf16x8 d0 = pack_op(dp, 0), d1 = pack_op(dp, 1);
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
-                const bf16x8 o0 = lds_op_t(DO, LD, 32 * hh, 32 * dt, lane);
-                const bf16x8 o1 = lds_op_t(DO, LD, 32 * hh + 16, 32 * dt, lane);
-                const bf16x8 q0t = lds_op_t(Q, LD, 32 * hh, 32 * dt, lane);
-                const bf16x8 q1t = lds_op_t(Q, LD, 32 * hh + 16, 32 * dt, lane);
+                const bf16x8 o0 = tile_op_t(tl, DO, 32 * hh, 32 * dt, lane);
+                const bf16x8 o1 = tile_op_t(tl, DO, 32 * hh + 16, 32 * dt, lane);
+                const bf16x8 q0t = tile_op_t(tl, Q, 32 * hh, 32 * dt, lane);
+                const bf16x8 q1t = tile_op_t(tl, Q, 32 * hh + 16, 32 * dt, lane);
                 adv[dt] = mfma32(o0, p0, adv[dt]);
                 adk[dt] = mfma32(q0t, d0, adk[dt]);
                 adv[dt] = mfma32(o1, p1, adv[dt]);
@@ -547,7 +641,7 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dkv_ker
     }
 
     __syncthreads();  // every wave is done with the Q/dO stages: they become store scratch
-    uint16_t* tmp = (wave < 2 ? sq0 : sq1) + (wave & 1) * 32 * LD;
+    uint16_t* tmp = wave == 0 ? sq0 : wave == 1 ? sq1 : wave == 2 ? sdo0 : sdo1;
     store_rows<D>(adk, a.scale, tmp, a.dk + b * a.dkb + h * a.dkh + (int64_t)k0w * a.dkt, a.dkt, T - k0w, lane);
     store_rows<D>(adv, 1.f, tmp, a.dv + b * a.dvb + h * a.dvh + (int64_t)k0w * a.dvt, a.dvt, T - k0w, lane);
 }
