@@ -49,18 +49,33 @@ def _events(torch):
     return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
 
-def time_us(torch, fn, iters=20, warm=5):
-    """Average duration (us) of fn() over `iters` runs, HIP events on the current stream."""
+def time_us(torch, fn, iters=20, warm=5, warm_ms=200.0, rounds=5):
+    """Steady-state duration (us) of fn(): the median over `rounds` of the average of
+    `iters` runs (HIP events on the current stream), after warm-up calls that fill at least
+    `warm_ms` of GPU time.  The GPU's clocks ramp up over the first ~100 ms of sustained
+    load: timed from idle, the attention backward measured 157 us, and 133-134 us once
+    warm (the training step's kernels run under sustained load)."""
     for _ in range(warm):
         fn()
     torch.cuda.synchronize()
     s, e = _events(torch)
     s.record()
-    for _ in range(iters):
-        fn()
+    fn()
     e.record()
     torch.cuda.synchronize()
-    return s.elapsed_time(e) / iters * 1e3
+    n = int(min(5000, max(1.0, warm_ms / max(s.elapsed_time(e), 1e-3))))
+    for _ in range(n):
+        fn()
+    res = []
+    for _ in range(rounds):
+        torch.cuda.synchronize()
+        s.record()
+        for _ in range(iters):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        res.append(s.elapsed_time(e) / iters * 1e3)
+    return sorted(res)[len(res) // 2]
 
 
 def graph_time_us(torch, fn, reps=20, iters=10):
