@@ -410,3 +410,23 @@ def test_deferred_residual_sums_bitwise(dev):
     assert torch.equal(loss_a, loss_b)
     for a, p in zip(ga, model.parameters()):
         assert torch.equal(a, p.grad)
+
+
+def test_train_lm_cli_on_the_gpu(dev, tmp_path):
+    # the front ends end to end on the GPU (fused kernels, FlatAdamW): prepare_bytes, a
+    # 12-step run with evaluation and checkpoints, the refusal to overwrite, and a resume
+    from fxlm import prepare_bytes, train_lm
+    from fxlm import train as tr
+    src = tmp_path / "corpus.txt"
+    src.write_bytes(b"pack my box with five dozen liquor jugs. " * 400)
+    prepare_bytes.main([str(src), "--out", str(tmp_path / "demo"), "--val-frac", "0.05"])
+    out = str(tmp_path / "run")
+    base = ["--data", str(tmp_path / "demo_train.bin"), "--out", out, "--seq-len", "64", "--layers", "2",
+            "--heads", "2", "--dim", "128", "--batch", "8", "--lr", "3e-3", "--warmup", "3",
+            "--eval-every", "6", "--eval-batches", "2", "--log-every", "4", "--init-scale", "8"]
+    r = train_lm.main(base + ["--steps", "12"])
+    assert r["step"] == 12 and r["skipped"] == 0 and r["val_loss"] < math.log(256)
+    with pytest.raises(SystemExit):
+        train_lm.main(base + ["--steps", "14"])
+    r2 = train_lm.main(base + ["--steps", "14", "--resume", r["ckpt"]])
+    assert r2["step"] == 14 and tr.load_checkpoint(r2["ckpt"])["step"] == 14
