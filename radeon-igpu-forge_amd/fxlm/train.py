@@ -1,7 +1,7 @@
 """fxlm.train: the data format, LR schedule and checkpoints of the fxlm training loop.
 
 Library form of what ml/fxlm/train_lm.py and ml/fxlm/prepare_bytes.py do around the
-GPU step (the argparse front ends are not part of this package):
+GPU step (their argparse front ends are fxlm.train_lm and fxlm.prepare_bytes):
 
 * byte-level token files: ``<prefix>_train.bin`` / ``<prefix>_val.bin`` (uint16, one
   token per byte value) and ``<prefix>.json`` {vocab_size, tokenizer, n_train, n_val,
