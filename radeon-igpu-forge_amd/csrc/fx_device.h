@@ -181,8 +181,43 @@ __device__ __forceinline__ void dma16_so(const void* sbase, uint32_t voff, uint3
         : "v"(voff), "s"(sbase), "s"(lds)
         : "memory");
 }
+// global_load_lds_dword: 4 bytes per active lane to lds + 4 * lane (same protocol as dma16)
+__device__ __forceinline__ void dma4(const void* src, uint32_t lds) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %2\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dword %1, off\n\t"
+        "s_nop 0\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(src), "s"(lds)
+        : "memory");
+}
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(lds_void*)p;
+}
+
+// Wait until at most N of this wave's vector-memory instructions (loads, stores and the
+// LDS loads above, completing in issue order) are outstanding.  The memory clobber keeps
+// the compiler from moving LDS reads of the awaited data above the wait.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit count");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// the same for a count that is a compile-time constant only after loop unrolling
+__device__ __forceinline__ void wait_vmcnt_folded(int n) {
+    switch (n) {
+#define FX_WC(i) case i: wait_vmcnt<i>(); break;
+        FX_WC(1) FX_WC(2) FX_WC(3) FX_WC(4) FX_WC(5) FX_WC(6) FX_WC(7) FX_WC(8) FX_WC(9) FX_WC(10)
+        FX_WC(11) FX_WC(12) FX_WC(13) FX_WC(14) FX_WC(15) FX_WC(16) FX_WC(17) FX_WC(18) FX_WC(19)
+        FX_WC(20) FX_WC(21) FX_WC(22) FX_WC(23) FX_WC(24) FX_WC(25) FX_WC(26) FX_WC(27) FX_WC(28)
+        FX_WC(29) FX_WC(30) FX_WC(31) FX_WC(32)
+#undef FX_WC
+        default: wait_vmcnt<0>();  // stricter than asked: always safe
+    }
 }
 
 // Wait for this wave's outstanding vector-memory operations (including its tile

@@ -263,6 +263,125 @@ rms_bwd_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ dy,
     for (int c = threadIdx.x; c < D; c += NT) pr[c] = red[c];
 }
 
+// Backward for 512 <= D <= 1536 with the rows prefetched into LDS.  Each wave owns one
+// row per step (64 lanes, lane j holding 16-byte vectors j, j + 64, ...) and keeps the
+// next S - 1 rows in flight in a private ring of S slots, each slot the row's x, dy and
+// (T == 3) dres plus its rstd, filled by global_load_lds (no registers held for the
+// prefetch, which the register kernel above cannot afford: loading the next row into
+// registers spilled).  One 512-thread block per CU (256 blocks): at [65536, 768] 50.2 us
+// against 54.3 us for the register kernel (75 % against 70 % of HBM), with dres 64.6
+// against 74.3 us; dx is bit for bit the register kernel's, dw the same sum over half as
+// many partial rows.
+//
+// Waits: every prefetched row is GOPS = T * NV + 1 vector-memory instructions (a masked
+// instruction still counts) and every computed row NV stores; completion is in issue
+// order, so row k has landed once at most (S - 1) * GOPS + min(k, S - 1) * NV
+// instructions are outstanding (the loads of rows k + 1 .. k + S - 1 and the stores of
+// the rows before k issued after row k's loads).  The last S - 1 rows wait for all.
+constexpr int kNormLdsBlocks = 256;  // one per CU
+
+template <int NV, int T, int S>
+__global__ void __launch_bounds__(kNormBwdThreads, 2)
+rms_bwd_lds_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ dy,
+                   const uint16_t* __restrict__ dres, const uint16_t* __restrict__ w,
+                   const float* __restrict__ rstd, uint16_t* __restrict__ dx, float* __restrict__ part,
+                   int64_t N, int D) {
+    constexpr int NT = kNormBwdThreads, NW = NT / 64, LPR = 64;
+    constexpr int GOPS = T * NV + 1;
+    extern __shared__ __attribute__((aligned(16))) unsigned char ring_mem[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int V8 = D >> 3;
+    const int RB = D * 2;          // bytes of one bf16 row
+    const int SB = T * RB + 16;    // bytes of one slot: T rows, then rstd
+    unsigned char* ring = ring_mem + wave * S * SB;
+    const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_addr(ring));
+    // rows first, first + stride, ... (the register kernel's assignment for 64-lane rows)
+    const int64_t stride = (int64_t)gridDim.x * NW;
+    const int64_t first = (int64_t)blockIdx.x * NW + wave;
+    const int nrows = first < N ? (int)((N - 1 - first) / stride + 1) : 0;
+    const float invD = 1.f / (float)D;
+
+    float acc[NV][8];
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = 0.f;
+    uint4 wv[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = i * LPR + lane;
+        wv[i] = c < V8 ? ld16(w + c * 8) : make_uint4(0u, 0u, 0u, 0u);
+    }
+    // row k of this wave into slot s: NV instructions per tensor (the last one with the
+    // lanes c < V8, at least one), then rstd by lane 0
+    auto prefetch = [&](int k, int s) {
+        const int64_t row = first + (int64_t)k * stride;
+        const uint32_t slot = ring_lds + s * SB;
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const uint16_t* src = (t == 0 ? x : t == 1 ? dy : dres) + row * D;
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                const int c = i * LPR + lane;
+                if (c < V8) dma16(src + c * 8, slot + t * RB + i * 1024);
+            }
+        }
+        if (lane == 0) dma4(rstd + row, slot + T * RB);
+    };
+#pragma unroll
+    for (int s = 0; s < S - 1; ++s)
+        if (s < nrows) prefetch(s, s);
+    for (int k0 = 0; k0 < nrows; k0 += S) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            const int k = k0 + s;
+            if (k >= nrows) break;
+            if (k + S - 1 < nrows) {
+                prefetch(k + S - 1, (s + S - 1) % S);
+                if (k0 == 0) wait_vmcnt_folded(GOPS * (S - 1) + NV * s);
+                else wait_vmcnt_folded((GOPS + NV) * (S - 1));
+            } else {
+                wait_vmcnt<0>();
+            }
+            const unsigned char* sl = ring + s * SB;
+            NormBwdRow<LPR, NV> b;
+#pragma unroll
+            for (int i = 0; i < NV; ++i) {
+                const int c = i * LPR + lane;
+                b.xv[i] = b.dv[i] = b.rv[i] = make_uint4(0u, 0u, 0u, 0u);
+                if (c < V8) {
+                    b.xv[i] = *reinterpret_cast<const uint4*>(sl + c * 16);
+                    b.dv[i] = *reinterpret_cast<const uint4*>(sl + RB + c * 16);
+                    if (T == 3) b.rv[i] = *reinterpret_cast<const uint4*>(sl + 2 * RB + c * 16);
+                }
+            }
+            b.r = *reinterpret_cast<const float*>(sl + T * RB);
+            norm_bwd_row<LPR, NV>(b, wv, dx + (first + (int64_t)k * stride) * D, acc, D, invD, lane, T == 3);
+            asm volatile("" ::: "memory");  // the slot's reads stay before its next prefetch
+        }
+    }
+
+    // dw partial of the block: as the register kernel's per-wave fold, in the ring's LDS
+    __syncthreads();  // every wave is done with its ring
+    float* red = reinterpret_cast<float*>(ring_mem);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = i * LPR + lane;
+        if (c < V8) {
+            float4* r = reinterpret_cast<float4*>(red + wave * D + c * 8);
+            r[0] = make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+            r[1] = make_float4(acc[i][4], acc[i][5], acc[i][6], acc[i][7]);
+        }
+    }
+    __syncthreads();
+    float* pr = part + (int64_t)blockIdx.x * D;
+    for (int c = threadIdx.x; c < D; c += NT) {
+        float sum = red[c];
+        for (int k = 1; k < NW; ++k) sum += red[k * D + c];
+        pr[c] = sum;
+    }
+}
+
 // dw[c] = sum_p part[p][c] in a fixed order.  A block owns 8 columns (2 float4 lanes)
 // and 128 partial-row lanes (32 per wave): each thread sums every 128th partial row of
 // its 4 columns with its loads in flight, the row lanes of a wave fold with a butterfly
@@ -372,6 +491,18 @@ static int64_t bwd_blocks(int64_t ngroups) {
     return ngroups < target ? (ngroups > 0 ? ngroups : 1) : target;
 }
 
+// The LDS-ring backward takes 512 <= D <= 1536 (1 to 3 vectors per lane), whether or not
+// dres is given, so that fx_rms_norm_bwd and fx_rms_norm_bwd_add produce the same dw bits;
+// its ring depth is the largest S <= 3 whose 8 waves' slots fit the CU's 160 KB of LDS
+// (S >= 2 for every such D, with dres too).
+constexpr int kNormLdsBytes = 160 * 1024;
+static bool bwd_lds_fits(int D) { return D >= 512 && D <= 1536; }
+static int bwd_lds_depth(int D, int T) {
+    const int slot = T * D * 2 + 16;
+    const int s = kNormLdsBytes / ((kNormBwdThreads / 64) * slot);
+    return s < 3 ? s : 3;
+}
+
 }  // namespace fx
 
 using namespace fx;
@@ -446,6 +577,28 @@ static int rms_norm_bwd(const uint16_t* x, const uint16_t* dy, const uint16_t* d
         return check_launch("rms_dw_reduce");
     }
     FX_REQUIRE(work != nullptr, "%s: null workspace", who);
+    if (bwd_lds_fits(D)) {
+        const int NV = (D / 8 + 63) / 64, T = dres ? 3 : 2, S = bwd_lds_depth(D, T);
+        const int64_t rows_per_block = kNormBwdThreads / 64;
+        const int64_t P = std::min<int64_t>(kNormLdsBlocks, (N + rows_per_block - 1) / rows_per_block);
+        const size_t lds = (size_t)(kNormBwdThreads / 64) * S * (T * D * 2 + 16);
+        bool launched = false;
+#define FX_LDS(NV_, T_, S_)                                                                            \
+    if (NV == NV_ && T == T_ && S == S_) {                                                             \
+        hipLaunchKernelGGL((rms_bwd_lds_kernel<NV_, T_, S_>), dim3((unsigned)P), dim3(kNormBwdThreads), \
+                           lds, (hipStream_t)stream, x, dy, dres, w, rstd, dx, work, N, (int)D);       \
+        launched = true;                                                                               \
+    }
+        // the (vectors, tensors, depth) triples 512 <= D <= 1536 gives
+        FX_LDS(1, 2, 3) FX_LDS(2, 2, 3) FX_LDS(3, 2, 3)
+        FX_LDS(1, 3, 3) FX_LDS(2, 3, 3) FX_LDS(3, 3, 3) FX_LDS(3, 3, 2)
+#undef FX_LDS
+        FX_REQUIRE(launched, "%s: no LDS backward for D=%d", who, D);
+        if (int e = check_launch("rms_norm_bwd")) return e;
+        hipLaunchKernelGGL(rms_dw_reduce_kernel, dim3((D + 7) / 8), dim3(256), 0, (hipStream_t)stream,
+                           (const float*)work, P, (int)D, dw_f32, dw);
+        return check_launch("rms_dw_reduce");
+    }
     const RowShape s = pick_bwd_shape(D);
     const int G = kNormBwdThreads / s.lpr;
     const int64_t P = bwd_blocks((N + G - 1) / G);  // every block gets a row group's worth
