@@ -121,7 +121,8 @@ int fx_ce_loss_finalize(const float* row_loss, int64_t N, const float* inv_n,
 
 /* grad *= (*g) / applied[src]; applied[1 - src] = *g.  `applied` holds two floats
  * (the multiplier already in grad lives in slot src; the caller flips src after each
- * call), so no block reads the slot that is written.  Exits at once when the ratio is
+ * call), so no block reads the slot that is written.  src == -1: grad holds multiplier
+ * 1 (applied is not read) and *g goes to applied[1].  Exits at once when the ratio is
  * 1, so the usual loss.backward() (g == 1) costs one tiny launch and no pass over grad.
  * Replaces _FusedCE.backward's `grad * g` (ml/fxlm/cross_entropy.py:90-93). */
 int fx_ce_scale_grad(uint16_t* grad, int64_t numel, const float* g, float* applied,

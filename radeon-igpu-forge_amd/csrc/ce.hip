@@ -221,8 +221,8 @@ __global__ void __launch_bounds__(256)
 ce_scale_grad_kernel(uint16_t* __restrict__ grad, int64_t numel, const float* __restrict__ g,
                      float* __restrict__ applied, int src) {
     const float gv = *g;
-    const float f = gv / applied[src];
-    if (blockIdx.x == 0 && threadIdx.x == 0) applied[1 - src] = gv;  // no block reads this slot
+    const float f = gv / (src < 0 ? 1.f : applied[src]);
+    if (blockIdx.x == 0 && threadIdx.x == 0) applied[src == 1 ? 0 : 1] = gv;  // no block reads this slot
     if (f == 1.f) return;
     const int64_t stride = (int64_t)gridDim.x * 256;
     const int64_t n8 = numel >> 3;
@@ -311,16 +311,19 @@ extern "C" int fx_ce_fwd_grad(const fxCEArgs* args, void* stream) {
     const bool vec = (a.V % 8 == 0) && (a.ld % 8 == 0) && (((uintptr_t)a.logits & 15) == 0) &&
                      (a.grad == nullptr || ((a.ldg % 8 == 0) && (((uintptr_t)a.grad & 15) == 0)));
     const int64_t V8 = a.V / 8;
-    // block size: the first of 64, 256, 512, 768 threads that holds the row in at most 10
-    // vectors per lane, else the first of 64, 256, 512, 1024 with at most 16 (V = 50304:
-    // 768 x 9, 575 us against 580 us for 512 x 13 at [16384, 50304])
+    // block size: the first of 64, 256, 512, 768, 1024 threads that holds the row in at
+    // most 8 vectors per lane, else the first of 64, 256, 512, 1024 with at most 16.  Fewer
+    // vectors per lane shorten the phase in which a row's block computes instead of
+    // loading: at [16384, 50304] 1024 x 7 ran 548 us against 560 us for 768 x 9 and 576 us
+    // for 512 x 13 (one process, medians), and a plain copy with the same access pattern
+    // 582 us.
     int nt = 0, nv = 0;
     if (vec) {
-        static const int nts10[] = {64, 256, 512, 768};
+        static const int nts8[] = {64, 256, 512, 768, 1024};
         static const int nts16[] = {64, 256, 512, 1024};
-        for (int cand : nts10) {
+        for (int cand : nts8) {
             const int64_t need = (V8 + cand - 1) / cand;
-            if (need <= 10) {
+            if (need <= 8) {
                 nt = cand;
                 nv = (int)need;
                 break;
@@ -364,7 +367,7 @@ extern "C" int fx_ce_loss_finalize(const float* row_loss, int64_t N, const float
 extern "C" int fx_ce_scale_grad(uint16_t* grad, int64_t numel, const float* g, float* applied,
                                 int32_t src, void* stream) {
     FX_REQUIRE(g != nullptr && applied != nullptr, "fx_ce_scale_grad: null scalar");
-    FX_REQUIRE(src == 0 || src == 1, "fx_ce_scale_grad: src=%d must be 0 or 1", src);
+    FX_REQUIRE(src >= -1 && src <= 1, "fx_ce_scale_grad: src=%d must be -1, 0 or 1", src);
     FX_REQUIRE(numel >= 0 && (numel == 0 || grad != nullptr), "fx_ce_scale_grad: bad grad");
     FX_REQUIRE(((uintptr_t)grad & 15) == 0, "fx_ce_scale_grad: grad not 16-byte aligned");
     // one launch whatever the ratio (the kernel writes applied[1 - src]); a grid-stride

@@ -90,9 +90,9 @@ class _FusedCE(torch.autograd.Function):
             grad = torch.empty(N, V, device=dev, dtype=torch.bfloat16)
         _ce_rows(logits, target, grad, row_loss, mul, ignore_index)
         ctx.save_for_backward(grad)
-        # applied[0] = 1: the multiplier in grad as written; the first backward's kernel
-        # stores its g in applied[1]
-        ctx.applied = torch.ones(2, device=dev, dtype=torch.float32)
+        # the first backward's kernel takes the multiplier in grad as written to be 1
+        # (src -1) and stores its g in applied[1]
+        ctx.applied = torch.empty(2, device=dev, dtype=torch.float32)
         ctx.calls = 0
         return _finalize(row_loss, inv_n)
 
@@ -104,7 +104,7 @@ class _FusedCE(torch.autograd.Function):
         if ctx.calls == 1:
             # the usual single backward: scale the saved dlogits in place (no pass at all
             # when g == 1) and hand them over
-            call("fx_ce_scale_grad", ptr(grad), grad.numel(), ptr(g32), ptr(ctx.applied), 0,
+            call("fx_ce_scale_grad", ptr(grad), grad.numel(), ptr(g32), ptr(ctx.applied), -1,
                  stream_of(grad))
             return grad, None, None
         # a further backward through a retained graph: a fresh tensor, so the gradient the
