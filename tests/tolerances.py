@@ -1,7 +1,12 @@
 """Parity tolerances of this build's kernels against the oracle, stated once for every test.
 
 * Attention and linear outputs / gradients (bf16 results of bf16 inputs):
-  max |ours - fp32 oracle| <= 2e-2.
+  |ours - oracle| <= 2^-8 |oracle| + f * max|oracle| elementwise (`oracle_close`), with
+  f = FRAC_OUT = 1e-3 for a product rounded once (linear outputs) and f = FRAC_GRAD =
+  4e-3 for results that pass through bf16 intermediates (attention's P and dS, the
+  linear backward's dh): twice the largest excess measured over the test shapes
+  (2.0e-3 for attention dQ, 2.2e-3 for a linear dW), so that a systematic error of a
+  percent of the largest value anywhere fails.
 * bf16 results of larger magnitude (RMSNorm y/dx on N(0, 3) inputs, the
   reference selftest's distribution): |ours - oracle| <= 2e-2 + 2^-8 |oracle|
   (the bf16 rounding of the result alone is up to 2^-9 |oracle|).
@@ -24,6 +29,16 @@ def bf16_close(ours, ref, atol=ATOL_BF16, rtol=RTOL_BF16):
     """True when |ours - ref| <= atol + rtol |ref| elementwise."""
     o, r = ours.double().cpu(), ref.double().cpu()
     return bool(((o - r).abs() <= atol + rtol * r.abs()).all())
+
+
+FRAC_OUT = 1e-3
+FRAC_GRAD = 4e-3
+
+
+def oracle_close(ours, ref, frac=FRAC_GRAD):
+    """|ours - ref| <= 2^-8 |ref| + frac * max|ref| elementwise (bf16 results)."""
+    r = ref.double().cpu()
+    return bf16_close(ours, r, atol=frac * float(r.abs().max()) + 1e-9, rtol=RTOL_BF16)
 
 
 def rel_err(ours, ref):
