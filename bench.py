@@ -295,7 +295,7 @@ def gpu_step_bench(torch, steps, warmup):
         loss = step(i)
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / steps
-    return {"ms_per_step": dt * 1e3, "tok_s": B * T / dt, "loss": float(loss),
+    return {"ms_per_step": dt * 1e3, "tok_s": B * T / dt, "loss": float(loss.detach()),
             "params": model.num_params(), "found_inf": float(opt._found_inf)}
 
 
