@@ -137,6 +137,14 @@ int fx_ce_lin_grad_scale(const float* dw, int64_t nw, const uint16_t* dx, int64_
                          const float* gs, float inv_value, uint16_t* dw_out, uint16_t* dx_out,
                          void* stream);
 
+/* fx_ce_lin_grad_scale for a bf16 dw: the weight gradient of a single-chunk linear-CE,
+ * the one bf16 product, which fp32 represents exactly, so the result is bit for bit that
+ * of converting dw to fp32 first (ml/fxlm/cross_entropy.py:135, 160-161) without the
+ * fp32 copy. */
+int fx_ce_lin_grad_scale_bf16w(const uint16_t* dw, int64_t nw, const uint16_t* dx, int64_t nx, const float* g,
+                               const float* gs, float inv_value, uint16_t* dw_out, uint16_t* dx_out,
+                               void* stream);
+
 /* ---- FlatAdamW ---------------------------------------------------------- */
 
 #define FX_ADAMW_MAX_TENSORS 64

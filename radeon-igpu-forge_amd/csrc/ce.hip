@@ -241,8 +241,10 @@ ce_scale_grad_kernel(uint16_t* __restrict__ grad, int64_t numel, const float* __
 // the product rounded as the separate fp32 operations round them), then
 // dw_out = bf16(dw * s) over nw fp32 elements and dx_out = bf16(dx * bf16(s)) over nx bf16
 // elements, 8 per thread and step with an element-wise tail.
+// WT: the weight gradient's element type, float or bf16 (uint16_t, exact in fp32)
+template <typename WT>
 __global__ void __launch_bounds__(256)
-ce_lin_grad_scale_kernel(const float* __restrict__ dw, int64_t nw, const uint16_t* __restrict__ dx, int64_t nx,
+ce_lin_grad_scale_kernel(const WT* __restrict__ dw, int64_t nw, const uint16_t* __restrict__ dx, int64_t nx,
                          const float* __restrict__ g, const float* __restrict__ gs, float inv_value,
                          uint16_t* __restrict__ dw_out, uint16_t* __restrict__ dx_out) {
     const float inv = gs != nullptr ? 1.f / *gs : inv_value;
@@ -253,9 +255,17 @@ ce_lin_grad_scale_kernel(const float* __restrict__ dw, int64_t nw, const uint16_
     const int64_t stride = (int64_t)gridDim.x * 256;
     const int64_t t0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
     for (int64_t v = t0; v < nw / 8; v += stride) {
-        const float4* p = reinterpret_cast<const float4*>(dw + v * 8);
-        const float4 lo = p[0], hi = p[1];
-        const float f[8] = {lo.x * sc, lo.y * sc, lo.z * sc, lo.w * sc, hi.x * sc, hi.y * sc, hi.z * sc, hi.w * sc};
+        float f[8];
+        if constexpr (sizeof(WT) == 4) {
+            const float4* p = reinterpret_cast<const float4*>(dw + v * 8);
+            const float4 lo = p[0], hi = p[1];
+            f[0] = lo.x; f[1] = lo.y; f[2] = lo.z; f[3] = lo.w;
+            f[4] = hi.x; f[5] = hi.y; f[6] = hi.z; f[7] = hi.w;
+        } else {
+            unpack8(ld16(dw + v * 8), f);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) f[j] *= sc;
         st16(dw_out + v * 8, pack8(f));
     }
     for (int64_t v = t0; v < nx / 8; v += stride) {
@@ -266,7 +276,11 @@ ce_lin_grad_scale_kernel(const float* __restrict__ dw, int64_t nw, const uint16_
         st16(dx_out + v * 8, pack8(f));
     }
     if (t0 == 0) {
-        for (int64_t i = nw / 8 * 8; i < nw; ++i) dw_out[i] = f32_to_bf16(dw[i] * sc);
+        for (int64_t i = nw / 8 * 8; i < nw; ++i) {
+            float w;
+            if constexpr (sizeof(WT) == 4) w = dw[i]; else w = bf16_to_f32(dw[i]);
+            dw_out[i] = f32_to_bf16(w * sc);
+        }
         for (int64_t i = nx / 8 * 8; i < nx; ++i) dx_out[i] = f32_to_bf16(bf16_to_f32(dx[i]) * sx);
     }
 }
@@ -380,18 +394,30 @@ extern "C" int fx_ce_scale_grad(uint16_t* grad, int64_t numel, const float* g, f
     return check_launch("ce_scale_grad");
 }
 
-extern "C" int fx_ce_lin_grad_scale(const float* dw, int64_t nw, const uint16_t* dx, int64_t nx, const float* g,
-                                    const float* gs, float inv_value, uint16_t* dw_out, uint16_t* dx_out,
-                                    void* stream) {
-    FX_REQUIRE(nw >= 0 && nx >= 0 && g != nullptr, "fx_ce_lin_grad_scale: bad arguments");
-    FX_REQUIRE((nw == 0 || (dw && dw_out)) && (nx == 0 || (dx && dx_out)), "fx_ce_lin_grad_scale: null pointer");
+template <typename WT>
+static int lin_grad_scale(const WT* dw, int64_t nw, const uint16_t* dx, int64_t nx, const float* g, const float* gs,
+                          float inv_value, uint16_t* dw_out, uint16_t* dx_out, void* stream, const char* who) {
+    FX_REQUIRE(nw >= 0 && nx >= 0 && g != nullptr, "%s: bad arguments", who);
+    FX_REQUIRE((nw == 0 || (dw && dw_out)) && (nx == 0 || (dx && dx_out)), "%s: null pointer", who);
     FX_REQUIRE(((((uintptr_t)dw) | ((uintptr_t)dx) | ((uintptr_t)dw_out) | ((uintptr_t)dx_out)) & 15) == 0,
-               "fx_ce_lin_grad_scale: buffers must be 16-byte aligned");
+               "%s: buffers must be 16-byte aligned", who);
     if (nw == 0 && nx == 0) return 0;
     const int64_t groups = (nw > nx ? nw : nx) / 8 + 1;
     int64_t blocks = (groups + 255) / 256;
     if (blocks > 8192) blocks = 8192;
-    hipLaunchKernelGGL(ce_lin_grad_scale_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, dw, nw,
-                       dx, nx, g, gs, inv_value, dw_out, dx_out);
+    hipLaunchKernelGGL(ce_lin_grad_scale_kernel<WT>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, dw,
+                       nw, dx, nx, g, gs, inv_value, dw_out, dx_out);
     return check_launch("ce_lin_grad_scale");
+}
+
+extern "C" int fx_ce_lin_grad_scale(const float* dw, int64_t nw, const uint16_t* dx, int64_t nx, const float* g,
+                                    const float* gs, float inv_value, uint16_t* dw_out, uint16_t* dx_out,
+                                    void* stream) {
+    return lin_grad_scale(dw, nw, dx, nx, g, gs, inv_value, dw_out, dx_out, stream, "fx_ce_lin_grad_scale");
+}
+
+extern "C" int fx_ce_lin_grad_scale_bf16w(const uint16_t* dw, int64_t nw, const uint16_t* dx, int64_t nx,
+                                          const float* g, const float* gs, float inv_value, uint16_t* dw_out,
+                                          uint16_t* dx_out, void* stream) {
+    return lin_grad_scale(dw, nw, dx, nx, g, gs, inv_value, dw_out, dx_out, stream, "fx_ce_lin_grad_scale_bf16w");
 }

@@ -115,6 +115,7 @@ SIGNATURES = {
     "fx_ce_loss_finalize": (c_int32, [_P, c_int64, _P, _P, _P]),
     "fx_ce_scale_grad": (c_int32, [_P, c_int64, _P, _P, c_int32, _P]),
     "fx_ce_lin_grad_scale": (c_int32, [_P, c_int64, _P, c_int64, _P, _P, c_float, _P, _P, _P]),
+    "fx_ce_lin_grad_scale_bf16w": (c_int32, [_P, c_int64, _P, c_int64, _P, _P, c_float, _P, _P, _P]),
     "fx_adamw_workspace": (c_int64, [ctypes.POINTER(fxTensorList), c_int32]),
     "fx_adamw_step": (c_int32, [ctypes.POINTER(fxAdamWState), ctypes.POINTER(fxTensorList),
                                 c_int32, _P]),

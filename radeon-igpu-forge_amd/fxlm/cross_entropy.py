@@ -159,9 +159,13 @@ class _LinearCE(torch.autograd.Function):
             _ce_rows(lg, target[r0:r1], lg, row_loss[r0:r1], mul, ignore_index)  # in place
             torch.mm(lg, weight, out=dx[r0:r1])                 # dx_c
             # the reference's dW.add_(torch.mm(dl.t(), xc).float()): a bf16 product,
-            # accumulated over the chunks in fp32 (ml/fxlm/cross_entropy.py:135)
+            # accumulated over the chunks in fp32 (ml/fxlm/cross_entropy.py:135); a single
+            # chunk's product stays bf16 (exact in fp32) and the backward reads it as such
             part = torch.mm(lg.t(), xc)                         # (V, D) bf16
-            dW = part.float() if dW is None else dW.add_(part)
+            if dW is None:
+                dW = part if r1 >= N else part.float()
+            else:
+                dW.add_(part)
             del lg
         if dW is None:
             dW = torch.zeros(V, D, device=dev, dtype=torch.float32)
@@ -180,12 +184,13 @@ class _LinearCE(torch.autograd.Function):
             gs_t = gs.detach().float().reshape(()) if torch.is_tensor(gs) else None
             gx = torch.empty_like(dx)
             gw = torch.empty(dW.shape, device=dW.device, dtype=torch.bfloat16)
-            call("fx_ce_lin_grad_scale", ptr(dW), dW.numel(), ptr(dx), dx.numel(), ptr(g32), ptr(gs_t),
+            fn = "fx_ce_lin_grad_scale_bf16w" if dW.dtype == torch.bfloat16 else "fx_ce_lin_grad_scale"
+            call(fn, ptr(dW), dW.numel(), ptr(dx), dx.numel(), ptr(g32), ptr(gs_t),
                  0.0 if gs_t is not None else 1.0 / gs, ptr(gw), ptr(gx), stream_of(dx))
             return gx, gw, None, None, None, None
         inv = torch.reciprocal(gs.float()) if torch.is_tensor(gs) else 1.0 / gs
         gx = dx * (g * inv)
-        gw = (dW * (g * inv)).to(ctx.wdtype)
+        gw = (dW.float() * (g * inv)).to(ctx.wdtype)
         return gx, gw, None, None, None, None
 
 

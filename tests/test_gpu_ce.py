@@ -158,6 +158,47 @@ def test_linear_ce(dev, N, D, V, gs):
     _assert_lin_grads(xq.grad, Wq.grad, rdx, rdW)
 
 
+@pytest.mark.parametrize("gs", [1.0, 3.0, None])
+def test_lin_grad_scale_bf16_weight_gradient_is_exact(dev, gs):
+    # a single chunk keeps its weight-gradient product in bf16: scaling it must give the
+    # bits of scaling its fp32 copy, for dx as well, with a float or a tensor grad_scale
+    from fxgpu.abi import call, ptr, stream_of
+    g = torch.Generator(device=dev).manual_seed(4)
+    dw16 = (torch.randn(1003, device=dev, generator=g) * 50).bfloat16()   # odd length: the tail too
+    dx = torch.randn(517, device=dev, generator=g).bfloat16()
+    gt = torch.tensor(0.37, device=dev)
+    gs_t = torch.tensor(1024.0, device=dev) if gs is None else None
+    inv = 0.0 if gs is None else 1.0 / gs
+    outs = []
+    for fn, dw in (("fx_ce_lin_grad_scale", dw16.float()), ("fx_ce_lin_grad_scale_bf16w", dw16)):
+        gw, gx = torch.empty_like(dw16), torch.empty_like(dx)
+        call(fn, ptr(dw), dw.numel(), ptr(dx), dx.numel(), ptr(gt), ptr(gs_t), inv, ptr(gw), ptr(gx), stream_of(dx))
+        outs.append((gw, gx))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+
+
+@pytest.mark.parametrize("gs", [1.0, None])
+def test_linear_ce_single_chunk(dev, gs):
+    # the default chunking holds these rows in one chunk (bf16 weight-gradient product)
+    from fxlm.cross_entropy import _auto_chunk, linear_cross_entropy
+    N, D, V = 300, 256, 4096
+    assert _auto_chunk(D, V) >= N
+    torch.manual_seed(9)
+    x = torch.randn(N, D).bfloat16()
+    W = (torch.randn(V, D) * 0.02).bfloat16()
+    tg = torch.randint(0, V, (N,))
+    tg[::7] = -100
+    grad_scale = torch.tensor(4096.0, device=dev) if gs is None else gs
+    xq, Wq = x.to(dev).requires_grad_(), W.to(dev).requires_grad_()
+    loss = linear_cross_entropy(xq, Wq, tg.to(dev), grad_scale=grad_scale)
+    loss.backward()
+    rl, _, _ = oce.linear_cross_entropy(x, W, tg)
+    assert abs(float(loss) - float(rl)) <= RTOL_LOSS * abs(float(rl))
+    rdx, rdW = _lin_ce_grads_bf16_points(x, W, tg)
+    _assert_lin_grads(xq.grad, Wq.grad, rdx, rdW)
+
+
 def _lin_ce_grads_bf16_points(x, W, tg, rows=None, chunk_rows=None):
     """(dx, dW) in fp64 with the path's rounding points: logits rounded to bf16 (the
     logits GEMM writes bf16), dlogits rounded to bf16 (the CE kernel's output), dW
