@@ -22,6 +22,7 @@
 #include <math.h>
 
 #include "fx_mfma.h"
+#include "gemm_kloop.h"
 
 namespace fx {
 
@@ -284,6 +285,160 @@ __global__ void __launch_bounds__(kGThreads, 1) gemm_bias_act_kernel(GemmArgs a)
             }
         }
     }
+}
+
+// ---------------------------------------------------------------------------
+// The same product for dense rows on whole tiles (M % 256 == 0, N % (64 NJ) == 0,
+// K % 96 == 0): 4 waves of 128 x (32 NJ), one workgroup per 256 x (64 NJ) tile, the K loop
+// a single generated inline-asm statement (gemm_kloop.h, from gemm_kloop_gen.py, which
+// documents the schedule and checks it on the CPU).  With the accumulators in AGPRs (one
+// wave per SIMD) and the LDS operand reads interleaved with the MFMAs by hand, the loop
+// runs at the MFMA rate the compiler-scheduled kernel above does not reach.  The products
+// are the same MFMAs on the same operands in the same K order as gemm_bias_act_kernel,
+// and the epilogue rounds the same way, so the results are bit-identical.
+// NJ = 4: 256 x 256 tiles; NJ = 3: 256 x 192 tiles (N = 768 is 4 of them: 256 tiles for
+// M = 16384, one per CU, where 256 x 256 tiles would leave a quarter of the CUs idle).
+__device__ __forceinline__ void raw_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+template <int NJ>
+struct FastGemm {
+    static constexpr int kStage = NJ == 4 ? FX_GEMM_STAGE_BYTES_NJ4 : FX_GEMM_STAGE_BYTES_NJ3;
+    static constexpr int kLoads = NJ == 4 ? FX_GEMM_LOADS_NJ4 : FX_GEMM_LOADS_NJ3;
+    static constexpr int kPW = kLoads - 5;   // W loads per wave and stage (X: 5)
+    static constexpr int kTN = 64 * NJ;      // tile columns
+    static constexpr int kXBytes = 256 * 80; // X rows of a stage: 256 x (32 bf16 + 8 of padding)
+    static constexpr int kLDE = 32 * NJ + 8; // epilogue staging row stride (elements)
+    static constexpr int kWaveLds = 3 * kStage / 4;
+    static_assert(kStage == kXBytes + 4 * kPW * 1024, "stage = X rows + the W load slots");
+    static_assert(32 * kLDE * 2 <= kWaveLds && kWaveLds % 16 == 0, "epilogue staging fits a wave's share");
+};
+
+// EPI: bit 0 GELU, bit 1 pre-activation H out, bit 2 bias (no residual, gather or Xg)
+template <int NJ, int EPI>
+__global__ void __launch_bounds__(256, 1) gemm_fast_kernel(GemmArgs a) {
+    using G = FastGemm<NJ>;
+    constexpr bool kGelu = EPI & 1, kH = EPI & 2, kBias = EPI & 4;
+    __shared__ __attribute__((aligned(16))) unsigned char lds[3 * G::kStage];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 5;
+    const int wm = (wave >> 1) * 128, wn = (wave & 1) * 32 * NJ;
+    int m0, n0, nt;
+    gemm_tile(blockIdx.x, a.M / 256, a.N / G::kTN, m0, n0, nt);
+    n0 = nt * G::kTN;
+    const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+    // load slots: wave-instruction q = wave + 4 t covers 64 16-byte slots, 5 to a row (the
+    // 5th, padding, loads the row's last chunk again); W slots past the tile's rows (the
+    // 16th instruction of NJ = 3) load its last row into the never-read pad
+    const uint16_t* pa[5];
+    const uint16_t* pb[G::kPW];
+#pragma unroll
+    for (int t = 0; t < 5; ++t) {
+        const int s = (wave + 4 * t) * 64 + lane;
+        const int r = s / 5, c = min(s - 5 * r, 3);
+        pa[t] = a.A + (int64_t)(m0 + r) * a.lda + 8 * c;
+    }
+#pragma unroll
+    for (int t = 0; t < G::kPW; ++t) {
+        const int s = (wave + 4 * t) * 64 + lane;
+        const int r = s / 5, c = min(s - 5 * r, 3);
+        pb[t] = a.B + (int64_t)(n0 + min(r, G::kTN - 1)) * a.ldb + 8 * c;
+    }
+#pragma unroll
+    for (int st = 0; st < 3; ++st) {  // K steps 0, 1, 2 into stages 0, 1, 2
+#pragma unroll
+        for (int t = 0; t < 5; ++t) dma16(pa[t] + 32 * st, base + st * G::kStage + (wave + 4 * t) * 1024);
+#pragma unroll
+        for (int t = 0; t < G::kPW; ++t)
+            dma16(pb[t] + 32 * st, base + st * G::kStage + G::kXBytes + (wave + 4 * t) * 1024);
+    }
+    const uint16_t* qa[5];
+    const uint16_t* qb[G::kPW];
+#pragma unroll
+    for (int t = 0; t < 5; ++t) qa[t] = pa[t] + 96;
+#pragma unroll
+    for (int t = 0; t < G::kPW; ++t) qb[t] = pb[t] + 96;
+    uint32_t vA[3], vB[3];
+#pragma unroll
+    for (int s = 0; s < 3; ++s) {
+        vA[s] = base + s * G::kStage + (wm + (lane & 31)) * 80 + 16 * g;
+        vB[s] = base + s * G::kStage + G::kXBytes + (wn + (lane & 31)) * 80 + 16 * g;
+    }
+    const uint32_t sbase = base + wave * 1024;
+    uint32_t iters = (uint32_t)(a.K / 32 - 3) / 3;  // 3-step iterations before the 3-step tail
+    uint32_t m0save;
+    f32x16 acc[4 * NJ];
+#pragma unroll
+    for (int k = 0; k < 4 * NJ; ++k) acc[k] = f32x16{};
+    bf16x8 F[3][4 + NJ];
+    if constexpr (NJ == 4)
+        asm volatile(FX_GEMM_KLOOP_NJ4 : FX_GEMM_KLOOP_OUTS_NJ4 : FX_GEMM_KLOOP_INS_NJ4 : "memory");
+    else
+        asm volatile(FX_GEMM_KLOOP_NJ3 : FX_GEMM_KLOOP_OUTS_NJ3 : FX_GEMM_KLOOP_INS_NJ3 : "memory");
+    (void)F;
+    (void)m0save;
+
+    // epilogue.  acc[4 j + i] holds C^T as in gemm_bias_act_kernel: lane l has row
+    // m0 + wm + 32 i + l%32 and the columns n0 + wn + 32 j + 8 q + 4 g + 0..3.  Each 32-row
+    // block leaves through the wave's share of the (now free) stages: 8-byte writes from the
+    // MFMA layout, read back and stored as 16-byte row chunks, 32 NJ columns contiguous.
+    raw_barrier();  // every wave is done reading the stages (the loop ends with no load in flight)
+    uint16_t* stg = reinterpret_cast<uint16_t*>(lds + wave * G::kWaveLds);
+    float bias[NJ][4][4];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                bias[j][q][e] = kBias ? bf16_to_f32(a.bias[n0 + wn + 32 * j + 8 * q + 4 * g + e]) : 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int mb = m0 + wm + 32 * i;
+#pragma unroll
+        for (int pass = kH ? 0 : 1; pass < 2; ++pass) {
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    float v[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        float h = acc[4 * j + i][4 * q + e];
+                        if (kBias) h += bias[j][q][e];
+                        if (pass == 1 && kGelu) h = gelu_tanh(h);
+                        v[e] = h;
+                    }
+                    *reinterpret_cast<uint2*>(stg + (lane & 31) * G::kLDE + 32 * j + 8 * q + 4 * g) =
+                        make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+                }
+            uint16_t* out = pass == 0 ? a.H : a.C;
+            const int64_t ld = pass == 0 ? a.ldh : a.ldc;
+#pragma unroll
+            for (int k = 0; k < 2 * NJ; ++k) {
+                const int idx = lane + 64 * k;
+                const int r = idx / (4 * NJ), c = idx - r * (4 * NJ);
+                st16(out + (int64_t)(mb + r) * ld + n0 + wn + 8 * c,
+                     *reinterpret_cast<const uint4*>(stg + r * G::kLDE + 8 * c));
+            }
+        }
+    }
+}
+
+// 4 or 3 (the tile width in 64-column units) when gemm_fast_kernel takes the product, else 0:
+// of the tile widths that divide N, the one with the fewest MFMA rounds per CU
+static int fast_gemm_nj(const GemmArgs& a) {
+    if (a.idx || a.res || a.nw || a.Xg) return 0;
+    if (a.M % 256 || a.K % 96 || a.ldb != a.K || a.lda % 8 || !a.vec_c || (a.H && !a.vec_h)) return 0;
+    const int64_t cus = device_cus();
+    int64_t best = 0, nj = 0;
+    for (int w : {4, 3}) {
+        if (a.N % (64 * w)) continue;
+        const int64_t tiles = (int64_t)(a.M / 256) * (a.N / (64 * w));
+        const int64_t cost = (tiles + cus - 1) / cus * w;
+        if (nj == 0 || cost < best) best = cost, nj = w;
+    }
+    return (int)nj;
 }
 
 // ---------------------------------------------------------------------------
@@ -646,6 +801,21 @@ static int linear_fwd(GemmArgs a, hipStream_t stream) {
     a.vec_h = a.H && a.ldh % 8 == 0 && ((uintptr_t)a.H & 15) == 0;
     const int64_t tiles = ((int64_t)(a.M + kGBM - 1) / kGBM) * ((a.N + kGBN - 1) / kGBN);
     FX_REQUIRE(tiles < 0x7fffffffLL, "fx_linear_fwd: too many tiles");
+    if (const int nj = fast_gemm_nj(a)) {
+        const int64_t ft = (int64_t)(a.M / 256) * (a.N / (64 * nj));
+        const int fe = (a.act == 1 ? 1 : 0) | (a.H ? 2 : 0) | (a.bias ? 4 : 0);
+#define FX_FAST_EPI(J, E) \
+    case E: hipLaunchKernelGGL((gemm_fast_kernel<J, E>), dim3((unsigned)ft), dim3(256), 0, stream, a); break;
+        if (nj == 4) {
+            switch (fe) { FX_FAST_EPI(4, 0) FX_FAST_EPI(4, 1) FX_FAST_EPI(4, 2) FX_FAST_EPI(4, 3)
+                          FX_FAST_EPI(4, 4) FX_FAST_EPI(4, 5) FX_FAST_EPI(4, 6) FX_FAST_EPI(4, 7) }
+        } else {
+            switch (fe) { FX_FAST_EPI(3, 0) FX_FAST_EPI(3, 1) FX_FAST_EPI(3, 2) FX_FAST_EPI(3, 3)
+                          FX_FAST_EPI(3, 4) FX_FAST_EPI(3, 5) FX_FAST_EPI(3, 6) FX_FAST_EPI(3, 7) }
+        }
+#undef FX_FAST_EPI
+        return check_launch("gemm_fast");
+    }
     // persistent grid: one workgroup per CU (the LDS of one is 147 KB)
     const int64_t cus = device_cus();
     const int64_t grid = tiles < cus ? tiles : cus;

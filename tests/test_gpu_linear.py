@@ -321,3 +321,50 @@ def test_linear_ex_rejects(dev):
         linear_ex(x, W, norm_weight=torch.ones(64, device=dev, dtype=torch.bfloat16))
     with pytest.raises(ValueError):
         linear_ex(x, W, residual=torch.zeros(65, 31, device=dev, dtype=torch.bfloat16))
+
+
+# ---- whole-tile kernel (M % 256 == 0, N % 192 or % 256 == 0, K % 96 == 0) ----------------
+# fx_linear_fwd takes such shapes on its hand-scheduled kernel.  It computes the same MFMAs
+# on the same operands in the same K order as the general tiled kernel and rounds the same
+# way, so the two agree bit for bit.  The general kernel's result for an element does not
+# depend on M or N, so it is read from the same operands with 8 more rows and columns
+# (a shape the whole-tile kernel does not take).
+
+def _linear_fwd(x, W, b, act, want_h):
+    from fxgpu.abi import call, ptr, stream_of
+    M, K = x.shape
+    N = W.shape[0]
+    y = torch.empty(M, N, device=x.device, dtype=torch.bfloat16)
+    h = torch.empty_like(y) if want_h else None
+    call("fx_linear_fwd", ptr(x), x.stride(0), None, 0, 0, ptr(W), ptr(b), ptr(y), ptr(h), None, M, N, K, act,
+         stream_of(x))
+    return y, h
+
+
+@pytest.mark.parametrize("M,K,N,act,bias,want_h,pad_k", [
+    (512, 96, 256, 1, True, True, 0),      # 256-wide tiles; one K step group: the loop's tail only
+    (512, 192, 192, 0, False, False, 0),   # 192-wide tiles, one loop iteration
+    (1024, 768, 768, 0, False, False, 64), # proj: 192-wide (a round of 16 tiles), rows of X strided
+    (768, 768, 2304, 0, True, False, 0),   # qkv widths
+    (256, 3072, 768, 1, False, True, 0),   # fc2 depth
+    (16384, 768, 3072, 1, False, True, 0), # the cfg5 MLP fc (256-wide tiles): GELU and the pre-activation
+])
+def test_whole_tile_kernel_matches_general_kernel(dev, M, K, N, act, bias, want_h, pad_k):
+    g = torch.Generator(device=dev).manual_seed(M + K + N)
+    xs = torch.randn(M + 8, K + pad_k, device=dev, generator=g).bfloat16()
+    Ws = (torch.randn(N + 8, K, device=dev, generator=g) * K ** -0.5).bfloat16()
+    bs = (torch.randn(N + 8, device=dev, generator=g) * 0.1).bfloat16() if bias else None
+    x, W, b = xs[:M, :K], Ws[:N], (bs[:N] if bias else None)
+    print(f"whole-tile fwd M={M} K={K} N={N} act={act} bias={bias} h={want_h} ldx={x.stride(0)}", flush=True)
+    y, h = _linear_fwd(x, W, b, act, want_h)
+    y_gen, h_gen = _linear_fwd(xs[:, :K], Ws, bs, act, want_h)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_gen[:M, :N])
+    if want_h:
+        assert torch.equal(h, h_gen[:M, :N])
+    ref = x.float() @ W.float().t() + (b.float() if bias else 0)
+    if want_h:
+        assert oracle_close(h, ref, FRAC_OUT)
+    if act:
+        ref = F.gelu(ref, approximate="tanh")
+    assert oracle_close(y, ref, FRAC_OUT)
