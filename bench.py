@@ -202,9 +202,22 @@ def bench_linear(torch):
         t = time_us(torch, lambda: fused_linear(x, W, None, "gelu_tanh"))
         t_ref = time_us(torch, lambda: torch.nn.functional.gelu(x @ W.t(), approximate="tanh"))
     f = 2.0 * M * K * N
+    del W
+    # the block's projections (y = x W^T): this build's routing (linear) against torch.mm
+    from fxgpu.fused_linear import linear
+    proj = {}
+    for name, (n, kk) in {"qkv": (2304, 768), "proj": (768, 768), "fc2": (768, 3072)}.items():
+        xp = torch.randn(M, kk, device="cuda", generator=g).bfloat16()
+        wp = (torch.randn(n, kk, device="cuda", generator=g) * 0.02).bfloat16()
+        with torch.no_grad():
+            t_o = time_us(torch, lambda: linear(xp, wp))
+            t_l = time_us(torch, lambda: torch.mm(xp, wp.t()))
+        proj[name] = {"us": round(t_o, 2), "tflops": round(2.0 * M * n * kk / t_o / 1e6, 1),
+                      "library_mm_us": round(t_l, 2)}
+        del xp, wp
     return {"shape": [M, K, N], "fwd_us": round(t, 2), "tflops": round(f / t / 1e6, 1),
             "frac_of_bf16_peak": round(f / t / 1e6 / BF16_PEAK_TFLOPS, 4),
-            "hipblaslt_mm_plus_gelu_us": round(t_ref, 2)}
+            "hipblaslt_mm_plus_gelu_us": round(t_ref, 2), "projections": proj}
 
 
 def bench_decode(torch):

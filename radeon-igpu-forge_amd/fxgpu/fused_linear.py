@@ -12,8 +12,8 @@
   on the library GEMM and dW = dh^T x on this build's split-K weight-gradient GEMM.
 * ``linear(x, weight)`` -- y = x W^T (no bias) with the same backward split: the
   GPT's qkv, proj and fc2 projections.  Forwards of at most FEW_ROWS rows (decode
-  steps) run on the few-row kernel behind fx_linear_fwd, larger ones on the library
-  GEMM.
+  steps) run on the few-row kernel behind fx_linear_fwd, the whole_tiles() shapes on
+  its whole-tile kernel, the others on the library GEMM.
 * ``linear_wgrad(dy, x)`` -- dW = dy^T x for dy (T, N) and x (T, K): the weight
   gradient that ml/fxgpu/fused_linear.py:90-101 computes with rocBLAS.
 * ``linear_ex(x, W, bias, residual, norm_weight, eps, activation)`` -- inference
@@ -62,11 +62,22 @@ def linear_wgrad(dy, x):
 
 
 # Up to this many rows the forward GEMM is a stream over the weight (decoding, small
-# batches) and runs on this build's few-row kernel; above it on the library GEMM.
+# batches) and runs on this build's few-row kernel; above it on the library GEMM, except
+# for the shapes of whole_tiles().
 FEW_ROWS = 64
 
 
-def _few_rows(x2, weight):
+def whole_tiles(M, N, K):
+    """Shapes that fx_linear_fwd runs on its whole-tile kernel (M % 256 == 0, N % 192 or
+    % 256 == 0, K % 96 == 0) and where that kernel measured faster than the library GEMM:
+    K up to 1024 (the cfg5 qkv and proj, 64 and 22.6 us against 66 and 25.3 us).  With
+    K = 3072 and N = 768 (fc2: one tile per CU) the library GEMM is faster (61.7 against
+    69.8 us)."""
+    return M % 256 == 0 and K % 96 == 0 and K <= 1024 and (N % 256 == 0 or N % 192 == 0)
+
+
+def _native_fwd(x2, weight):
+    """y = x2 W^T on fx_linear_fwd (the few-row kernel for M <= FEW_ROWS, else the tiled ones)."""
     M, K = x2.shape
     y = torch.empty(M, weight.shape[0], device=x2.device, dtype=torch.bfloat16)
     call("fx_linear_fwd", ptr(x2), x2.stride(0), None, 0, 0, ptr(weight), None, ptr(y), None, None,
@@ -84,9 +95,10 @@ class Linear(torch.autograd.Function):
         if weight.dim() != 2 or weight.shape[1] != x.shape[-1]:
             raise ValueError(f"weight must be (N, {x.shape[-1]}), got {tuple(weight.shape)}")
         x2 = _rows(x)
-        if (0 < x2.shape[0] <= FEW_ROWS and x2.shape[1] % 8 == 0 and x2.is_cuda and weight.is_contiguous()
-                and weight.data_ptr() % 16 == 0):
-            y = _few_rows(x2, weight)
+        M, K = x2.shape
+        native = x2.is_cuda and weight.is_contiguous() and weight.data_ptr() % 16 == 0 and K % 8 == 0
+        if native and (0 < M <= FEW_ROWS or whole_tiles(M, weight.shape[0], K)):
+            y = _native_fwd(x2, weight)
         else:
             y = torch.mm(x2, weight.t())
         ctx.save_for_backward(x2, weight)
