@@ -20,9 +20,11 @@
 // transposed layout with 8-byte stores scattered over 32 rows measured 1.6x slower).
 // Tiles sharing an A row panel are dealt to one XCD (shared L2).
 #include <math.h>
+#include <stdlib.h>
 
 #include "fx_mfma.h"
 #include "gemm_kloop.h"
+#include "gemm_wgrad_kloop.h"
 
 namespace fx {
 
@@ -425,10 +427,18 @@ __global__ void __launch_bounds__(256, 1) gemm_fast_kernel(GemmArgs a) {
     }
 }
 
+// FX_GEMM_GENERAL=1 in the environment routes every product to the general kernels
+// (gemm_bias_act_kernel, gemm_wgrad_kernel): a diagnostic switch, read on every call, that
+// lets a test compare the whole-tile kernels with them on the same shapes
+static bool whole_tile_kernels_enabled() {
+    const char* v = getenv("FX_GEMM_GENERAL");
+    return !(v && v[0] == '1');
+}
+
 // 4 or 3 (the tile width in 64-column units) when gemm_fast_kernel takes the product, else 0:
 // of the tile widths that divide N, the one with the fewest MFMA rounds per CU
 static int fast_gemm_nj(const GemmArgs& a) {
-    if (a.idx || a.res || a.nw || a.Xg) return 0;
+    if (a.idx || a.res || a.nw || a.Xg || !whole_tile_kernels_enabled()) return 0;
     if (a.M % 256 || a.K % 96 || a.ldb != a.K || a.lda % 8 || !a.vec_c || (a.H && !a.vec_h)) return 0;
     const int64_t cus = device_cus();
     int64_t best = 0, nj = 0;
@@ -570,6 +580,102 @@ __global__ void __launch_bounds__(kGThreads, 1) gemm_wgrad_kernel(WgradArgs a) {
                 }
             }
     }
+}
+
+// The same product on whole tiles (M % 256 == 0, N % 256 == 0, K % 32 == 0) with the K loop
+// generated by gemm_wgrad_gen.py (gemm_wgrad_kloop.h; the generator documents the schedule
+// and checks it on the CPU): 4 waves of 128 x 128, accumulators in AGPRs, 32-token steps in
+// 3 LDS stages loaded two steps ahead.  The slices, their token ranges, the transposed
+// operand reads (lds_op_t's K permutation) and the MFMA order over K are those of
+// gemm_wgrad_kernel, so its partial tiles, and the reduced result, are bit-identical.
+__global__ void __launch_bounds__(256, 1) gemm_wgrad_fast_kernel(WgradArgs a) {
+    constexpr int kStage = FX_WGRAD_STAGE_BYTES, kRow = FX_WGRAD_ROW_BYTES;
+    static_assert(kStage == 2 * 32 * kRow && kRow == 2 * (256 + 32) && FX_WGRAD_LOADS == 9, "stage layout");
+    __shared__ __attribute__((aligned(16))) unsigned char lds[3 * kStage];
+    const int nn = a.N / 256;
+    const int ntiles = (a.M / 256) * nn;
+    const int sl = blockIdx.x / ntiles, t = blockIdx.x - sl * ntiles;
+    const int m0 = (t / nn) * 256, n0 = (t - (t / nn) * nn) * 256;
+    const int nk64 = (a.K + 63) / 64;
+    const int kb = (int)((int64_t)nk64 * sl / a.slices), ke = (int)((int64_t)nk64 * (sl + 1) / a.slices);
+    const int t0 = 64 * kb, nsteps = (min(64 * ke, a.K) - t0) / 32;  // >= 3: the host checks
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = (wave >> 1) * 128, wn = (wave & 1) * 128;
+    const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+    // load slots: wave-instruction q = wave + 4 t (t = 0..8) covers 64 of the 2 x 1152 16-byte
+    // slots of a stage (A rows, then B rows; 36 slots a row, the last 4 padding that loads
+    // the row's first chunks again)
+    const uint16_t* P[9];
+    int64_t ld[9];
+#pragma unroll
+    for (int u = 0; u < 9; ++u) {
+        const int q = wave + 4 * u;
+        const bool isa = q < 18;
+        const int s = (isa ? q : q - 18) * 64 + lane;
+        const int r = s / 36;
+        int c = s - 36 * r;
+        if (c >= 32) c -= 32;
+        ld[u] = isa ? a.lda : a.ldb;
+        P[u] = (isa ? a.A + m0 : a.B + n0) + (int64_t)(t0 + r) * ld[u] + 8 * c;
+    }
+    const uint32_t phase = __builtin_amdgcn_readfirstlane((3 - nsteps % 3) % 3);
+    uint32_t iters = __builtin_amdgcn_readfirstlane((nsteps - 3 + (int)phase) / 3);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {  // steps 0, 1, 2 into stages phase + j (mod 3)
+        const int st = (j + (int)phase) % 3;
+#pragma unroll
+        for (int u = 0; u < 9; ++u) dma16(P[u] + (int64_t)32 * j * ld[u], base + st * kStage + (wave + 4 * u) * 1024);
+    }
+#pragma unroll
+    for (int u = 0; u < 9; ++u) P[u] += (int64_t)96 * ld[u];
+    const uint64_t stride_a = (uint64_t)a.lda * 64, stride_b = (uint64_t)a.ldb * 64;  // 32 rows, bytes
+    const uint64_t stride_4 = wave < 2 ? stride_a : stride_b;
+    const int grp = lane >> 4, s16 = lane & 15;
+    const uint32_t rowpart = (4 * (grp >> 1) + (s16 >> 2)) * kRow, colpart = (16 * (grp & 1) + 4 * (s16 & 3)) * 2;
+    uint32_t vA[3], vB[3];
+#pragma unroll
+    for (int s = 0; s < 3; ++s) {
+        vA[s] = base + s * kStage + rowpart + wm * 2 + colpart;
+        vB[s] = base + s * kStage + 32 * kRow + rowpart + wn * 2 + colpart;
+    }
+    const uint32_t sbase = base + wave * 1024;
+    uint32_t m0save;
+    f32x16 acc[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) acc[k] = f32x16{};
+    asm volatile(FX_WGRAD_KLOOP : FX_WGRAD_KLOOP_OUTS : FX_WGRAD_KLOOP_INS : FX_WGRAD_KLOOP_CLOBBERS);
+    (void)m0save;
+
+    // lane holds column n = n0 + wn + 32 j + lane%32 and rows m0 + wm + 32 i + 8 (e/4) + 4 g
+    // + e%4 (acc[4 j + i]); a half-wave stores 32 consecutive columns of a row.  Addresses:
+    // a wave-uniform row base plus a per-lane 32-bit offset (4 g rows + the column), one
+    // accumulator block at a time (the scheduler otherwise reads all 256 accumulators
+    // ahead of the stores and spills)
+    const int g = lane >> 5;
+    auto store = [&](auto* out, int64_t ldo) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t voff = (uint32_t)(4 * g * ldo + wn + 32 * j + (lane & 31));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int64_t row0 = m0 + wm + 32 * i;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    auto* o = out + (row0 + 8 * (e >> 2) + (e & 3)) * ldo + n0;
+                    if constexpr (sizeof(*out) == 4)
+                        o[voff] = acc[4 * j + i][e];
+                    else
+                        o[voff] = f32_to_bf16(acc[4 * j + i][e]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    };
+    if (a.slices > 1)
+        store(a.part + (int64_t)sl * a.M * a.N, (int64_t)a.N);
+    else
+        store(a.C, a.ldc);
 }
 
 // C = bf16(sum over slices of the fp32 partials), slice 0 first; 8 consecutive
@@ -961,7 +1067,13 @@ extern "C" int fx_linear_wgrad(const uint16_t* dY, int64_t ldy, const uint16_t* 
     a.slices = slices;
     const int64_t tiles = ((M + kGBM - 1) / kGBM) * ((N + kGBN - 1) / kGBN);
     hipStream_t s = (hipStream_t)stream;
-    hipLaunchKernelGGL(gemm_wgrad_kernel, dim3((unsigned)(tiles * slices)), dim3(kGThreads), 0, s, a);
+    // whole tiles and 32-token steps, every slice at least 3 steps: the generated loop (with
+    // several slices each spans at least 4 64-token steps, the last perhaps 32 tokens short)
+    const bool fast = M % 256 == 0 && N % 256 == 0 && K % 32 == 0 && K >= 96 && whole_tile_kernels_enabled();
+    if (fast)
+        hipLaunchKernelGGL(gemm_wgrad_fast_kernel, dim3((unsigned)(tiles * slices)), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL(gemm_wgrad_kernel, dim3((unsigned)(tiles * slices)), dim3(kGThreads), 0, s, a);
     if (int e = check_launch("gemm_wgrad")) return e;
     if (slices == 1) return 0;
     int64_t blocks = (M * N / 8 + 255) / 256;

@@ -1,4 +1,5 @@
-"""The generated K loop of the whole-tile GEMM (csrc/gemm_kloop_gen.py -> gemm_kloop.h), on the CPU:
+"""The generated K loops of the whole-tile GEMMs (csrc/gemm_kloop_gen.py -> gemm_kloop.h, forward;
+csrc/gemm_wgrad_gen.py -> gemm_wgrad_kloop.h, weight gradient), on the CPU:
 the committed header is the generator's output, the schedule checker passes it for both tile
 widths and several depths, and the checker fails schedules with a planted mistake of each kind
 it is meant to catch (a wait too weak, a barrier or LDS wait missing, a pointer advanced before
@@ -77,3 +78,88 @@ def test_checker_catches_planted_mistakes(gen, monkeypatch, nj, mistake):
     monkeypatch.setattr(gen, "generate", lambda n: mistake(*good(n)))
     with pytest.raises(AssertionError):
         gen.check(nj, 768)
+
+
+# ---- the weight-gradient loop (csrc/gemm_wgrad_gen.py -> gemm_wgrad_kloop.h) ---------------
+
+@pytest.fixture(scope="module")
+def wgen():
+    path = os.path.join(ROOT, "radeon-igpu-forge_amd", "csrc", "gemm_wgrad_gen.py")
+    spec = importlib.util.spec_from_file_location("gemm_wgrad_gen", path)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_wgrad_header_is_generated(wgen):
+    with open(wgen.OUT) as f:
+        assert f.read() == wgen.header_text()
+
+
+@pytest.mark.parametrize("nsteps", [3, 4, 5, 6, 7, 8, 9, 17, 18, 19, 72, 73, 74, 512])
+def test_wgrad_schedule_checks(wgen, nsteps):
+    phase, iters = wgen.check(nsteps)
+    assert (nsteps - 3 + phase) % 3 == 0 and iters == (nsteps - 3 + phase) // 3
+
+
+def _first(prog, pred, k=0):
+    return [i for i, l in enumerate(prog) if pred(l)][k]
+
+
+def _w_vm_weaker(p):
+    p[_first(p, lambda l: l == "s_waitcnt vmcnt(9)")] = "s_waitcnt vmcnt(10)"
+    return p
+
+
+def _w_drop(line, k):
+    def f(p):
+        del p[_first(p, lambda l: l == line, k)]
+        return p
+    return f
+
+
+def _w_advance_first(p):
+    import re
+    a = _first(p, lambda l: l.startswith("v_lshl_add_u64"))
+    reg = re.search(r"%(\d+)", p[a])[1]
+    p.insert(_first(p, lambda x: x == f"global_load_lds_dwordx4 %{reg}, off"), p.pop(a))
+    return p
+
+
+def _w_read_offset(p):
+    import re
+    i = _first(p, lambda l: l.startswith("ds_read_b64_tr_b16"), 5)
+    p[i] = re.sub(r"offset:(\d+)", lambda m: f"offset:{int(m[1]) + 64}", p[i])
+    return p
+
+
+def _w_entry(p):
+    p[_first(p, lambda l: l == "s_branch .Lu1%=")] = "s_branch .Lu2%="
+    return p
+
+
+def _w_swap_operands(p):
+    import re
+    i = _first(p, lambda l: l.startswith("v_mfma"), 1)
+    m = re.match(r"(v_mfma\S+ %\d+, )(v\[\d+:\d+\]), (v\[\d+:\d+\])(.*)", p[i])
+    p[i] = m[1] + m[3] + ", " + m[2] + m[4]
+    return p
+
+
+def _w_tail_vm(p):
+    p[_first(p, lambda l: l == "s_waitcnt vmcnt(0)")] = "s_waitcnt vmcnt(9)"
+    return p
+
+
+@pytest.mark.parametrize("mistake", [_w_vm_weaker, _w_drop("s_barrier", 2), _w_drop("s_waitcnt lgkmcnt(0)", 3),
+                                     _w_advance_first, _w_read_offset, _w_entry, _w_swap_operands, _w_tail_vm])
+def test_wgrad_checker_catches_planted_mistakes(wgen, monkeypatch, mistake):
+    good = wgen.generate
+    monkeypatch.setattr(wgen, "generate", lambda: mistake(list(good())))
+    caught = 0
+    for n in (3, 4, 5, 72, 73, 74):
+        try:
+            wgen.check(n)
+        except (AssertionError, KeyError, TypeError):
+            caught += 1
+    assert caught > 0

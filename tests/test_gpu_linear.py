@@ -368,3 +368,32 @@ def test_whole_tile_kernel_matches_general_kernel(dev, M, K, N, act, bias, want_
     if act:
         ref = F.gelu(ref, approximate="tanh")
     assert oracle_close(y, ref, FRAC_OUT)
+
+
+# ---- whole-tile weight gradient (M, N % 256 == 0, T % 32 == 0, T >= 96) -------------------
+# Same slices, token ranges and MFMA order as the general split-K kernel, so the two agree bit
+# for bit; FX_GEMM_GENERAL=1 (read on every call) routes the product to the general kernel.
+
+@pytest.mark.parametrize("T,M,N,ld_pad", [
+    (96, 256, 256, 0),       # 3 steps: the loop's tail only, one slice (bf16 written directly)
+    (128, 256, 512, 0),      # 4 steps: enters the loop body at its third step
+    (160, 512, 256, 8),      # 5 steps: enters at the second; rows of dY and X strided
+    (544, 256, 512, 0),      # 2 slices of 8 and 9 steps
+    (4096, 768, 768, 0),     # proj-shaped: 9 tiles x 28 slices
+    (16384, 3072, 768, 0),   # the cfg5 fc weight (7 slices of 36-37 64-token steps)
+])
+def test_wgrad_whole_tile_kernel_matches_general(dev, monkeypatch, T, M, N, ld_pad):
+    from fxgpu.fused_linear import linear_wgrad
+    g = torch.Generator(device=dev).manual_seed(T + M + N)
+    dy = torch.randn(T, M + ld_pad, device=dev, generator=g).bfloat16()[:, :M]
+    x = torch.randn(T, N + ld_pad, device=dev, generator=g).bfloat16()[:, :N]
+    print(f"whole-tile wgrad T={T} M={M} N={N} ldy={dy.stride(0)}", flush=True)
+    dw = linear_wgrad(dy, x)
+    monkeypatch.setenv("FX_GEMM_GENERAL", "1")
+    dw_gen = linear_wgrad(dy, x)
+    monkeypatch.delenv("FX_GEMM_GENERAL")
+    torch.cuda.synchronize()
+    assert torch.equal(dw, dw_gen)
+    ref = dy.double().t() @ x.double()
+    from tolerances import bf16_close
+    assert bf16_close(dw, ref, atol=1e-3 * float(ref.abs().max()), rtol=2.0 ** -8)
