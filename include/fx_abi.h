@@ -350,6 +350,19 @@ int64_t fx_linear_wgrad_workspace(int64_t M, int64_t N, int64_t K);
 int fx_linear_wgrad(const uint16_t* dY, int64_t ldy, const uint16_t* X, int64_t ldx, uint16_t* dW,
                     int64_t ldw, float* work, int64_t M, int64_t N, int64_t K, void* stream);
 
+/* Input gradient dX (M, N) = dY (M, K) W (K, N), W the layer's (out, in) weight with row
+ * stride ldw, dY row stride ldy, dX (and H) row stride ldx; bf16 in and out, fp32
+ * accumulation.  With H non-null (the pre-activation of a GELU(tanh) layer feeding this
+ * one, (M, N)): dX = bf16(bf16(dY W) gelu'(H)), the GELU backward of fx_gelu_bwd folded
+ * into the product's epilogue, bit for bit the unfused pair.  Whole tiles only: M % 256 == 0,
+ * N % 256 == 0 or N % 192 == 0, K % 32 == 0 and K >= 96, row strides multiples of 8,
+ * 16-byte aligned buffers; other shapes return FX_EINVAL before any launch.
+ * Replaces the dense layers' input gradients of the GPT (ml/fxlm/model.py:22-130, torch
+ * autograd of nn.Linear: dY W) and, with H, the F.gelu backward between fc and fc2
+ * (ml/fxlm/model.py:71). */
+int fx_linear_dgrad(const uint16_t* dY, int64_t ldy, const uint16_t* W, int64_t ldw, const uint16_t* H,
+                    uint16_t* dX, int64_t ldx, int64_t M, int64_t N, int64_t K, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -23,8 +23,7 @@
 #include <stdlib.h>
 
 #include "fx_mfma.h"
-#include "gemm_kloop.h"
-#include "gemm_wgrad_kloop.h"
+#include "gemm_asm.h"
 
 namespace fx {
 
@@ -290,35 +289,136 @@ __global__ void __launch_bounds__(kGThreads, 1) gemm_bias_act_kernel(GemmArgs a)
 }
 
 // ---------------------------------------------------------------------------
-// The same product for dense rows on whole tiles (M % 256 == 0, N % (64 NJ) == 0,
-// K % 96 == 0): 4 waves of 128 x (32 NJ), one workgroup per 256 x (64 NJ) tile, the K loop
-// a single generated inline-asm statement (gemm_kloop.h, from gemm_kloop_gen.py, which
-// documents the schedule and checks it on the CPU).  With the accumulators in AGPRs (one
-// wave per SIMD) and the LDS operand reads interleaved with the MFMAs by hand, the loop
-// runs at the MFMA rate the compiler-scheduled kernel above does not reach.  The products
-// are the same MFMAs on the same operands in the same K order as gemm_bias_act_kernel,
-// and the epilogue rounds the same way, so the results are bit-identical.
+// Whole-tile kernels: the forward product above, the input gradient dX = dY W and the
+// weight gradient below, on tiles that divide the output (M % 256 == 0, N % (64 NJ) == 0)
+// and K steps of 32 (K % 32 == 0, K >= 96).  4 waves of 128 x (32 NJ), one workgroup per
+// 256 x (64 NJ) tile, the K loop a single generated inline-asm statement (gemm_asm.h, from
+// gemm_asm_gen.py, which documents the schedule and checks it on the CPU).  With the
+// accumulators in AGPRs (one wave per SIMD) and the LDS operand reads interleaved with the
+// MFMAs by hand, the loop runs at the MFMA rate the compiler-scheduled kernels do not
+// reach.  The products are the same MFMAs on the same operands in the same K order as the
+// general kernels', and the epilogues round the same way, so the results are bit-identical.
 // NJ = 4: 256 x 256 tiles; NJ = 3: 256 x 192 tiles (N = 768 is 4 of them: 256 tiles for
 // M = 16384, one per CU, where 256 x 256 tiles would leave a quarter of the CUs idle).
 __device__ __forceinline__ void raw_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-template <int NJ>
-struct FastGemm {
-    static constexpr int kStage = NJ == 4 ? FX_GEMM_STAGE_BYTES_NJ4 : FX_GEMM_STAGE_BYTES_NJ3;
-    static constexpr int kLoads = NJ == 4 ? FX_GEMM_LOADS_NJ4 : FX_GEMM_LOADS_NJ3;
-    static constexpr int kPW = kLoads - 5;   // W loads per wave and stage (X: 5)
-    static constexpr int kTN = 64 * NJ;      // tile columns
-    static constexpr int kXBytes = 256 * 80; // X rows of a stage: 256 x (32 bf16 + 8 of padding)
-    static constexpr int kLDE = 32 * NJ + 8; // epilogue staging row stride (elements)
-    static constexpr int kWaveLds = 3 * kStage / 4;
-    static_assert(kStage == kXBytes + 4 * kPW * 1024, "stage = X rows + the W load slots");
-    static_assert(32 * kLDE * 2 <= kWaveLds && kWaveLds % 16 == 0, "epilogue staging fits a wave's share");
+// One operand tile of a whole-tile kernel as its loads see it.  base: the tile's element
+// (0, 0) at K step 0.  Row operand (K along the rows, `rows` tile rows): LDS rows of 5 16-byte
+// slots, the 5th (padding) loading the row's 4th chunk again.  Col operand (K down the rows,
+// `cols` tile columns): LDS rows of cols / 8 + 4 slots, the last 4 (padding) loading the row's
+// first chunks again.  step: bytes from one K step of 32 to the next.
+struct TileSrc {
+    const uint16_t* base;
+    int64_t ld;
+    bool col;
+    int cols;
+    uint64_t step;
 };
 
-// EPI: bit 0 GELU, bit 1 pre-activation H out, bit 2 bias (no residual, gather or Xg)
+__device__ __forceinline__ const uint16_t* slot_addr(const TileSrc& t, int s) {
+    if (!t.col) {
+        const int r = s / 5;
+        return t.base + (int64_t)r * t.ld + 8 * min(s - 5 * r, 3);
+    }
+    const int spr = t.cols / 8 + 4;
+    const int r = s / spr;
+    int c = s - spr * r;
+    if (c >= t.cols / 8) c -= t.cols / 8;
+    return t.base + (int64_t)r * t.ld + 8 * c;
+}
+
+// Load pointers, their strides and the prologue: wave-instruction q = wave + 4 t of a stage
+// covers 64 slots of the M-side tile (q < MI), the N-side tile (q < MI + NI) or a pad after
+// them that is never read (loading the N tile's first slot); its LDS slots start at q KiB.
+// Steps 0, 1, 2 go to stages phase + 0, 1, 2 (mod 3); the pointers are left at step 3.
+template <int L, int MI, int NI>
+__device__ __forceinline__ void asm_gemm_prologue(const TileSrc& ms, const TileSrc& ns, int wave, int lane, int phase,
+                                                  uint32_t base, int stage_bytes, uint64_t (&P)[L],
+                                                  uint64_t (&S)[L]) {
+    static_assert(MI + NI <= 4 * L && MI + NI > 4 * (L - 1), "load count");
+#pragma unroll
+    for (int t = 0; t < L; ++t) {
+        const int q = wave + 4 * t;
+        const TileSrc& src = q < MI ? ms : ns;
+        const int s = q < MI ? q * 64 + lane : q < MI + NI ? (q - MI) * 64 + lane : 0;
+        P[t] = (uint64_t)(uintptr_t)slot_addr(src, s);
+        S[t] = src.step;
+    }
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        const int st = (j + phase) % 3;
+#pragma unroll
+        for (int t = 0; t < L; ++t)
+            dma16((const void*)(uintptr_t)(P[t] + j * S[t]), base + st * stage_bytes + (wave + 4 * t) * 1024);
+    }
+#pragma unroll
+    for (int t = 0; t < L; ++t) P[t] += 3 * S[t];
+}
+
+// Per-lane LDS read address of a wave's operand blocks in stage 0 (the stages follow at
+// stage_bytes).  Row side: row w0 + l%32, 16 bytes per l/32.  Col side (row_bytes per K row):
+// the transposed reads' lane pattern, K rows 8 (g'/2) + l%16 / 4 (natural order: the second
+// read 4 rows on) or 4 (g'/2) + l%16 / 4 (lds_op_t's order: 8 rows on), columns
+// w0 + 16 (g' % 2) + 4 (l % 4), g' = l / 16.
+__device__ __forceinline__ uint32_t read_addr(bool col, bool natural, int row_bytes, int w0, int lane) {
+    if (!col) return (w0 + (lane & 31)) * 80 + 16 * (lane >> 5);
+    const int grp = lane >> 4, s16 = lane & 15;
+    const int k = (natural ? 8 : 4) * (grp >> 1) + (s16 >> 2);
+    return k * row_bytes + (w0 + 16 * (grp & 1) + 4 * (s16 & 3)) * 2;
+}
+
+// phase and loop iterations for n K steps (the loop body is 3 steps; the last 3 are its tail)
+__device__ __forceinline__ void asm_gemm_schedule(int nsteps, uint32_t& phase, uint32_t& iters) {
+    phase = __builtin_amdgcn_readfirstlane((3 - nsteps % 3) % 3);
+    iters = __builtin_amdgcn_readfirstlane((nsteps - 3 + (int)phase) / 3);
+}
+
+// C^T-layout epilogue of the forward and input-gradient kernels: acc[4 j + i] holds rows
+// m0 + wm + 32 i + l%32, columns n0 + wn + 32 j + 8 q + 4 g + 0..3 (g = l/32).  Each 32-row
+// block leaves through the wave's LDS share `stg` (free once every wave is done with the
+// stages): 8-byte writes from the MFMA layout, read back and stored as 16-byte row chunks,
+// 32 NJ columns contiguous.  value(i, j, q, a, v) turns the 4 accumulators a into the
+// 4 outputs v.
+constexpr int kStgExtra = 8;  // staging row padding (elements)
+template <int NJ, class Value>
+__device__ __forceinline__ void ct_store_block(uint16_t* stg, int lane, int i, uint16_t* out, int64_t ld, int64_t row0,
+                                               int col0, const f32x16 (&acc)[4 * NJ], Value&& value) {
+    constexpr int LDE = 32 * NJ + kStgExtra;
+    const int g = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float a[4] = {acc[4 * j + i][4 * q], acc[4 * j + i][4 * q + 1], acc[4 * j + i][4 * q + 2],
+                                acc[4 * j + i][4 * q + 3]};
+            float v[4];
+            value(j, q, a, v);
+            *reinterpret_cast<uint2*>(stg + (lane & 31) * LDE + 32 * j + 8 * q + 4 * g) =
+                make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+        }
+#pragma unroll
+    for (int k = 0; k < 2 * NJ; ++k) {
+        const int idx = lane + 64 * k;
+        const int r = idx / (4 * NJ), c = idx - r * (4 * NJ);
+        st16(out + (row0 + r) * ld + col0 + 8 * c, *reinterpret_cast<const uint4*>(stg + r * LDE + 8 * c));
+    }
+}
+
+template <int NJ>
+struct FastGemm {
+    static constexpr int kStage = NJ == 4 ? FX_FWD_NJ4_STAGE : FX_FWD_NJ3_STAGE;
+    static constexpr int kLoads = NJ == 4 ? FX_FWD_NJ4_LOADS : FX_FWD_NJ3_LOADS;
+    static constexpr int kTN = 64 * NJ;
+    static constexpr int kWaveLds = 3 * kStage / 4;
+    static_assert(32 * (32 * NJ + kStgExtra) * 2 <= kWaveLds && kWaveLds % 16 == 0, "staging fits a wave's share");
+};
+
+// Forward: C = act(X W^T + bias), with the pre-activation H.  EPI: bit 0 GELU, bit 1 H out,
+// bit 2 bias (no residual, gather or Xg)
 template <int NJ, int EPI>
 __global__ void __launch_bounds__(256, 1) gemm_fast_kernel(GemmArgs a) {
     using G = FastGemm<NJ>;
+    constexpr int L = G::kLoads;
     constexpr bool kGelu = EPI & 1, kH = EPI & 2, kBias = EPI & 4;
     __shared__ __attribute__((aligned(16))) unsigned char lds[3 * G::kStage];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -329,61 +429,35 @@ __global__ void __launch_bounds__(256, 1) gemm_fast_kernel(GemmArgs a) {
     gemm_tile(blockIdx.x, a.M / 256, a.N / G::kTN, m0, n0, nt);
     n0 = nt * G::kTN;
     const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(lds));
-    // load slots: wave-instruction q = wave + 4 t covers 64 16-byte slots, 5 to a row (the
-    // 5th, padding, loads the row's last chunk again); W slots past the tile's rows (the
-    // 16th instruction of NJ = 3) load its last row into the never-read pad
-    const uint16_t* pa[5];
-    const uint16_t* pb[G::kPW];
-#pragma unroll
-    for (int t = 0; t < 5; ++t) {
-        const int s = (wave + 4 * t) * 64 + lane;
-        const int r = s / 5, c = min(s - 5 * r, 3);
-        pa[t] = a.A + (int64_t)(m0 + r) * a.lda + 8 * c;
-    }
-#pragma unroll
-    for (int t = 0; t < G::kPW; ++t) {
-        const int s = (wave + 4 * t) * 64 + lane;
-        const int r = s / 5, c = min(s - 5 * r, 3);
-        pb[t] = a.B + (int64_t)(n0 + min(r, G::kTN - 1)) * a.ldb + 8 * c;
-    }
-#pragma unroll
-    for (int st = 0; st < 3; ++st) {  // K steps 0, 1, 2 into stages 0, 1, 2
-#pragma unroll
-        for (int t = 0; t < 5; ++t) dma16(pa[t] + 32 * st, base + st * G::kStage + (wave + 4 * t) * 1024);
-#pragma unroll
-        for (int t = 0; t < G::kPW; ++t)
-            dma16(pb[t] + 32 * st, base + st * G::kStage + G::kXBytes + (wave + 4 * t) * 1024);
-    }
-    const uint16_t* qa[5];
-    const uint16_t* qb[G::kPW];
-#pragma unroll
-    for (int t = 0; t < 5; ++t) qa[t] = pa[t] + 96;
-#pragma unroll
-    for (int t = 0; t < G::kPW; ++t) qb[t] = pb[t] + 96;
-    uint32_t vA[3], vB[3];
+    uint32_t phase, iters;
+    asm_gemm_schedule(a.K / 32, phase, iters);
+    const TileSrc ms{a.A + (int64_t)m0 * a.lda, a.lda, false, 0, 64};
+    const TileSrc ns{a.B + (int64_t)n0 * a.ldb, a.ldb, false, 0, 64};
+    uint64_t P[L], S[L];
+    if constexpr (NJ == 4)
+        asm_gemm_prologue<L, FX_FWD_NJ4_M_INS, FX_FWD_NJ4_N_INS>(ms, ns, wave, lane, phase, base, G::kStage, P, S);
+    else
+        asm_gemm_prologue<L, FX_FWD_NJ3_M_INS, FX_FWD_NJ3_N_INS>(ms, ns, wave, lane, phase, base, G::kStage, P, S);
+    constexpr int kNOff = NJ == 4 ? FX_FWD_NJ4_N_OFF : FX_FWD_NJ3_N_OFF;
+    uint32_t vM[3], vN[3];
 #pragma unroll
     for (int s = 0; s < 3; ++s) {
-        vA[s] = base + s * G::kStage + (wm + (lane & 31)) * 80 + 16 * g;
-        vB[s] = base + s * G::kStage + G::kXBytes + (wn + (lane & 31)) * 80 + 16 * g;
+        vM[s] = base + s * G::kStage + read_addr(false, true, 0, wm, lane);
+        vN[s] = base + s * G::kStage + kNOff + read_addr(false, true, 0, wn, lane);
     }
     const uint32_t sbase = base + wave * 1024;
-    uint32_t iters = (uint32_t)(a.K / 32 - 3) / 3;  // 3-step iterations before the 3-step tail
     uint32_t m0save;
     f32x16 acc[4 * NJ];
 #pragma unroll
     for (int k = 0; k < 4 * NJ; ++k) acc[k] = f32x16{};
-    bf16x8 F[3][4 + NJ];
     if constexpr (NJ == 4)
-        asm volatile(FX_GEMM_KLOOP_NJ4 : FX_GEMM_KLOOP_OUTS_NJ4 : FX_GEMM_KLOOP_INS_NJ4 : "memory");
+        asm volatile(FX_FWD_NJ4_KLOOP : FX_FWD_NJ4_OUTS : FX_FWD_NJ4_INS : FX_FWD_NJ4_CLOBBERS);
     else
-        asm volatile(FX_GEMM_KLOOP_NJ3 : FX_GEMM_KLOOP_OUTS_NJ3 : FX_GEMM_KLOOP_INS_NJ3 : "memory");
-    (void)F;
+        asm volatile(FX_FWD_NJ3_KLOOP : FX_FWD_NJ3_OUTS : FX_FWD_NJ3_INS : FX_FWD_NJ3_CLOBBERS);
     (void)m0save;
 
-    // epilogue.  acc[4 j + i] holds C^T as in gemm_bias_act_kernel: lane l has row
-    // m0 + wm + 32 i + l%32 and the columns n0 + wn + 32 j + 8 q + 4 g + 0..3.  Each 32-row
-    // block leaves through the wave's share of the (now free) stages: 8-byte writes from the
-    // MFMA layout, read back and stored as 16-byte row chunks, 32 NJ columns contiguous.
+    // epilogue: h = acc + bias (H, when wanted), then C = act(h), rounded as
+    // gemm_bias_act_kernel rounds them
     raw_barrier();  // every wave is done reading the stages (the loop ends with no load in flight)
     uint16_t* stg = reinterpret_cast<uint16_t*>(lds + wave * G::kWaveLds);
     float bias[NJ][4][4];
@@ -396,34 +470,110 @@ __global__ void __launch_bounds__(256, 1) gemm_fast_kernel(GemmArgs a) {
                 bias[j][q][e] = kBias ? bf16_to_f32(a.bias[n0 + wn + 32 * j + 8 * q + 4 * g + e]) : 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int mb = m0 + wm + 32 * i;
+        const int64_t row0 = m0 + wm + 32 * i;
+        if constexpr (kH)
+            ct_store_block<NJ>(stg, lane, i, a.H, a.ldh, row0, n0 + wn, acc,
+                               [&](int j, int q, const float (&v)[4], float (&o)[4]) {
 #pragma unroll
-        for (int pass = kH ? 0 : 1; pass < 2; ++pass) {
+                                   for (int e = 0; e < 4; ++e) o[e] = kBias ? v[e] + bias[j][q][e] : v[e];
+                               });
+        ct_store_block<NJ>(stg, lane, i, a.C, a.ldc, row0, n0 + wn, acc,
+                           [&](int j, int q, const float (&v)[4], float (&o)[4]) {
 #pragma unroll
-            for (int j = 0; j < NJ; ++j)
+                               for (int e = 0; e < 4; ++e) {
+                                   float h = kBias ? v[e] + bias[j][q][e] : v[e];
+                                   o[e] = kGelu ? gelu_tanh(h) : h;
+                               }
+                           });
+    }
+}
+
+// Input gradient dX (M x N) = dY (M x K) W (K x N), W row-major with K down its rows (the
+// layer's weight, N its input features); EPI 1: dX = (dY W) gelu'(H), H (M x N) the
+// pre-activation at dX's layout: the GELU backward of the layer below, which the unfused
+// path computes as bf16(bf16(dY W) gelu'(H)), rounded the same way here.
+struct DgradArgs {
+    const uint16_t* dY;
+    int64_t ldy;
+    const uint16_t* W;
+    int64_t ldw;
+    const uint16_t* H;
+    uint16_t* dX;
+    int64_t ldx;
+    int M, N, K;
+};
+
+template <int NJ>
+struct DgradGemm {
+    static constexpr int kStage = NJ == 4 ? FX_DGRAD_NJ4_STAGE : FX_DGRAD_NJ3_STAGE;
+    static constexpr int kLoads = NJ == 4 ? FX_DGRAD_NJ4_LOADS : FX_DGRAD_NJ3_LOADS;
+    static constexpr int kNOff = NJ == 4 ? FX_DGRAD_NJ4_N_OFF : FX_DGRAD_NJ3_N_OFF;
+    static constexpr int kRow = (64 * NJ + 32) * 2;  // LDS bytes per K row of the W tile
+    static constexpr int kTN = 64 * NJ;
+    static constexpr int kWaveLds = 3 * kStage / 4;
+    static_assert(32 * (32 * NJ + kStgExtra) * 2 <= kWaveLds && kWaveLds % 16 == 0, "staging fits a wave's share");
+};
+
+template <int NJ, int EPI>
+__global__ void __launch_bounds__(256, 1) gemm_dgrad_fast_kernel(DgradArgs a) {
+    using G = DgradGemm<NJ>;
+    constexpr int L = G::kLoads;
+    __shared__ __attribute__((aligned(16))) unsigned char lds[3 * G::kStage];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 5;
+    const int wm = (wave >> 1) * 128, wn = (wave & 1) * 32 * NJ;
+    int m0, n0, nt;
+    gemm_tile(blockIdx.x, a.M / 256, a.N / G::kTN, m0, n0, nt);
+    n0 = nt * G::kTN;
+    const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(lds));
+    uint32_t phase, iters;
+    asm_gemm_schedule(a.K / 32, phase, iters);
+    const TileSrc ms{a.dY + (int64_t)m0 * a.ldy, a.ldy, false, 0, 64};
+    const TileSrc ns{a.W + n0, a.ldw, true, G::kTN, (uint64_t)a.ldw * 64};
+    uint64_t P[L], S[L];
+    if constexpr (NJ == 4)
+        asm_gemm_prologue<L, FX_DGRAD_NJ4_M_INS, FX_DGRAD_NJ4_N_INS>(ms, ns, wave, lane, phase, base, G::kStage, P, S);
+    else
+        asm_gemm_prologue<L, FX_DGRAD_NJ3_M_INS, FX_DGRAD_NJ3_N_INS>(ms, ns, wave, lane, phase, base, G::kStage, P, S);
+    uint32_t vM[3], vN[3];
 #pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    float v[4];
+    for (int s = 0; s < 3; ++s) {
+        vM[s] = base + s * G::kStage + read_addr(false, true, 0, wm, lane);
+        vN[s] = base + s * G::kStage + G::kNOff + read_addr(true, true, G::kRow, wn, lane);
+    }
+    const uint32_t sbase = base + wave * 1024;
+    uint32_t m0save;
+    f32x16 acc[4 * NJ];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        float h = acc[4 * j + i][4 * q + e];
-                        if (kBias) h += bias[j][q][e];
-                        if (pass == 1 && kGelu) h = gelu_tanh(h);
-                        v[e] = h;
-                    }
-                    *reinterpret_cast<uint2*>(stg + (lane & 31) * G::kLDE + 32 * j + 8 * q + 4 * g) =
-                        make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
-                }
-            uint16_t* out = pass == 0 ? a.H : a.C;
-            const int64_t ld = pass == 0 ? a.ldh : a.ldc;
+    for (int k = 0; k < 4 * NJ; ++k) acc[k] = f32x16{};
+    if constexpr (NJ == 4)
+        asm volatile(FX_DGRAD_NJ4_KLOOP : FX_DGRAD_NJ4_OUTS : FX_DGRAD_NJ4_INS : FX_DGRAD_NJ4_CLOBBERS);
+    else
+        asm volatile(FX_DGRAD_NJ3_KLOOP : FX_DGRAD_NJ3_OUTS : FX_DGRAD_NJ3_INS : FX_DGRAD_NJ3_CLOBBERS);
+    (void)m0save;
+
+    raw_barrier();
+    uint16_t* stg = reinterpret_cast<uint16_t*>(lds + wave * G::kWaveLds);
 #pragma unroll
-            for (int k = 0; k < 2 * NJ; ++k) {
-                const int idx = lane + 64 * k;
-                const int r = idx / (4 * NJ), c = idx - r * (4 * NJ);
-                st16(out + (int64_t)(mb + r) * ld + n0 + wn + 8 * c,
-                     *reinterpret_cast<const uint4*>(stg + r * G::kLDE + 8 * c));
-            }
-        }
+    for (int i = 0; i < 4; ++i) {
+        const int64_t row0 = m0 + wm + 32 * i;
+        const int m = (int)row0 + (lane & 31);
+        ct_store_block<NJ>(stg, lane, i, a.dX, a.ldx, row0, n0 + wn, acc,
+                           [&](int j, int q, const float (&v)[4], float (&o)[4]) {
+                               if constexpr (EPI == 1) {
+                                   const uint2 hh = *reinterpret_cast<const uint2*>(
+                                       a.H + (int64_t)m * a.ldx + n0 + wn + 32 * j + 8 * q + 4 * g);
+                                   const float h[4] = {bf16_to_f32((uint16_t)hh.x), bf16_to_f32((uint16_t)(hh.x >> 16)),
+                                                       bf16_to_f32((uint16_t)hh.y), bf16_to_f32((uint16_t)(hh.y >> 16))};
+#pragma unroll
+                                   for (int e = 0; e < 4; ++e)
+                                       o[e] = bf16_to_f32(f32_to_bf16(v[e])) * gelu_tanh_grad(h[e]);
+                               } else {
+#pragma unroll
+                                   for (int e = 0; e < 4; ++e) o[e] = v[e];
+                               }
+                           });
     }
 }
 
@@ -439,7 +589,7 @@ static bool whole_tile_kernels_enabled() {
 // of the tile widths that divide N, the one with the fewest MFMA rounds per CU
 static int fast_gemm_nj(const GemmArgs& a) {
     if (a.idx || a.res || a.nw || a.Xg || !whole_tile_kernels_enabled()) return 0;
-    if (a.M % 256 || a.K % 96 || a.ldb != a.K || a.lda % 8 || !a.vec_c || (a.H && !a.vec_h)) return 0;
+    if (a.M % 256 || a.K % 32 || a.K < 96 || a.lda % 8 || a.ldb % 8 || !a.vec_c || (a.H && !a.vec_h)) return 0;
     const int64_t cus = device_cus();
     int64_t best = 0, nj = 0;
     for (int w : {4, 3}) {
@@ -582,15 +732,15 @@ __global__ void __launch_bounds__(kGThreads, 1) gemm_wgrad_kernel(WgradArgs a) {
     }
 }
 
-// The same product on whole tiles (M % 256 == 0, N % 256 == 0, K % 32 == 0) with the K loop
-// generated by gemm_wgrad_gen.py (gemm_wgrad_kloop.h; the generator documents the schedule
-// and checks it on the CPU): 4 waves of 128 x 128, accumulators in AGPRs, 32-token steps in
-// 3 LDS stages loaded two steps ahead.  The slices, their token ranges, the transposed
-// operand reads (lds_op_t's K permutation) and the MFMA order over K are those of
-// gemm_wgrad_kernel, so its partial tiles, and the reduced result, are bit-identical.
+// The same product on whole tiles (M % 256 == 0, N % 256 == 0, K % 32 == 0) with the
+// generated K loop (gemm_asm.h's WGRAD): 4 waves of 128 x 128, accumulators in AGPRs,
+// 32-token steps in 3 LDS stages loaded two steps ahead.  The slices, their token ranges,
+// the transposed operand reads (lds_op_t's K permutation) and the MFMA order over K are
+// those of gemm_wgrad_kernel, so its partial tiles, and the reduced result, are
+// bit-identical.
 __global__ void __launch_bounds__(256, 1) gemm_wgrad_fast_kernel(WgradArgs a) {
-    constexpr int kStage = FX_WGRAD_STAGE_BYTES, kRow = FX_WGRAD_ROW_BYTES;
-    static_assert(kStage == 2 * 32 * kRow && kRow == 2 * (256 + 32) && FX_WGRAD_LOADS == 9, "stage layout");
+    constexpr int kStage = FX_WGRAD_STAGE, L = FX_WGRAD_LOADS, kRow = (256 + 32) * 2;
+    static_assert(FX_WGRAD_N_OFF == 32 * kRow, "stage layout");
     __shared__ __attribute__((aligned(16))) unsigned char lds[3 * kStage];
     const int nn = a.N / 256;
     const int ntiles = (a.M / 256) * nn;
@@ -603,48 +753,24 @@ __global__ void __launch_bounds__(256, 1) gemm_wgrad_fast_kernel(WgradArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = (wave >> 1) * 128, wn = (wave & 1) * 128;
     const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(lds));
-    // load slots: wave-instruction q = wave + 4 t (t = 0..8) covers 64 of the 2 x 1152 16-byte
-    // slots of a stage (A rows, then B rows; 36 slots a row, the last 4 padding that loads
-    // the row's first chunks again)
-    const uint16_t* P[9];
-    int64_t ld[9];
-#pragma unroll
-    for (int u = 0; u < 9; ++u) {
-        const int q = wave + 4 * u;
-        const bool isa = q < 18;
-        const int s = (isa ? q : q - 18) * 64 + lane;
-        const int r = s / 36;
-        int c = s - 36 * r;
-        if (c >= 32) c -= 32;
-        ld[u] = isa ? a.lda : a.ldb;
-        P[u] = (isa ? a.A + m0 : a.B + n0) + (int64_t)(t0 + r) * ld[u] + 8 * c;
-    }
-    const uint32_t phase = __builtin_amdgcn_readfirstlane((3 - nsteps % 3) % 3);
-    uint32_t iters = __builtin_amdgcn_readfirstlane((nsteps - 3 + (int)phase) / 3);
-#pragma unroll
-    for (int j = 0; j < 3; ++j) {  // steps 0, 1, 2 into stages phase + j (mod 3)
-        const int st = (j + (int)phase) % 3;
-#pragma unroll
-        for (int u = 0; u < 9; ++u) dma16(P[u] + (int64_t)32 * j * ld[u], base + st * kStage + (wave + 4 * u) * 1024);
-    }
-#pragma unroll
-    for (int u = 0; u < 9; ++u) P[u] += (int64_t)96 * ld[u];
-    const uint64_t stride_a = (uint64_t)a.lda * 64, stride_b = (uint64_t)a.ldb * 64;  // 32 rows, bytes
-    const uint64_t stride_4 = wave < 2 ? stride_a : stride_b;
-    const int grp = lane >> 4, s16 = lane & 15;
-    const uint32_t rowpart = (4 * (grp >> 1) + (s16 >> 2)) * kRow, colpart = (16 * (grp & 1) + 4 * (s16 & 3)) * 2;
-    uint32_t vA[3], vB[3];
+    uint32_t phase, iters;
+    asm_gemm_schedule(nsteps, phase, iters);
+    const TileSrc ms{a.A + (int64_t)t0 * a.lda + m0, a.lda, true, 256, (uint64_t)a.lda * 64};
+    const TileSrc ns{a.B + (int64_t)t0 * a.ldb + n0, a.ldb, true, 256, (uint64_t)a.ldb * 64};
+    uint64_t P[L], S[L];
+    asm_gemm_prologue<L, FX_WGRAD_M_INS, FX_WGRAD_N_INS>(ms, ns, wave, lane, phase, base, kStage, P, S);
+    uint32_t vM[3], vN[3];
 #pragma unroll
     for (int s = 0; s < 3; ++s) {
-        vA[s] = base + s * kStage + rowpart + wm * 2 + colpart;
-        vB[s] = base + s * kStage + 32 * kRow + rowpart + wn * 2 + colpart;
+        vM[s] = base + s * kStage + read_addr(true, false, kRow, wm, lane);
+        vN[s] = base + s * kStage + FX_WGRAD_N_OFF + read_addr(true, false, kRow, wn, lane);
     }
     const uint32_t sbase = base + wave * 1024;
     uint32_t m0save;
     f32x16 acc[16];
 #pragma unroll
     for (int k = 0; k < 16; ++k) acc[k] = f32x16{};
-    asm volatile(FX_WGRAD_KLOOP : FX_WGRAD_KLOOP_OUTS : FX_WGRAD_KLOOP_INS : FX_WGRAD_KLOOP_CLOBBERS);
+    asm volatile(FX_WGRAD_KLOOP : FX_WGRAD_OUTS : FX_WGRAD_INS : FX_WGRAD_CLOBBERS);
     (void)m0save;
 
     // lane holds column n = n0 + wn + 32 j + lane%32 and rows m0 + wm + 32 i + 8 (e/4) + 4 g
@@ -1081,6 +1207,48 @@ extern "C" int fx_linear_wgrad(const uint16_t* dY, int64_t ldy, const uint16_t* 
     hipLaunchKernelGGL(wgrad_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, s, (const float*)work, slices,
                        M * N, (int)N, dW, ldw);
     return check_launch("wgrad_reduce");
+}
+
+// the tile width (in 64-column units) of gemm_dgrad_fast_kernel for N columns: of the widths
+// that divide N, the one with the fewest MFMA rounds per CU; 0 if none divides it
+static int dgrad_nj(int64_t M, int64_t N) {
+    const int64_t cus = device_cus();
+    int64_t best = 0, nj = 0;
+    for (int w : {4, 3}) {
+        if (N % (64 * w)) continue;
+        const int64_t cost = ((M / 256) * (N / (64 * w)) + cus - 1) / cus * w;
+        if (nj == 0 || cost < best) best = cost, nj = w;
+    }
+    return (int)nj;
+}
+
+extern "C" int fx_linear_dgrad(const uint16_t* dY, int64_t ldy, const uint16_t* W, int64_t ldw, const uint16_t* H,
+                               uint16_t* dX, int64_t ldx, int64_t M, int64_t N, int64_t K, void* stream) {
+    FX_REQUIRE(dY && W && dX, "fx_linear_dgrad: null pointer");
+    FX_REQUIRE(M >= 0 && N >= 1 && K >= 1, "fx_linear_dgrad: bad shape M=%lld N=%lld K=%lld", (long long)M,
+               (long long)N, (long long)K);
+    FX_REQUIRE(M < 0x7fffffffLL && N < 0x7fffffffLL && K < 0x7fffffffLL, "fx_linear_dgrad: size too large");
+    const int nj = dgrad_nj(M, N);
+    FX_REQUIRE(M % 256 == 0 && nj != 0 && K % 32 == 0 && K >= 96,
+               "fx_linear_dgrad: whole tiles only (M %% 256, N %% 256 or %% 192, K %% 32 == 0, K >= 96): "
+               "M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
+    FX_REQUIRE(ldy >= K && ldw >= N && ldx >= N && ldy % 8 == 0 && ldw % 8 == 0 && ldx % 8 == 0,
+               "fx_linear_dgrad: bad leading dimension (ldy=%lld ldw=%lld ldx=%lld)", (long long)ldy, (long long)ldw,
+               (long long)ldx);
+    FX_REQUIRE(((((uintptr_t)dY) | ((uintptr_t)W) | ((uintptr_t)H) | ((uintptr_t)dX)) & 15) == 0,
+               "fx_linear_dgrad: dY, W, H and dX must be 16-byte aligned");
+    if (M == 0) return 0;
+    DgradArgs a{dY, ldy, W, ldw, H, dX, ldx, (int)M, (int)N, (int)K};
+    const unsigned tiles = (unsigned)((M / 256) * (N / (64 * nj)));
+    hipStream_t s = (hipStream_t)stream;
+    if (nj == 4) {
+        if (H) hipLaunchKernelGGL((gemm_dgrad_fast_kernel<4, 1>), dim3(tiles), dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((gemm_dgrad_fast_kernel<4, 0>), dim3(tiles), dim3(256), 0, s, a);
+    } else {
+        if (H) hipLaunchKernelGGL((gemm_dgrad_fast_kernel<3, 1>), dim3(tiles), dim3(256), 0, s, a);
+        else hipLaunchKernelGGL((gemm_dgrad_fast_kernel<3, 0>), dim3(tiles), dim3(256), 0, s, a);
+    }
+    return check_launch("gemm_dgrad");
 }
 
 extern "C" int fx_gelu_bwd(const uint16_t* dy, const uint16_t* h, uint16_t* dh, int64_t n, void* stream) {

@@ -348,6 +348,8 @@ def _linear_fwd(x, W, b, act, want_h):
     (768, 768, 2304, 0, True, False, 0),   # qkv widths
     (256, 3072, 768, 1, False, True, 0),   # fc2 depth
     (16384, 768, 3072, 1, False, True, 0), # the cfg5 MLP fc (256-wide tiles): GELU and the pre-activation
+    (512, 128, 256, 1, True, True, 0),     # 4 K steps: enters the loop body at its third step
+    (512, 160, 192, 0, False, False, 8),   # 5 K steps: enters at the second
 ])
 def test_whole_tile_kernel_matches_general_kernel(dev, M, K, N, act, bias, want_h, pad_k):
     g = torch.Generator(device=dev).manual_seed(M + K + N)
@@ -397,3 +399,50 @@ def test_wgrad_whole_tile_kernel_matches_general(dev, monkeypatch, T, M, N, ld_p
     ref = dy.double().t() @ x.double()
     from tolerances import bf16_close
     assert bf16_close(dw, ref, atol=1e-3 * float(ref.abs().max()), rtol=2.0 ** -8)
+
+
+# ---- whole-tile input gradient dX = dY W (fx_linear_dgrad), optionally with the GELU backward -----
+# Against the fp32 product (tolerance as for the forward), and with H against the unfused pair
+# (fx_linear_dgrad, then fx_gelu_bwd) bit for bit.
+
+def _dgrad(dy, W, h=None):
+    from fxgpu.abi import call, ptr, stream_of
+    M, K = dy.shape
+    N = W.shape[1]
+    dx = torch.empty(M, N, device=dy.device, dtype=torch.bfloat16)
+    call("fx_linear_dgrad", ptr(dy), dy.stride(0), ptr(W), W.stride(0), ptr(h), ptr(dx), N, M, N, K, stream_of(dy))
+    return dx
+
+
+@pytest.mark.parametrize("M,N,K,pad", [
+    (256, 256, 96, 0),       # 256-wide tiles, the loop's tail only
+    (512, 192, 128, 0),      # 192-wide tiles, 4 K steps (entry at the body's third step)
+    (256, 768, 160, 8),      # 5 K steps; rows of dY strided
+    (1024, 3072, 768, 0),    # fc2's input gradient shape (192-wide tiles at this M)
+    (16384, 3072, 768, 0),   # cfg5 fc2 (256-wide tiles, 768 tiles)
+    (16384, 768, 2304, 0),   # cfg5 qkv
+])
+def test_dgrad_whole_tile_kernel(dev, M, N, K, pad):
+    from fxgpu.abi import call, ptr, stream_of
+    g = torch.Generator(device=dev).manual_seed(M + N + K)
+    dy = torch.randn(M, K + pad, device=dev, generator=g).bfloat16()[:, :K]
+    W = (torch.randn(K, N, device=dev, generator=g) * K ** -0.5).bfloat16()
+    h = torch.randn(M, N, device=dev, generator=g).bfloat16()
+    print(f"whole-tile dgrad M={M} N={N} K={K} ldy={dy.stride(0)}", flush=True)
+    dx = _dgrad(dy, W)
+    dh = _dgrad(dy, W, h)
+    dh_pair = torch.empty_like(dx)
+    call("fx_gelu_bwd", ptr(dx), ptr(h), ptr(dh_pair), dx.numel(), stream_of(dx))
+    torch.cuda.synchronize()
+    assert torch.equal(dh, dh_pair)
+    ref = dy.float() @ W.float()
+    assert oracle_close(dx, ref, FRAC_OUT)
+
+
+def test_dgrad_rejects_partial_tiles(dev):
+    from fxgpu.abi import call, ptr, stream_of
+    dy = torch.zeros(300, 96, device=dev, dtype=torch.bfloat16)
+    W = torch.zeros(96, 256, device=dev, dtype=torch.bfloat16)
+    dx = torch.empty(300, 256, device=dev, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="whole tiles"):
+        call("fx_linear_dgrad", ptr(dy), 96, ptr(W), 256, None, ptr(dx), 256, 300, 256, 96, stream_of(dy))
