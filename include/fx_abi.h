@@ -355,7 +355,7 @@ int fx_linear_wgrad(const uint16_t* dY, int64_t ldy, const uint16_t* X, int64_t 
  * accumulation.  With H non-null (the pre-activation of a GELU(tanh) layer feeding this
  * one, (M, N)): dX = bf16(bf16(dY W) gelu'(H)), the GELU backward of fx_gelu_bwd folded
  * into the product's epilogue, bit for bit the unfused pair.  Whole tiles only: M % 256 == 0,
- * N % 256 == 0 or N % 192 == 0, K % 32 == 0 and K >= 96, row strides multiples of 8,
+ * N % 256 == 0 or N % 192 == 0, K % 32 == 0 and K >= 128, row strides multiples of 8,
  * 16-byte aligned buffers; other shapes return FX_EINVAL before any launch.
  * Replaces the dense layers' input gradients of the GPT (ml/fxlm/model.py:22-130, torch
  * autograd of nn.Linear: dY W) and, with H, the F.gelu backward between fc and fc2

@@ -11,7 +11,7 @@ accumulators stay in AGPRs for the whole K loop (one inline-asm statement):
   dgrad  C = dY W       dY (M x K) a row operand, W (K x N) with K down its rows ("col")
   wgrad  C = dY^T X     dY (K x M), X (K x N): both col operands (K = tokens)
 
-K advances in steps of 32 held in 3 LDS stages.  A stage holds the M-side operand's tile,
+K advances in steps of 32 held in 4 LDS stages.  A stage holds the M-side operand's tile,
 then the N-side's:
   row operand: one LDS row per tile row, 80 bytes (32 bf16 + 16 of padding: the 32 rows
     of a read fall in distinct banks); an operand block is one `ds_read_b128`, lane l taking
@@ -30,17 +30,19 @@ Per step: the first half runs 4 NJ MFMAs on chunk 0 while the reads of chunk 1 f
 first MFMAs; `s_waitcnt vmcnt` for the next stage's loads, `lgkmcnt(0)` and `s_barrier`
 (every wave is then done reading this stage); the second half runs chunk 1's MFMAs with the
 reads of the next step's chunk 0 and, after its last 8 MFMAs, this stage's loads of step
-j + 3 (`global_load_lds_dwordx4`, L per wave; instruction q = wave + 4 t of a stage covers 64
+j + 4 (`global_load_lds_dwordx4`, L per wave; instruction q = wave + 4 t of a stage covers 64
 16-byte slots, the M-side's, then the N-side's, then a never-read pad that rounds the count
 to a multiple of 4), each pointer then advanced by its stride (one SGPR pair per t: the
-region of instruction q may differ between waves).  Loads run two steps ahead: at the
-barrier of step j only the loads of step j + 2 may be outstanding (`vmcnt(L)`), none in the
-last two steps.
+region of instruction q may differ between waves).  Loads run three steps ahead (the data
+of a step is requested about three steps of MFMA time before it is read, enough for loads
+that miss the caches): at the barrier of step j only the loads of steps j + 2 and j + 3 may
+be outstanding (`vmcnt(2 L)`), fewer in the last three steps.  The operands rotate through
+4 register sets (one per half step, refilled three halves after the MFMAs that read it).
 
-Any number of steps >= 3: the loop body is 3 steps (stages and operand sets both rotate
-with period 3) and the last 3 steps are a tail without loads, so a product of n steps enters
-the body at step p = (3 - n % 3) % 3 (`phase`), its prologue having loaded steps 0..2 into
-stages p, p + 1, p + 2 (mod 3).
+Any number of steps >= 4: the loop body is 4 steps (stages rotate with period 4, operand sets
+with period 2) and the last 4 steps are a tail without loads, so a product of n steps enters
+the body at step p = (4 - n % 4) % 4 (`phase`), its prologue having loaded steps 0..3 into
+stages p, p + 1, p + 2, p + 3 (mod 4).
 
 Operands of each loop (FX_<KIND>_OUTS / _INS / _CLOBBERS): acc[4 j + i] ("+a"; i: M-side
 block, j: N-side block), the L load pointers P[t] ("+v", 64-bit), the loop iterations
@@ -53,6 +55,8 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 OUT = os.path.join(HERE, "gemm_asm.h")
+STAGES = 4          # LDS stages
+SETS = 4            # operand register sets
 
 
 class Kind:
@@ -61,7 +65,7 @@ class Kind:
     def __init__(self, name, m_mode, n_mode, nj, order):
         self.name, self.m_mode, self.n_mode, self.nj, self.order = name, m_mode, n_mode, nj, order
         self.set_size = 4 + nj                        # operand blocks per set
-        self.fb = 256 - 12 * self.set_size            # first VGPR of the operand sets
+        self.fb = 256 - 4 * SETS * self.set_size      # first VGPR of the operand sets
         self.n_acc = 4 * nj
         self.region = []                              # (mode, bytes, wave-instructions) per side
         for mode, rows in ((m_mode, 256), (n_mode, 64 * nj)):
@@ -83,8 +87,8 @@ class Kind:
         self.iters = self.ptr0 + self.loads
         self.m0s = self.iters + 1
         self.vm0 = self.m0s + 1
-        self.vn0 = self.vm0 + 3
-        self.sbase = self.vn0 + 3
+        self.vn0 = self.vm0 + STAGES
+        self.sbase = self.vn0 + STAGES
         self.phase = self.sbase + 1
         self.stride0 = self.phase + 1
 
@@ -99,11 +103,8 @@ class Kind:
         return 1 if q < self.region[0][2] + self.region[1][2] else 2
 
     def hi_off(self, side):
+        """offset of a col block's second transposed read (4 K rows on, or 8 in lds_op_t's order)"""
         return (8 if self.order == "lds_op_t" else 4) * self.col_row[side]
-
-    def lo_k(self, side):
-        """K rows of a col block's two reads relative to 16 ch: first read base"""
-        return 0
 
 
 KINDS = [Kind("FWD_NJ4", "row", "row", 4, "natural"), Kind("FWD_NJ3", "row", "row", 3, "natural"),
@@ -161,40 +162,39 @@ def generate(kd):
                     e(x)
 
     def step(u, vm, do_load, next_reads):
-        c0, c1, c2 = (2 * u) % 3, (2 * u + 1) % 3, (2 * u + 2) % 3
-        half(c0, reads(c1, u, 1), None)
+        c0, c1, c2 = (2 * u) % SETS, (2 * u + 1) % SETS, (2 * u + 2) % SETS
+        half(c0, reads(c1, u % STAGES, 1), None)
         e(f"s_waitcnt vmcnt({vm})")
         e("s_waitcnt lgkmcnt(0)")
         e("s_barrier")
-        half(c1, reads(c2, (u + 1) % 3, 0) if next_reads else None, loads(u) if do_load else None)
+        half(c1, reads(c2, (u + 1) % STAGES, 0) if next_reads else None, loads(u % STAGES) if do_load else None)
 
     e(f"s_mov_b32 %{kd.m0s}, m0")
-    e(f"s_waitcnt vmcnt({2 * kd.loads})")
+    e(f"s_waitcnt vmcnt({(STAGES - 1) * kd.loads})")
     e("s_barrier")
-    e(f"s_cmp_eq_u32 %{kd.phase}, 1")
-    e("s_cbranch_scc1 .Lp1%=")
-    e(f"s_cmp_eq_u32 %{kd.phase}, 2")
-    e("s_cbranch_scc1 .Lp2%=")
-    for p, label in ((0, None), (1, ".Lp1%=:"), (2, ".Lp2%=:")):
-        if label:
-            e(label)
-        for blk in reads((2 * p) % 3, p, 0):
+    for p in range(1, STAGES):
+        e(f"s_cmp_eq_u32 %{kd.phase}, {p}")
+        e(f"s_cbranch_scc1 .Lp{p}%=")
+    for p in range(STAGES):
+        if p:
+            e(f".Lp{p}%=:")
+        for blk in reads((2 * p) % SETS, p, 0):
             for x in blk:
                 e(x)
         if p == 0:
             e(f"s_cmp_eq_u32 %{kd.iters}, 0")
             e("s_cbranch_scc1 .Ltail%=")
         e(f"s_branch .Lu{p}%=")
-    for u in range(3):
+    for u in range(STAGES):
         e(f".Lu{u}%=:")
-        step(u, kd.loads, True, True)
+        step(u, (STAGES - 2) * kd.loads, True, True)
     e(f"s_sub_u32 %{kd.iters}, %{kd.iters}, 1")
     e(f"s_cmp_lg_u32 %{kd.iters}, 0")
     e("s_cbranch_scc1 .Lu0%=")
     e(".Ltail%=:")
-    step(0, kd.loads, False, True)
-    step(1, 0, False, True)
-    step(2, 0, False, False)
+    for u in range(STAGES):   # the last STAGES steps: no loads; the next step's were issued
+        left = max(0, STAGES - 2 - u)
+        step(u, left * kd.loads, False, u < STAGES - 1)
     for _ in range(8):  # the last MFMAs' results before the compiler reads the AGPRs
         e("s_nop 7")
     e(f"s_mov_b32 m0, %{kd.m0s}")
@@ -203,8 +203,8 @@ def generate(kd):
 
 def schedule(nsteps):
     """(phase, iterations) for a product of nsteps K steps"""
-    p = (3 - nsteps % 3) % 3
-    return p, (nsteps - 3 + p) // 3
+    p = (STAGES - nsteps % STAGES) % STAGES
+    return p, (nsteps - STAGES + p) // STAGES
 
 
 def decode_read(kd, ins):
@@ -212,7 +212,7 @@ def decode_read(kd, ins):
     if m := re.match(r"ds_read_b128 v\[(\d+):(\d+)\], %(\d+) offset:(\d+)$", ins):
         reg, op, off = int(m[1]), int(m[3]), int(m[4])
         assert int(m[2]) == reg + 3
-        side = 0 if kd.vm0 <= op < kd.vm0 + 3 else 1
+        side = 0 if kd.vm0 <= op < kd.vm0 + STAGES else 1
         assert kd.region[side][0] == "row", ("b128 read of a col operand", ins)
         blk, r = divmod(off, 2560)
         ch, r = divmod(r, 32)
@@ -222,7 +222,7 @@ def decode_read(kd, ins):
     assert m, ins
     reg, op, off = int(m[1]), int(m[3]), int(m[4])
     assert int(m[2]) == reg + 1
-    side = 0 if kd.vm0 <= op < kd.vm0 + 3 else 1
+    side = 0 if kd.vm0 <= op < kd.vm0 + STAGES else 1
     assert kd.region[side][0] == "col", ("transposed read of a row operand", ins)
     rowb = kd.col_row[side]
     ch, r = divmod(off, 16 * rowb)
@@ -243,20 +243,20 @@ def check(kd, nsteps):
     after a barrier that follows this wave's lgkmcnt(0) after its last read of it; loads go to
     their pointer's slots at the stage of their step, and each pointer advances by its own
     stride after its load; an operand set is refilled only 4 MFMAs or more after its last use."""
-    assert nsteps >= 3
+    assert nsteps >= STAGES
     prog = generate(kd)
     labels = {l[:-1]: n for n, l in enumerate(prog) if l.endswith(":")}
     phase, iters = schedule(nsteps)
     sreg = {kd.iters: iters, kd.phase: phase}
-    stage_of = lambda j: (j + phase) % 3  # noqa: E731
+    stage_of = lambda j: (j + phase) % STAGES  # noqa: E731
     L = kd.loads
-    vmq = [(stage_of(j), j) for j in range(3) for _ in range(L)]
-    stage_data = {stage_of(j): [j, L, None] for j in range(3)}
-    ptr_step = {kd.ptr0 + t: 3 for t in range(L)}
+    vmq = [(stage_of(j), j) for j in range(STAGES) for _ in range(L)]
+    stage_data = {stage_of(j): [j, L, None] for j in range(STAGES)}
+    ptr_step = {kd.ptr0 + t: STAGES for t in range(L)}
     loaded = {}
     reg_holds, pending = {}, []
-    last_read = {0: -1, 1: -1, 2: -1}
-    last_wait = {0: -1, 1: -1, 2: -1}
+    last_read = {s_: -1 for s_ in range(STAGES)}
+    last_wait = {s_: -1 for s_ in range(STAGES)}
     last_barrier = -1
     set_last_use = {}
     acc_seq = {k: [] for k in range(kd.n_acc)}
@@ -343,7 +343,7 @@ def check(kd, nsteps):
             assert last_read[st] < last_wait[st] < last_barrier, ("reload before the reads ended", ins)
             d = stage_data[st]
             if d[0] != j:
-                assert d[1] == 0 and d[0] == j - 3
+                assert d[1] == 0 and d[0] == j - STAGES
                 stage_data[st] = d = [j, 0, None]
             d[1] += 1
             loaded.setdefault(j, []).append(t)
@@ -361,7 +361,7 @@ def check(kd, nsteps):
         pc = nxt
     assert not pending and cur_step == nsteps, (cur_step, nsteps)
     assert all(v == nsteps for v in ptr_step.values()), ptr_step
-    for j in range(3, nsteps):
+    for j in range(STAGES, nsteps):
         assert sorted(loaded[j]) == list(range(L)), (j, loaded[j])
     want = [(j, c) for j in range(nsteps) for c in (0, 1)]
     for k in range(kd.n_acc):
@@ -376,7 +376,7 @@ def header_text():
         out = generate(kd)
         outs = [f'"+a"(acc[{k}])' for k in range(kd.n_acc)] + [f'"+v"(P[{t}])' for t in range(kd.loads)]
         outs += ['"+s"(iters)', '"=&s"(m0save)']
-        ins = [f'"v"(vM[{s}])' for s in range(3)] + [f'"v"(vN[{s}])' for s in range(3)]
+        ins = [f'"v"(vM[{s}])' for s in range(STAGES)] + [f'"v"(vN[{s}])' for s in range(STAGES)]
         ins += ['"s"(sbase)', '"s"(phase)'] + [f'"s"(S[{t}])' for t in range(kd.loads)]
         clob = ['"memory"', '"scc"'] + [f'"v{r}"' for r in range(kd.fb, 256)]
         body = " \\\n    ".join('"' + x + '\\n\\t"' for x in out)
@@ -384,6 +384,7 @@ def header_text():
         parts += [f"// {n}: M side {kd.region[0][0]}, N side {kd.region[1][0]}, NJ = {kd.nj}; "
                   f"{len(out)} instructions",
                   f"#define FX_{n}_STAGE {kd.stage}",
+                  f"#define FX_{n}_STAGES {STAGES}",
                   f"#define FX_{n}_LOADS {kd.loads}",
                   f"#define FX_{n}_N_OFF {kd.n_off}",
                   f"#define FX_{n}_M_INS {kd.region[0][2]}",
@@ -395,7 +396,7 @@ def header_text():
     return "\n".join(parts)
 
 
-STEP_COUNTS = (3, 4, 5, 6, 7, 8, 9, 24, 72, 73, 74, 96)
+STEP_COUNTS = (4, 5, 6, 7, 8, 9, 24, 72, 73, 74, 75, 96)
 
 
 def main(argv):

@@ -291,7 +291,7 @@ __global__ void __launch_bounds__(kGThreads, 1) gemm_bias_act_kernel(GemmArgs a)
 // ---------------------------------------------------------------------------
 // Whole-tile kernels: the forward product above, the input gradient dX = dY W and the
 // weight gradient below, on tiles that divide the output (M % 256 == 0, N % (64 NJ) == 0)
-// and K steps of 32 (K % 32 == 0, K >= 96).  4 waves of 128 x (32 NJ), one workgroup per
+// and K steps of 32 (K % 32 == 0, K >= 128).  4 waves of 128 x (32 NJ), one workgroup per
 // 256 x (64 NJ) tile, the K loop a single generated inline-asm statement (gemm_asm.h, from
 // gemm_asm_gen.py, which documents the schedule and checks it on the CPU).  With the
 // accumulators in AGPRs (one wave per SIMD) and the LDS operand reads interleaved with the
@@ -301,6 +301,9 @@ __global__ void __launch_bounds__(kGThreads, 1) gemm_bias_act_kernel(GemmArgs a)
 // NJ = 4: 256 x 256 tiles; NJ = 3: 256 x 192 tiles (N = 768 is 4 of them: 256 tiles for
 // M = 16384, one per CU, where 256 x 256 tiles would leave a quarter of the CUs idle).
 __device__ __forceinline__ void raw_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+constexpr int kAsmStages = FX_FWD_NJ4_STAGES;  // LDS stages of every generated loop
+static_assert(kAsmStages == FX_WGRAD_STAGES && kAsmStages == FX_DGRAD_NJ4_STAGES, "one stage count");
 
 // One operand tile of a whole-tile kernel as its loads see it.  base: the tile's element
 // (0, 0) at K step 0.  Row operand (K along the rows, `rows` tile rows): LDS rows of 5 16-byte
@@ -330,7 +333,7 @@ __device__ __forceinline__ const uint16_t* slot_addr(const TileSrc& t, int s) {
 // Load pointers, their strides and the prologue: wave-instruction q = wave + 4 t of a stage
 // covers 64 slots of the M-side tile (q < MI), the N-side tile (q < MI + NI) or a pad after
 // them that is never read (loading the N tile's first slot); its LDS slots start at q KiB.
-// Steps 0, 1, 2 go to stages phase + 0, 1, 2 (mod 3); the pointers are left at step 3.
+// Steps 0..3 go to stages phase + 0..3 (mod 4); the pointers are left at step 4.
 template <int L, int MI, int NI>
 __device__ __forceinline__ void asm_gemm_prologue(const TileSrc& ms, const TileSrc& ns, int wave, int lane, int phase,
                                                   uint32_t base, int stage_bytes, uint64_t (&P)[L],
@@ -345,14 +348,14 @@ __device__ __forceinline__ void asm_gemm_prologue(const TileSrc& ms, const TileS
         S[t] = src.step;
     }
 #pragma unroll
-    for (int j = 0; j < 3; ++j) {
-        const int st = (j + phase) % 3;
+    for (int j = 0; j < kAsmStages; ++j) {
+        const int st = (j + phase) % kAsmStages;
 #pragma unroll
         for (int t = 0; t < L; ++t)
             dma16((const void*)(uintptr_t)(P[t] + j * S[t]), base + st * stage_bytes + (wave + 4 * t) * 1024);
     }
 #pragma unroll
-    for (int t = 0; t < L; ++t) P[t] += 3 * S[t];
+    for (int t = 0; t < L; ++t) P[t] += kAsmStages * S[t];
 }
 
 // Per-lane LDS read address of a wave's operand blocks in stage 0 (the stages follow at
@@ -367,10 +370,11 @@ __device__ __forceinline__ uint32_t read_addr(bool col, bool natural, int row_by
     return k * row_bytes + (w0 + 16 * (grp & 1) + 4 * (s16 & 3)) * 2;
 }
 
-// phase and loop iterations for n K steps (the loop body is 3 steps; the last 3 are its tail)
+// phase and loop iterations for n >= 4 K steps (the loop body is 4 steps; the last 4 are its
+// tail)
 __device__ __forceinline__ void asm_gemm_schedule(int nsteps, uint32_t& phase, uint32_t& iters) {
-    phase = __builtin_amdgcn_readfirstlane((3 - nsteps % 3) % 3);
-    iters = __builtin_amdgcn_readfirstlane((nsteps - 3 + (int)phase) / 3);
+    phase = __builtin_amdgcn_readfirstlane((kAsmStages - nsteps % kAsmStages) % kAsmStages);
+    iters = __builtin_amdgcn_readfirstlane((nsteps - kAsmStages + (int)phase) / kAsmStages);
 }
 
 // C^T-layout epilogue of the forward and input-gradient kernels: acc[4 j + i] holds rows
@@ -409,7 +413,7 @@ struct FastGemm {
     static constexpr int kStage = NJ == 4 ? FX_FWD_NJ4_STAGE : FX_FWD_NJ3_STAGE;
     static constexpr int kLoads = NJ == 4 ? FX_FWD_NJ4_LOADS : FX_FWD_NJ3_LOADS;
     static constexpr int kTN = 64 * NJ;
-    static constexpr int kWaveLds = 3 * kStage / 4;
+    static constexpr int kWaveLds = kAsmStages * kStage / 4;
     static_assert(32 * (32 * NJ + kStgExtra) * 2 <= kWaveLds && kWaveLds % 16 == 0, "staging fits a wave's share");
 };
 
@@ -420,7 +424,7 @@ __global__ void __launch_bounds__(256, 1) gemm_fast_kernel(GemmArgs a) {
     using G = FastGemm<NJ>;
     constexpr int L = G::kLoads;
     constexpr bool kGelu = EPI & 1, kH = EPI & 2, kBias = EPI & 4;
-    __shared__ __attribute__((aligned(16))) unsigned char lds[3 * G::kStage];
+    __shared__ __attribute__((aligned(16))) unsigned char lds[kAsmStages * G::kStage];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 5;
@@ -439,9 +443,9 @@ __global__ void __launch_bounds__(256, 1) gemm_fast_kernel(GemmArgs a) {
     else
         asm_gemm_prologue<L, FX_FWD_NJ3_M_INS, FX_FWD_NJ3_N_INS>(ms, ns, wave, lane, phase, base, G::kStage, P, S);
     constexpr int kNOff = NJ == 4 ? FX_FWD_NJ4_N_OFF : FX_FWD_NJ3_N_OFF;
-    uint32_t vM[3], vN[3];
+    uint32_t vM[kAsmStages], vN[kAsmStages];
 #pragma unroll
-    for (int s = 0; s < 3; ++s) {
+    for (int s = 0; s < kAsmStages; ++s) {
         vM[s] = base + s * G::kStage + read_addr(false, true, 0, wm, lane);
         vN[s] = base + s * G::kStage + kNOff + read_addr(false, true, 0, wn, lane);
     }
@@ -510,7 +514,7 @@ struct DgradGemm {
     static constexpr int kNOff = NJ == 4 ? FX_DGRAD_NJ4_N_OFF : FX_DGRAD_NJ3_N_OFF;
     static constexpr int kRow = (64 * NJ + 32) * 2;  // LDS bytes per K row of the W tile
     static constexpr int kTN = 64 * NJ;
-    static constexpr int kWaveLds = 3 * kStage / 4;
+    static constexpr int kWaveLds = kAsmStages * kStage / 4;
     static_assert(32 * (32 * NJ + kStgExtra) * 2 <= kWaveLds && kWaveLds % 16 == 0, "staging fits a wave's share");
 };
 
@@ -518,7 +522,7 @@ template <int NJ, int EPI>
 __global__ void __launch_bounds__(256, 1) gemm_dgrad_fast_kernel(DgradArgs a) {
     using G = DgradGemm<NJ>;
     constexpr int L = G::kLoads;
-    __shared__ __attribute__((aligned(16))) unsigned char lds[3 * G::kStage];
+    __shared__ __attribute__((aligned(16))) unsigned char lds[kAsmStages * G::kStage];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 5;
@@ -536,9 +540,9 @@ __global__ void __launch_bounds__(256, 1) gemm_dgrad_fast_kernel(DgradArgs a) {
         asm_gemm_prologue<L, FX_DGRAD_NJ4_M_INS, FX_DGRAD_NJ4_N_INS>(ms, ns, wave, lane, phase, base, G::kStage, P, S);
     else
         asm_gemm_prologue<L, FX_DGRAD_NJ3_M_INS, FX_DGRAD_NJ3_N_INS>(ms, ns, wave, lane, phase, base, G::kStage, P, S);
-    uint32_t vM[3], vN[3];
+    uint32_t vM[kAsmStages], vN[kAsmStages];
 #pragma unroll
-    for (int s = 0; s < 3; ++s) {
+    for (int s = 0; s < kAsmStages; ++s) {
         vM[s] = base + s * G::kStage + read_addr(false, true, 0, wm, lane);
         vN[s] = base + s * G::kStage + G::kNOff + read_addr(true, true, G::kRow, wn, lane);
     }
@@ -547,6 +551,18 @@ __global__ void __launch_bounds__(256, 1) gemm_dgrad_fast_kernel(DgradArgs a) {
     f32x16 acc[4 * NJ];
 #pragma unroll
     for (int k = 0; k < 4 * NJ; ++k) acc[k] = f32x16{};
+    // EPI 1: the pre-activation of each 32-row block, 4 columns per (j, q), loaded one block
+    // ahead (the first before the K loop: older than the loop's loads, so its waits only
+    // get stricter)
+    uint2 hb[2][NJ][4];
+    auto load_h = [&](int i, uint2 (&d)[NJ][4]) {
+        const uint16_t* hrow = a.H + (int64_t)(m0 + wm + 32 * i + (lane & 31)) * a.ldx + n0 + wn + 4 * g;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) d[j][q] = *reinterpret_cast<const uint2*>(hrow + 32 * j + 8 * q);
+    };
+    if constexpr (EPI == 1) load_h(0, hb[0]);
     if constexpr (NJ == 4)
         asm volatile(FX_DGRAD_NJ4_KLOOP : FX_DGRAD_NJ4_OUTS : FX_DGRAD_NJ4_INS : FX_DGRAD_NJ4_CLOBBERS);
     else
@@ -558,12 +574,12 @@ __global__ void __launch_bounds__(256, 1) gemm_dgrad_fast_kernel(DgradArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int64_t row0 = m0 + wm + 32 * i;
-        const int m = (int)row0 + (lane & 31);
+        if constexpr (EPI == 1)
+            if (i + 1 < 4) load_h(i + 1, hb[(i + 1) & 1]);
         ct_store_block<NJ>(stg, lane, i, a.dX, a.ldx, row0, n0 + wn, acc,
                            [&](int j, int q, const float (&v)[4], float (&o)[4]) {
                                if constexpr (EPI == 1) {
-                                   const uint2 hh = *reinterpret_cast<const uint2*>(
-                                       a.H + (int64_t)m * a.ldx + n0 + wn + 32 * j + 8 * q + 4 * g);
+                                   const uint2 hh = hb[i & 1][j][q];
                                    const float h[4] = {bf16_to_f32((uint16_t)hh.x), bf16_to_f32((uint16_t)(hh.x >> 16)),
                                                        bf16_to_f32((uint16_t)hh.y), bf16_to_f32((uint16_t)(hh.y >> 16))};
 #pragma unroll
@@ -589,7 +605,8 @@ static bool whole_tile_kernels_enabled() {
 // of the tile widths that divide N, the one with the fewest MFMA rounds per CU
 static int fast_gemm_nj(const GemmArgs& a) {
     if (a.idx || a.res || a.nw || a.Xg || !whole_tile_kernels_enabled()) return 0;
-    if (a.M % 256 || a.K % 32 || a.K < 96 || a.lda % 8 || a.ldb % 8 || !a.vec_c || (a.H && !a.vec_h)) return 0;
+    if (a.M % 256 || a.K % 32 || a.K < 32 * kAsmStages || a.lda % 8 || a.ldb % 8 || !a.vec_c || (a.H && !a.vec_h))
+        return 0;
     const int64_t cus = device_cus();
     int64_t best = 0, nj = 0;
     for (int w : {4, 3}) {
@@ -734,21 +751,21 @@ __global__ void __launch_bounds__(kGThreads, 1) gemm_wgrad_kernel(WgradArgs a) {
 
 // The same product on whole tiles (M % 256 == 0, N % 256 == 0, K % 32 == 0) with the
 // generated K loop (gemm_asm.h's WGRAD): 4 waves of 128 x 128, accumulators in AGPRs,
-// 32-token steps in 3 LDS stages loaded two steps ahead.  The slices, their token ranges,
+// 32-token steps in 4 LDS stages loaded three steps ahead.  The slices, their token ranges,
 // the transposed operand reads (lds_op_t's K permutation) and the MFMA order over K are
 // those of gemm_wgrad_kernel, so its partial tiles, and the reduced result, are
 // bit-identical.
 __global__ void __launch_bounds__(256, 1) gemm_wgrad_fast_kernel(WgradArgs a) {
     constexpr int kStage = FX_WGRAD_STAGE, L = FX_WGRAD_LOADS, kRow = (256 + 32) * 2;
     static_assert(FX_WGRAD_N_OFF == 32 * kRow, "stage layout");
-    __shared__ __attribute__((aligned(16))) unsigned char lds[3 * kStage];
+    __shared__ __attribute__((aligned(16))) unsigned char lds[kAsmStages * kStage];
     const int nn = a.N / 256;
     const int ntiles = (a.M / 256) * nn;
     const int sl = blockIdx.x / ntiles, t = blockIdx.x - sl * ntiles;
     const int m0 = (t / nn) * 256, n0 = (t - (t / nn) * nn) * 256;
     const int nk64 = (a.K + 63) / 64;
     const int kb = (int)((int64_t)nk64 * sl / a.slices), ke = (int)((int64_t)nk64 * (sl + 1) / a.slices);
-    const int t0 = 64 * kb, nsteps = (min(64 * ke, a.K) - t0) / 32;  // >= 3: the host checks
+    const int t0 = 64 * kb, nsteps = (min(64 * ke, a.K) - t0) / 32;  // >= 4: the host checks
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = (wave >> 1) * 128, wn = (wave & 1) * 128;
@@ -759,9 +776,9 @@ __global__ void __launch_bounds__(256, 1) gemm_wgrad_fast_kernel(WgradArgs a) {
     const TileSrc ns{a.B + (int64_t)t0 * a.ldb + n0, a.ldb, true, 256, (uint64_t)a.ldb * 64};
     uint64_t P[L], S[L];
     asm_gemm_prologue<L, FX_WGRAD_M_INS, FX_WGRAD_N_INS>(ms, ns, wave, lane, phase, base, kStage, P, S);
-    uint32_t vM[3], vN[3];
+    uint32_t vM[kAsmStages], vN[kAsmStages];
 #pragma unroll
-    for (int s = 0; s < 3; ++s) {
+    for (int s = 0; s < kAsmStages; ++s) {
         vM[s] = base + s * kStage + read_addr(true, false, kRow, wm, lane);
         vN[s] = base + s * kStage + FX_WGRAD_N_OFF + read_addr(true, false, kRow, wn, lane);
     }
@@ -1193,9 +1210,9 @@ extern "C" int fx_linear_wgrad(const uint16_t* dY, int64_t ldy, const uint16_t* 
     a.slices = slices;
     const int64_t tiles = ((M + kGBM - 1) / kGBM) * ((N + kGBN - 1) / kGBN);
     hipStream_t s = (hipStream_t)stream;
-    // whole tiles and 32-token steps, every slice at least 3 steps: the generated loop (with
+    // whole tiles and 32-token steps, every slice at least 4 steps: the generated loop (with
     // several slices each spans at least 4 64-token steps, the last perhaps 32 tokens short)
-    const bool fast = M % 256 == 0 && N % 256 == 0 && K % 32 == 0 && K >= 96 && whole_tile_kernels_enabled();
+    const bool fast = M % 256 == 0 && N % 256 == 0 && K % 32 == 0 && K >= 32 * kAsmStages && whole_tile_kernels_enabled();
     if (fast)
         hipLaunchKernelGGL(gemm_wgrad_fast_kernel, dim3((unsigned)(tiles * slices)), dim3(256), 0, s, a);
     else
@@ -1229,8 +1246,8 @@ extern "C" int fx_linear_dgrad(const uint16_t* dY, int64_t ldy, const uint16_t* 
                (long long)N, (long long)K);
     FX_REQUIRE(M < 0x7fffffffLL && N < 0x7fffffffLL && K < 0x7fffffffLL, "fx_linear_dgrad: size too large");
     const int nj = dgrad_nj(M, N);
-    FX_REQUIRE(M % 256 == 0 && nj != 0 && K % 32 == 0 && K >= 96,
-               "fx_linear_dgrad: whole tiles only (M %% 256, N %% 256 or %% 192, K %% 32 == 0, K >= 96): "
+    FX_REQUIRE(M % 256 == 0 && nj != 0 && K % 32 == 0 && K >= 32 * kAsmStages,
+               "fx_linear_dgrad: whole tiles only (M %% 256, N %% 256 or %% 192, K %% 32 == 0, K >= 128): "
                "M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
     FX_REQUIRE(ldy >= K && ldw >= N && ldx >= N && ldy % 8 == 0 && ldw % 8 == 0 && ldx % 8 == 0,
                "fx_linear_dgrad: bad leading dimension (ldy=%lld ldw=%lld ldx=%lld)", (long long)ldy, (long long)ldw,

@@ -10,13 +10,15 @@ __all__ = [
     "fused_gather_linear",
     "FusedLinear",
     "fused_linear",
+    "FusedMLP",
+    "fused_mlp",
     "setup_env",
     "require_gpu",
 ]
 
 
 def __getattr__(name):
-    if name in ("FusedGatherLinear", "fused_gather_linear", "FusedLinear", "fused_linear"):
+    if name in ("FusedGatherLinear", "fused_gather_linear", "FusedLinear", "fused_linear", "FusedMLP", "fused_mlp"):
         from . import fused_linear as _m
         return getattr(_m, name)
     if name in ("setup_env", "require_gpu"):

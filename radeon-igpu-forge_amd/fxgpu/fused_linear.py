@@ -14,6 +14,10 @@
   GPT's qkv, proj and fc2 projections.  Forwards of at most FEW_ROWS rows (decode
   steps) run on the few-row kernel behind fx_linear_fwd, the whole_tiles() shapes on
   its whole-tile kernel, the others on the library GEMM.
+* ``fused_mlp(x, w1, w2)`` -- gelu_tanh(x w1^T) w2^T as one autograd node: the GELU in
+  the fc epilogue, its derivative in the fc2 input gradient's epilogue (fx_linear_dgrad).
+* ``input_grad(dy, W, h=None)`` -- dx = dy W (and * gelu'(h)) on fx_linear_dgrad for whole
+  tiles, else the library GEMM.
 * ``linear_wgrad(dy, x)`` -- dW = dy^T x for dy (T, N) and x (T, K): the weight
   gradient that ml/fxgpu/fused_linear.py:90-101 computes with rocBLAS.
 * ``linear_ex(x, W, bias, residual, norm_weight, eps, activation)`` -- inference
@@ -69,11 +73,54 @@ FEW_ROWS = 64
 
 def whole_tiles(M, N, K):
     """Shapes that fx_linear_fwd runs on its whole-tile kernel (M % 256 == 0, N % 192 or
-    % 256 == 0, K % 96 == 0) and where that kernel measured faster than the library GEMM:
-    K up to 1024 (the cfg5 qkv and proj, 64 and 22.6 us against 66 and 25.3 us).  With
-    K = 3072 and N = 768 (fc2: one tile per CU) the library GEMM is faster (61.7 against
-    69.8 us)."""
-    return M % 256 == 0 and K % 96 == 0 and K <= 1024 and (N % 256 == 0 or N % 192 == 0)
+    % 256 == 0, K % 32 == 0, K >= 128) and where that kernel measured faster than the library
+    GEMM in isolation: K up to 1024 (the cfg5 qkv and proj, 64 and 22.6 us against 66 and
+    25.3 us).  With K = 3072 and N = 768 (fc2: one tile per CU) the library GEMM is faster
+    (61.7 against 69.8 us).  Taken only with NATIVE_PROJ_FWD."""
+    return M % 256 == 0 and K % 32 == 0 and 128 <= K <= 1024 and (N % 256 == 0 or N % 192 == 0)
+
+
+# Routing switches, set by measurements inside the cfg5 training step.  In isolation, with
+# the operands left in the caches by the previous call, the whole-tile kernels beat the
+# library GEMM at these shapes; inside the step, where the weights come from HBM, they
+# lose: 18.92 against 18.61 ms per step with the input gradients on fx_linear_dgrad, 18.93
+# against 18.82 ms with the qkv / proj forwards on fx_linear_fwd.  So both are off.
+# NATIVE_INPUT_GRAD: input gradients on fx_linear_dgrad where input_grad() takes them;
+# NATIVE_PROJ_FWD: the whole_tiles() forwards on fx_linear_fwd.  False: the library GEMM.
+NATIVE_INPUT_GRAD = False
+NATIVE_PROJ_FWD = False
+
+
+def dgrad_tiles(M, N, K):
+    """Shapes fx_linear_dgrad takes (whole-tile kernel): dX (M, N) = dY (M, K) W (K, N)."""
+    return M % 256 == 0 and (N % 256 == 0 or N % 192 == 0) and K % 32 == 0 and K >= 128
+
+
+def input_grad(dy2, weight, h=None):
+    """dx = dy2 @ weight (bf16), and with h (the pre-activation of a GELU(tanh) layer feeding
+    this one) dx * gelu'(h).  With NATIVE_INPUT_GRAD, on fx_linear_dgrad for dgrad_tiles()
+    shapes where it measured at least as fast as the library GEMM in isolation (input widths
+    up to 1024 columns: the cfg5 qkv, proj and fc input gradients, 52.9 / 22.6 / 68.1 us
+    against 53.7 / 25.9 / 68.7 us), and always with h (the GELU backward folded into the
+    epilogue: 116 us against 78 + 45.7 us for the cfg5 fc2 product and fx_gelu_bwd); else
+    torch.mm, then fx_gelu_bwd for h."""
+    M, K = dy2.shape
+    N = weight.shape[1]
+    native = (NATIVE_INPUT_GRAD and dy2.is_cuda and dgrad_tiles(M, N, K) and (h is not None or N <= 1024)
+              and weight.is_contiguous() and weight.data_ptr() % 16 == 0
+              and dy2.stride(1) == 1 and dy2.stride(0) % 8 == 0 and dy2.data_ptr() % 16 == 0
+              and (h is None or (h.is_contiguous() and h.data_ptr() % 16 == 0)))
+    if native:
+        dx = torch.empty(M, N, device=dy2.device, dtype=torch.bfloat16)
+        call("fx_linear_dgrad", ptr(dy2), dy2.stride(0), ptr(weight), N, ptr(h), ptr(dx), N, M, N, K,
+             stream_of(dy2))
+        return dx
+    dx = torch.mm(dy2, weight)
+    if h is None:
+        return dx
+    dh = torch.empty_like(dx)
+    call("fx_gelu_bwd", ptr(dx), ptr(h), ptr(dh), dh.numel(), stream_of(dx))
+    return dh
 
 
 def _native_fwd(x2, weight):
@@ -97,7 +144,7 @@ class Linear(torch.autograd.Function):
         x2 = _rows(x)
         M, K = x2.shape
         native = x2.is_cuda and weight.is_contiguous() and weight.data_ptr() % 16 == 0 and K % 8 == 0
-        if native and (0 < M <= FEW_ROWS or whole_tiles(M, weight.shape[0], K)):
+        if native and (0 < M <= FEW_ROWS or (NATIVE_PROJ_FWD and whole_tiles(M, weight.shape[0], K))):
             y = _native_fwd(x2, weight)
         else:
             y = torch.mm(x2, weight.t())
@@ -109,7 +156,7 @@ class Linear(torch.autograd.Function):
     def backward(ctx, dy):
         x2, weight = ctx.saved_tensors
         dy2 = _rows(dy.to(torch.bfloat16) if dy.dtype != torch.bfloat16 else dy)
-        dx = torch.mm(dy2, weight).view(ctx.xshape) if ctx.needs_input_grad[0] else None
+        dx = input_grad(dy2, weight).view(ctx.xshape) if ctx.needs_input_grad[0] else None
         dW = linear_wgrad(dy2, x2) if ctx.needs_input_grad[1] else None
         return dx, dW
 
@@ -224,7 +271,7 @@ class FusedLinear(torch.autograd.Function):
             call("fx_gelu_bwd", ptr(dy2), ptr(h), ptr(dh), dh.numel(), stream_of(dy2))
         else:
             dh = dy2
-        dx = torch.mm(dh, weight).view(ctx.xshape) if ctx.needs_input_grad[0] else None
+        dx = input_grad(dh, weight).view(ctx.xshape) if ctx.needs_input_grad[0] else None
         dW = linear_wgrad(dh, x2) if ctx.needs_input_grad[1] else None
         db = dh.sum(0) if (ctx.has_bias and ctx.needs_input_grad[2]) else None
         return dx, dW, db, None
@@ -233,6 +280,58 @@ class FusedLinear(torch.autograd.Function):
 def fused_linear(x, weight, bias=None, activation="gelu_tanh"):
     """y = activation(x @ weight.T + bias) with the activation fused into the GEMM."""
     return FusedLinear.apply(x, weight, bias, activation)
+
+
+class FusedMLP(torch.autograd.Function):
+    """y = gelu_tanh(x W1^T) W2^T (no biases): the GPT MLP (ml/fxlm/model.py:64-66,71,
+    nn.Linear fc -> F.gelu(approximate="tanh") -> nn.Linear fc2) as one autograd node, so
+    that the backward can fold the GELU derivative into the fc2 input-gradient product
+    (fx_linear_dgrad with the pre-activation).  Same kernels and roundings as fused_linear
+    followed by linear in the forward."""
+
+    @staticmethod
+    def forward(ctx, x, w1, w2):
+        if x.dtype != torch.bfloat16 or w1.dtype != torch.bfloat16 or w2.dtype != torch.bfloat16:
+            raise TypeError("x, w1 and w2 must be bfloat16")
+        if not (x.is_cuda and w1.is_cuda and w2.is_cuda):
+            raise TypeError("x, w1 and w2 must be cuda tensors")
+        K = x.shape[-1]
+        if w1.dim() != 2 or w1.shape[1] != K or w2.dim() != 2 or w2.shape[1] != w1.shape[0]:
+            raise ValueError(f"weights must be (F, {K}) and (N, F), got {tuple(w1.shape)}, {tuple(w2.shape)}")
+        if K % 8 or w1.shape[0] % 8:
+            raise ValueError("in_features and the hidden width must be multiples of 8")
+        if not (w1.is_contiguous() and w2.is_contiguous()):
+            raise ValueError("weights must be contiguous")
+        x2 = _rows(x)
+        M, Fh = x2.shape[0], w1.shape[0]
+        u = torch.empty(M, Fh, device=x.device, dtype=torch.bfloat16)
+        h = torch.empty_like(u) if any(ctx.needs_input_grad) else None
+        call("fx_linear_fwd", ptr(x2), x2.stride(0), None, 0, 0, ptr(w1), None, ptr(u), ptr(h), None,
+             M, Fh, K, 1, stream_of(x))
+        N = w2.shape[0]
+        if 0 < M <= FEW_ROWS or (NATIVE_PROJ_FWD and whole_tiles(M, N, Fh)):
+            y = _native_fwd(u, w2)
+        else:
+            y = torch.mm(u, w2.t())
+        ctx.save_for_backward(x2, w1, w2, u, h)
+        ctx.xshape = x.shape
+        return y.view(*x.shape[:-1], N)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, w1, w2, u, h = ctx.saved_tensors
+        dy2 = _rows(dy.to(torch.bfloat16) if dy.dtype != torch.bfloat16 else dy)
+        dh = input_grad(dy2, w2, h)              # (dy W2) gelu'(h)
+        dw2 = linear_wgrad(dy2, u) if ctx.needs_input_grad[2] else None
+        dx = input_grad(dh, w1).view(ctx.xshape) if ctx.needs_input_grad[0] else None
+        dw1 = linear_wgrad(dh, x2) if ctx.needs_input_grad[1] else None
+        return dx, dw1, dw2
+
+
+def fused_mlp(x, w1, w2):
+    """gelu_tanh(x @ w1.T) @ w2.T with the GELU in the fc epilogue and its derivative in the
+    fc2 input gradient's epilogue."""
+    return FusedMLP.apply(x, w1, w2)
 
 
 def linear_ex(x, weight, bias=None, residual=None, norm_weight=None, eps=1e-6, activation=None):

@@ -16,7 +16,7 @@ import torch
 import torch.nn.functional as Fn
 from torch import nn
 
-from fxgpu.fused_linear import FEW_ROWS, fused_linear, linear, linear_ex
+from fxgpu.fused_linear import FEW_ROWS, fused_linear, fused_mlp, linear, linear_ex
 
 from .attention import decode_attention, flash_attention_qkv
 from .cross_entropy import linear_cross_entropy
@@ -74,13 +74,20 @@ class Block(nn.Module):
             return linear(x, layer.weight)
         return layer(x)
 
-    def _mlp(self, x):
-        x, h = self._prenorm(x, self.ln2_w)
+    def _mlp_out(self, h):
+        """fc2(gelu(fc(h))) (ml/fxlm/model.py:64-66,71): one node (fused_mlp) when both the
+        MLP and the projections take the fused kernels"""
+        if self.mlp_impl == "fused" and self.linear_impl == "fused" and h.is_cuda:
+            return fused_mlp(h, self.fc.weight, self.fc2.weight)
         if self.mlp_impl == "fused":
             u = fused_linear(h, self.fc.weight, None, "gelu_tanh")
         else:
             u = Fn.gelu(self.fc(h), approximate="tanh")
-        return x + self._lin(u, self.fc2)
+        return self._lin(u, self.fc2)
+
+    def _mlp(self, x):
+        x, h = self._prenorm(x, self.ln2_w)
+        return x + self._mlp_out(h)
 
     def _add_prenorm(self, x, r, w):
         """(x + r, norm(x + r)); the fused form adds inside the norm's own pass."""
@@ -115,11 +122,7 @@ class Block(nn.Module):
             y = Fn.scaled_dot_product_attention(q, k, v, is_causal=True)
             y = y.transpose(1, 2)
         x, h = self._add_prenorm(x, self._lin(y.reshape(B, T, D), self.proj), self.ln2_w)
-        if self.mlp_impl == "fused":
-            u = fused_linear(h, self.fc.weight, None, "gelu_tanh")
-        else:
-            u = Fn.gelu(self.fc(h), approximate="tanh")
-        return x, self._lin(u, self.fc2)
+        return x, self._mlp_out(h)
 
     def step(self, x, kv, pos, lens):
         """One new token per sequence: x (B, 1, D) at position lens[b] - 1 (lens (B,) int32

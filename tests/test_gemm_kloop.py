@@ -30,10 +30,10 @@ def test_header_is_generated(gen):
 
 
 @pytest.mark.parametrize("kind", range(5))
-@pytest.mark.parametrize("nsteps", [3, 4, 5, 6, 7, 8, 24, 72, 73, 74, 96])
+@pytest.mark.parametrize("nsteps", [4, 5, 6, 7, 8, 9, 24, 72, 73, 74, 75, 96])
 def test_schedule_checks(gen, kind, nsteps):
     phase, iters = gen.check(gen.KINDS[kind], nsteps)
-    assert (nsteps - 3 + phase) % 3 == 0 and iters == (nsteps - 3 + phase) // 3
+    assert (nsteps - 4 + phase) % 4 == 0 and iters == (nsteps - 4 + phase) // 4
 
 
 def test_layouts(gen):
@@ -41,7 +41,7 @@ def test_layouts(gen):
     for kd in gen.KINDS:
         assert kd.stage == 4 * kd.loads * 1024
         assert kd.region[0][1] + kd.region[1][1] <= kd.stage
-        assert 3 * kd.stage <= 160 * 1024
+        assert gen.STAGES * kd.stage <= 160 * 1024
     fwd4, fwd3, dg4, dg3, wg = gen.KINDS
     assert (fwd4.loads, fwd3.loads, dg4.loads, dg3.loads, wg.loads) == (10, 9, 10, 9, 9)
 
@@ -114,7 +114,7 @@ def test_checker_catches_planted_mistakes(gen, monkeypatch, kind, mistake):
     good = gen.generate
     monkeypatch.setattr(gen, "generate", lambda kd: mistake(list(good(kd))))
     caught = 0
-    for n in (3, 4, 5, 72, 73, 74):
+    for n in (4, 5, 6, 7, 72, 73, 74, 75):
         try:
             gen.check(gen.KINDS[kind], n)
         except (AssertionError, KeyError, TypeError):

@@ -342,14 +342,15 @@ def _linear_fwd(x, W, b, act, want_h):
 
 
 @pytest.mark.parametrize("M,K,N,act,bias,want_h,pad_k", [
-    (512, 96, 256, 1, True, True, 0),      # 256-wide tiles; one K step group: the loop's tail only
-    (512, 192, 192, 0, False, False, 0),   # 192-wide tiles, one loop iteration
+    (512, 128, 256, 1, True, True, 0),     # 256-wide tiles; 4 K steps: the loop's tail only
+    (512, 256, 192, 0, False, False, 0),   # 192-wide tiles, one loop iteration
     (1024, 768, 768, 0, False, False, 64), # proj: 192-wide (a round of 16 tiles), rows of X strided
     (768, 768, 2304, 0, True, False, 0),   # qkv widths
     (256, 3072, 768, 1, False, True, 0),   # fc2 depth
     (16384, 768, 3072, 1, False, True, 0), # the cfg5 MLP fc (256-wide tiles): GELU and the pre-activation
-    (512, 128, 256, 1, True, True, 0),     # 4 K steps: enters the loop body at its third step
-    (512, 160, 192, 0, False, False, 8),   # 5 K steps: enters at the second
+    (512, 160, 256, 1, True, True, 0),     # 5 K steps: enters the loop body at its fourth step
+    (512, 192, 192, 0, False, False, 8),   # 6 K steps: enters at the third
+    (512, 224, 256, 0, True, False, 0),    # 7 K steps: enters at the second
 ])
 def test_whole_tile_kernel_matches_general_kernel(dev, M, K, N, act, bias, want_h, pad_k):
     g = torch.Generator(device=dev).manual_seed(M + K + N)
@@ -377,9 +378,10 @@ def test_whole_tile_kernel_matches_general_kernel(dev, M, K, N, act, bias, want_
 # for bit; FX_GEMM_GENERAL=1 (read on every call) routes the product to the general kernel.
 
 @pytest.mark.parametrize("T,M,N,ld_pad", [
-    (96, 256, 256, 0),       # 3 steps: the loop's tail only, one slice (bf16 written directly)
-    (128, 256, 512, 0),      # 4 steps: enters the loop body at its third step
-    (160, 512, 256, 8),      # 5 steps: enters at the second; rows of dY and X strided
+    (128, 256, 256, 0),      # 4 steps: the loop's tail only, one slice (bf16 written directly)
+    (160, 256, 512, 0),      # 5 steps: enters the loop body at its fourth step
+    (192, 512, 256, 8),      # 6 steps: enters at the third; rows of dY and X strided
+    (224, 256, 256, 0),      # 7 steps: enters at the second
     (544, 256, 512, 0),      # 2 slices of 8 and 9 steps
     (4096, 768, 768, 0),     # proj-shaped: 9 tiles x 28 slices
     (16384, 3072, 768, 0),   # the cfg5 fc weight (7 slices of 36-37 64-token steps)
@@ -415,9 +417,9 @@ def _dgrad(dy, W, h=None):
 
 
 @pytest.mark.parametrize("M,N,K,pad", [
-    (256, 256, 96, 0),       # 256-wide tiles, the loop's tail only
-    (512, 192, 128, 0),      # 192-wide tiles, 4 K steps (entry at the body's third step)
-    (256, 768, 160, 8),      # 5 K steps; rows of dY strided
+    (256, 256, 128, 0),      # 256-wide tiles, the loop's tail only
+    (512, 192, 160, 0),      # 192-wide tiles, 5 K steps (entry at the body's fourth step)
+    (256, 768, 224, 8),      # 7 K steps; rows of dY strided
     (1024, 3072, 768, 0),    # fc2's input gradient shape (192-wide tiles at this M)
     (16384, 3072, 768, 0),   # cfg5 fc2 (256-wide tiles, 768 tiles)
     (16384, 768, 2304, 0),   # cfg5 qkv
@@ -441,8 +443,44 @@ def test_dgrad_whole_tile_kernel(dev, M, N, K, pad):
 
 def test_dgrad_rejects_partial_tiles(dev):
     from fxgpu.abi import call, ptr, stream_of
-    dy = torch.zeros(300, 96, device=dev, dtype=torch.bfloat16)
-    W = torch.zeros(96, 256, device=dev, dtype=torch.bfloat16)
+    dy = torch.zeros(300, 128, device=dev, dtype=torch.bfloat16)
+    W = torch.zeros(128, 256, device=dev, dtype=torch.bfloat16)
     dx = torch.empty(300, 256, device=dev, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="whole tiles"):
-        call("fx_linear_dgrad", ptr(dy), 96, ptr(W), 256, None, ptr(dx), 256, 300, 256, 96, stream_of(dy))
+        call("fx_linear_dgrad", ptr(dy), 128, ptr(W), 256, None, ptr(dx), 256, 300, 256, 128, stream_of(dy))
+    with pytest.raises(ValueError, match="whole tiles"):      # 3 K steps: fewer than the loop's 4
+        call("fx_linear_dgrad", ptr(dy), 128, ptr(W), 256, None, ptr(dx), 256, 256, 256, 96, stream_of(dy))
+
+
+# ---- the GPT MLP as one node (fused_mlp): GELU in the fc epilogue, its derivative in the fc2
+# input gradient's epilogue ---------------------------------------------------------------------
+
+@pytest.mark.parametrize("native", [True, False])  # the whole-tile kernels where shapes allow, or the library
+@pytest.mark.parametrize("M,K,Fh,N", [(512, 256, 1024, 256),     # whole tiles: fx_linear_dgrad with H
+                                      (300, 64, 256, 64),        # partial tiles: library GEMM + fx_gelu_bwd
+                                      (16384, 768, 3072, 768)])  # cfg5
+def test_fused_mlp_against_composition_and_fp32(dev, monkeypatch, native, M, K, Fh, N):
+    import fxgpu.fused_linear as FL
+    monkeypatch.setattr(FL, "NATIVE_INPUT_GRAD", native)
+    monkeypatch.setattr(FL, "NATIVE_PROJ_FWD", native)
+    g = torch.Generator(device=dev).manual_seed(M + Fh)
+    x = torch.randn(M, K, device=dev, generator=g).bfloat16()
+    w1 = (torch.randn(Fh, K, device=dev, generator=g) * K ** -0.5).bfloat16()
+    w2 = (torch.randn(N, Fh, device=dev, generator=g) * Fh ** -0.5).bfloat16()
+    dy = torch.randn(M, N, device=dev, generator=g).bfloat16()
+    print(f"fused_mlp M={M} K={K} F={Fh} N={N}", flush=True)
+    xa, w1a, w2a = (t.clone().requires_grad_() for t in (x, w1, w2))
+    y = FL.fused_mlp(xa, w1a, w2a)
+    y.backward(dy)
+    xb, w1b, w2b = (t.clone().requires_grad_() for t in (x, w1, w2))
+    yb = FL.linear(FL.fused_linear(xb, w1b, None, "gelu_tanh"), w2b)
+    yb.backward(dy)
+    assert torch.equal(y, yb)                      # the same forward kernels
+    xr, w1r, w2r = (t.float().requires_grad_() for t in (x, w1, w2))
+    yr = F.gelu(xr @ w1r.t(), approximate="tanh") @ w2r.t()
+    yr.backward(dy.float())
+    assert oracle_close(y, yr, 4e-3)               # through the bf16 GELU output
+    for ours, comp, ref in ((xa.grad, xb.grad, xr.grad), (w1a.grad, w1b.grad, w1r.grad),
+                            (w2a.grad, w2b.grad, w2r.grad)):
+        assert oracle_close(ours, ref)
+        assert oracle_close(comp, ref)
