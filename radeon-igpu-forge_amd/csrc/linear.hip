@@ -593,18 +593,23 @@ __global__ void __launch_bounds__(256, 1) gemm_dgrad_fast_kernel(DgradArgs a) {
     }
 }
 
-// FX_GEMM_GENERAL=1 in the environment routes every product to the general kernels
-// (gemm_bias_act_kernel, gemm_wgrad_kernel): a diagnostic switch, read on every call, that
-// lets a test compare the whole-tile kernels with them on the same shapes
-static bool whole_tile_kernels_enabled() {
+// FX_GEMM_GENERAL in the environment routes products to the general kernels
+// (gemm_bias_act_kernel, gemm_wgrad_kernel): "1" all of them, a value containing 'f' the
+// forwards, one containing 'w' the weight gradients.  A diagnostic switch, read on every
+// call, that lets a test or a benchmark compare the whole-tile kernels with them.
+static bool whole_tile_kernels_enabled(char kind) {
     const char* v = getenv("FX_GEMM_GENERAL");
-    return !(v && v[0] == '1');
+    if (!v) return true;
+    if (v[0] == '1') return false;
+    for (; *v; ++v)
+        if (*v == kind) return false;
+    return true;
 }
 
 // 4 or 3 (the tile width in 64-column units) when gemm_fast_kernel takes the product, else 0:
 // of the tile widths that divide N, the one with the fewest MFMA rounds per CU
 static int fast_gemm_nj(const GemmArgs& a) {
-    if (a.idx || a.res || a.nw || a.Xg || !whole_tile_kernels_enabled()) return 0;
+    if (a.idx || a.res || a.nw || a.Xg || !whole_tile_kernels_enabled('f')) return 0;
     if (a.M % 256 || a.K % 32 || a.K < 32 * kAsmStages || a.lda % 8 || a.ldb % 8 || !a.vec_c || (a.H && !a.vec_h))
         return 0;
     const int64_t cus = device_cus();
@@ -1212,7 +1217,7 @@ extern "C" int fx_linear_wgrad(const uint16_t* dY, int64_t ldy, const uint16_t* 
     hipStream_t s = (hipStream_t)stream;
     // whole tiles and 32-token steps, every slice at least 4 steps: the generated loop (with
     // several slices each spans at least 4 64-token steps, the last perhaps 32 tokens short)
-    const bool fast = M % 256 == 0 && N % 256 == 0 && K % 32 == 0 && K >= 32 * kAsmStages && whole_tile_kernels_enabled();
+    const bool fast = M % 256 == 0 && N % 256 == 0 && K % 32 == 0 && K >= 32 * kAsmStages && whole_tile_kernels_enabled('w');
     if (fast)
         hipLaunchKernelGGL(gemm_wgrad_fast_kernel, dim3((unsigned)(tiles * slices)), dim3(256), 0, s, a);
     else
