@@ -1,7 +1,8 @@
 """Benchmark: the fxlm GPT 12L-d768 training step on one MI355X, plus the hot-path kernels.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-    python bench.py --only {attention,ce,norm,adamw,linear,step,copy,decode,cpu}   (profiling runs)
+    python bench.py --only {attention,ce,norm,adamw,linear,step,copy,decode,cpu,fc-ours,fc-library,
+                            fc-ours-cold,fc-library-cold}   (profiling runs)
     python bench.py --counter-table p_counter_collection.csv [...]   (per-kernel counter table)
     python bench.py --traffic-table FETCH.csv WRITE.csv COPY_FETCH.csv COPY_WRITE.csv
     python bench.py --pmc-summary FETCH.csv WRITE.csv COPY_FETCH.csv COPY_WRITE.csv
@@ -389,6 +390,29 @@ def bench_copy(torch):
     return {"bytes_read": n * 2, "bytes_written": n * 2, "us": round(t, 2)}
 
 
+def bench_fc_product(torch, which, cold):
+    """Profiling workload: the cfg5 fc product y = x W^T (16384 x 768 x 3072) 12 times, on
+    this build's whole-tile kernel (`ours`) or torch.mm (hipBLASLt, `library`); with `cold`
+    a 1 GiB buffer is written before each call, so the operands come from HBM."""
+    from fxgpu.abi import call, ptr, stream_of
+    M, K, N = 16384, 768, 3072
+    g = torch.Generator(device="cuda").manual_seed(1)
+    x = torch.randn(M, K, device="cuda", generator=g).bfloat16()
+    W = (torch.randn(N, K, device="cuda", generator=g) * 0.02).bfloat16()
+    y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+    flush = torch.empty(1 << 29, device="cuda", dtype=torch.bfloat16)
+    for i in range(12):
+        if cold:
+            flush.fill_(i)
+        if which == "ours":
+            call("fx_linear_fwd", ptr(x), K, None, 0, 0, ptr(W), None, ptr(y), None, None, M, N, K, 0,
+                 stream_of(x))
+        else:
+            torch.mm(x, W.t(), out=y)
+    torch.cuda.synchronize()
+    return {"product": which, "cold": cold, "calls": 12}
+
+
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "attn_bwd_cfg2_traffic.json")
 _TRAFFIC_KERNELS = ("attn_bwd_dq_kernel", "attn_bwd_dkv_kernel")
 
@@ -531,7 +555,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU baseline")
     ap.add_argument("--only", choices=["attention", "ce", "norm", "adamw", "linear", "step", "copy", "decode",
-                                       "cpu"],
+                                       "cpu", "fc-ours", "fc-library", "fc-ours-cold", "fc-library-cold"],
                     help="run one workload and print its figures (for profiling runs)")
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV",
                                                        "COPY_WRITE_CSV"),
@@ -564,7 +588,11 @@ def main():
     if args.only:
         fn = {"attention": bench_attention, "ce": bench_ce, "norm": bench_norm, "adamw": bench_adamw,
               "linear": bench_linear, "copy": bench_copy, "decode": bench_decode, "cpu": cpu_baseline,
-              "step": lambda t: gpu_step_bench(t, args.steps, args.warmup)}[args.only]
+              "step": lambda t: gpu_step_bench(t, args.steps, args.warmup),
+              "fc-ours": lambda t: bench_fc_product(t, "ours", False),
+              "fc-library": lambda t: bench_fc_product(t, "library", False),
+              "fc-ours-cold": lambda t: bench_fc_product(t, "ours", True),
+              "fc-library-cold": lambda t: bench_fc_product(t, "library", True)}[args.only]
         r = fn(torch)
         print(json.dumps({k: v for k, v in r.items() if not k.startswith("flop")}))
         return
