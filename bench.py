@@ -1,7 +1,7 @@
 """Benchmark: the fxlm GPT 12L-d768 training step on one MI355X, plus the hot-path kernels.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-    python bench.py --only {attention,ce,norm,adamw,linear,step,copy,decode,cpu,fc-ours,fc-library,
+    python bench.py --only {attention,ce,norm,adamw,linear,wgrad,step,copy,decode,cpu,fc-ours,fc-library,
                             fc-ours-cold,fc-library-cold}   (profiling runs)
     python bench.py --counter-table p_counter_collection.csv [...]   (per-kernel counter table)
     python bench.py --traffic-table FETCH.csv WRITE.csv COPY_FETCH.csv COPY_WRITE.csv
@@ -22,6 +22,7 @@ are launched on (torch's current stream):
   RMSNorm cfg4 [65536, 768]: forward and backward
   FlatAdamW cfg4: one step over 124,373,760 parameters
   fused linear + GELU: the cfg5 MLP fc (16384 x 768 x 3072)
+  weight gradients: the four cfg5 dW = dy^T x products over 16384 tokens
 and, on the host CPU, the reference's naive-PyTorch fp32 training step
 (oracle/gpt.py) on a bounded sample.  Prints ONE JSON line.
 """
@@ -219,6 +220,36 @@ def bench_linear(torch):
     return {"shape": [M, K, N], "fwd_us": round(t, 2), "tflops": round(f / t / 1e6, 1),
             "frac_of_bf16_peak": round(f / t / 1e6 / BF16_PEAK_TFLOPS, 4),
             "hipblaslt_mm_plus_gelu_us": round(t_ref, 2), "projections": proj}
+
+
+def bench_wgrad(torch):
+    """The GPT's weight gradients dW = dy^T x at cfg5 (16384 tokens) on fx_linear_wgrad
+    (the whole-tile kernel with the split-K reduce), beside the general kernel
+    (FX_GEMM_GENERAL=w) and the library's torch.mm(dy.t(), x)."""
+    from fxgpu.fused_linear import linear_wgrad
+    T = 16384
+    g = torch.Generator(device="cuda").manual_seed(8)
+    out = {}
+    for name, (M, N) in {"qkv": (2304, 768), "proj": (768, 768), "fc": (3072, 768), "fc2": (768, 3072)}.items():
+        dy = torch.randn(T, M, device="cuda", generator=g).bfloat16()
+        x = torch.randn(T, N, device="cuda", generator=g).bfloat16()
+        t = time_us(torch, lambda: linear_wgrad(dy, x))
+        prev = os.environ.get("FX_GEMM_GENERAL")
+        os.environ["FX_GEMM_GENERAL"] = "w"
+        try:
+            t_gen = time_us(torch, lambda: linear_wgrad(dy, x))
+        finally:
+            if prev is None:
+                os.environ.pop("FX_GEMM_GENERAL", None)
+            else:
+                os.environ["FX_GEMM_GENERAL"] = prev
+        t_mm = time_us(torch, lambda: torch.mm(dy.t(), x))
+        f = 2.0 * T * M * N
+        out[name] = {"shape_TMN": [T, M, N], "us": round(t, 2), "tflops": round(f / t / 1e6, 1),
+                     "frac_of_bf16_peak": round(f / t / 1e6 / BF16_PEAK_TFLOPS, 4),
+                     "general_kernel_us": round(t_gen, 2), "library_mm_us": round(t_mm, 2)}
+        del dy, x
+    return out
 
 
 def bench_decode(torch):
@@ -554,7 +585,7 @@ def main():
     # counts, so a batch's first step can allocate; 42 ms once when it fell in the timed steps)
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU baseline")
-    ap.add_argument("--only", choices=["attention", "ce", "norm", "adamw", "linear", "step", "copy", "decode",
+    ap.add_argument("--only", choices=["attention", "ce", "norm", "adamw", "linear", "wgrad", "step", "copy", "decode",
                                        "cpu", "fc-ours", "fc-library", "fc-ours-cold", "fc-library-cold"],
                     help="run one workload and print its figures (for profiling runs)")
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV",
@@ -587,7 +618,8 @@ def main():
     lib()
     if args.only:
         fn = {"attention": bench_attention, "ce": bench_ce, "norm": bench_norm, "adamw": bench_adamw,
-              "linear": bench_linear, "copy": bench_copy, "decode": bench_decode, "cpu": cpu_baseline,
+              "linear": bench_linear, "wgrad": bench_wgrad, "copy": bench_copy, "decode": bench_decode,
+              "cpu": cpu_baseline,
               "step": lambda t: gpu_step_bench(t, args.steps, args.warmup),
               "fc-ours": lambda t: bench_fc_product(t, "ours", False),
               "fc-library": lambda t: bench_fc_product(t, "library", False),
@@ -602,6 +634,7 @@ def main():
     norm = bench_norm(torch)
     adamw = bench_adamw(torch)
     lin = bench_linear(torch)
+    wg = bench_wgrad(torch)
     dec = bench_decode(torch)
     torch.cuda.empty_cache()
     step = gpu_step_bench(torch, args.steps, args.warmup)
@@ -632,7 +665,7 @@ def main():
         "gpu_over_cpu": (round(step["tok_s"] / cpu["value"], 1) if cpu else None),
         "kernels": {"attention_cfg2": {k: v for k, v in attn.items() if not k.startswith("flop")},
                     "cross_entropy_cfg3": ce, "rmsnorm_cfg4": norm, "flat_adamw_cfg4": adamw,
-                    "fused_linear_gelu_cfg5_fc": lin, "decode": dec},
+                    "fused_linear_gelu_cfg5_fc": lin, "linear_wgrad_cfg5": wg, "decode": dec},
         "final_loss": round(step["loss"], 4),
     }
     print(json.dumps(out))
