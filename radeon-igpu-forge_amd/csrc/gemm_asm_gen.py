@@ -109,7 +109,7 @@ class Kind:
 
 KINDS = [Kind("FWD_NJ4", "row", "row", 4, "natural"), Kind("FWD_NJ3", "row", "row", 3, "natural"),
          Kind("DGRAD_NJ4", "row", "col", 4, "natural"), Kind("DGRAD_NJ3", "row", "col", 3, "natural"),
-         Kind("WGRAD", "col", "col", 4, "lds_op_t")]
+         Kind("WGRAD", "col", "col", 4, "lds_op_t"), Kind("WGRAD_NJ3", "col", "col", 3, "lds_op_t")]
 
 
 def block_reads(kd, b, x, stage, ch):
@@ -146,7 +146,7 @@ def generate(kd):
     def mfma(k, cur):
         j, i = k // 4, k % 4
         m_reg, n_reg = kd.freg(cur, i), kd.freg(cur, 4 + j)
-        a, b_ = (n_reg, m_reg) if kd.name != "WGRAD" else (m_reg, n_reg)
+        a, b_ = (n_reg, m_reg) if not kd.name.startswith("WGRAD") else (m_reg, n_reg)
         e(f"v_mfma_f32_32x32x16_bf16 %{kd.acc0 + k}, v[{a}:{a + 3}], v[{b_}:{b_ + 3}], %{kd.acc0 + k}")
 
     def half(cur, rd, extra):
@@ -317,7 +317,7 @@ def check(kd, nsteps):
             k = int(m[1]) - kd.acc0
             assert int(m[6]) == int(m[1]) and int(m[3]) == int(m[2]) + 3 and int(m[5]) == int(m[4]) + 3
             ra, rb = int(m[2]), int(m[4])
-            m_reg, n_reg = (rb, ra) if kd.name != "WGRAD" else (ra, rb)
+            m_reg, n_reg = (rb, ra) if not kd.name.startswith("WGRAD") else (ra, rb)
             bm, qm = divmod(m_reg - kd.fb, 4 * kd.set_size)
             bn, qn = divmod(n_reg - kd.fb, 4 * kd.set_size)
             assert bm == bn and qm == 4 * (k % 4) and qn == 4 * (4 + k // 4), ("wrong operand blocks", ins)

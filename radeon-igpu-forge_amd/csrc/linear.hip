@@ -760,39 +760,55 @@ __global__ void __launch_bounds__(kGThreads, 1) gemm_wgrad_kernel(WgradArgs a) {
 // the transposed operand reads (lds_op_t's K permutation) and the MFMA order over K are
 // those of gemm_wgrad_kernel, so its partial tiles, and the reduced result, are
 // bit-identical.
+template <int NJ>
+struct WgradGemm {
+    static constexpr int kStage = NJ == 4 ? FX_WGRAD_STAGE : FX_WGRAD_NJ3_STAGE;
+    static constexpr int kLoads = NJ == 4 ? FX_WGRAD_LOADS : FX_WGRAD_NJ3_LOADS;
+    static constexpr int kNOff = NJ == 4 ? FX_WGRAD_N_OFF : FX_WGRAD_NJ3_N_OFF;
+    static constexpr int kRowM = (256 + 32) * 2, kRowN = (64 * NJ + 32) * 2;  // LDS bytes per token row
+    static_assert(kNOff == 32 * kRowM, "stage layout");
+};
+
+template <int NJ>
 __global__ void __launch_bounds__(256, 1) gemm_wgrad_fast_kernel(WgradArgs a) {
-    constexpr int kStage = FX_WGRAD_STAGE, L = FX_WGRAD_LOADS, kRow = (256 + 32) * 2;
-    static_assert(FX_WGRAD_N_OFF == 32 * kRow, "stage layout");
-    __shared__ __attribute__((aligned(16))) unsigned char lds[kAsmStages * kStage];
-    const int nn = a.N / 256;
+    using G = WgradGemm<NJ>;
+    constexpr int L = G::kLoads;
+    __shared__ __attribute__((aligned(16))) unsigned char lds[kAsmStages * G::kStage];
+    const int nn = a.N / (64 * NJ);
     const int ntiles = (a.M / 256) * nn;
     const int sl = blockIdx.x / ntiles, t = blockIdx.x - sl * ntiles;
-    const int m0 = (t / nn) * 256, n0 = (t - (t / nn) * nn) * 256;
+    const int m0 = (t / nn) * 256, n0 = (t - (t / nn) * nn) * 64 * NJ;
     const int nk64 = (a.K + 63) / 64;
     const int kb = (int)((int64_t)nk64 * sl / a.slices), ke = (int)((int64_t)nk64 * (sl + 1) / a.slices);
     const int t0 = 64 * kb, nsteps = (min(64 * ke, a.K) - t0) / 32;  // >= 4: the host checks
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = (wave >> 1) * 128, wn = (wave & 1) * 128;
+    const int wm = (wave >> 1) * 128, wn = (wave & 1) * 32 * NJ;
     const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(lds));
     uint32_t phase, iters;
     asm_gemm_schedule(nsteps, phase, iters);
     const TileSrc ms{a.A + (int64_t)t0 * a.lda + m0, a.lda, true, 256, (uint64_t)a.lda * 64};
-    const TileSrc ns{a.B + (int64_t)t0 * a.ldb + n0, a.ldb, true, 256, (uint64_t)a.ldb * 64};
+    const TileSrc ns{a.B + (int64_t)t0 * a.ldb + n0, a.ldb, true, 64 * NJ, (uint64_t)a.ldb * 64};
     uint64_t P[L], S[L];
-    asm_gemm_prologue<L, FX_WGRAD_M_INS, FX_WGRAD_N_INS>(ms, ns, wave, lane, phase, base, kStage, P, S);
+    if constexpr (NJ == 4)
+        asm_gemm_prologue<L, FX_WGRAD_M_INS, FX_WGRAD_N_INS>(ms, ns, wave, lane, phase, base, G::kStage, P, S);
+    else
+        asm_gemm_prologue<L, FX_WGRAD_NJ3_M_INS, FX_WGRAD_NJ3_N_INS>(ms, ns, wave, lane, phase, base, G::kStage, P, S);
     uint32_t vM[kAsmStages], vN[kAsmStages];
 #pragma unroll
     for (int s = 0; s < kAsmStages; ++s) {
-        vM[s] = base + s * kStage + read_addr(true, false, kRow, wm, lane);
-        vN[s] = base + s * kStage + FX_WGRAD_N_OFF + read_addr(true, false, kRow, wn, lane);
+        vM[s] = base + s * G::kStage + read_addr(true, false, G::kRowM, wm, lane);
+        vN[s] = base + s * G::kStage + G::kNOff + read_addr(true, false, G::kRowN, wn, lane);
     }
     const uint32_t sbase = base + wave * 1024;
     uint32_t m0save;
-    f32x16 acc[16];
+    f32x16 acc[4 * NJ];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) acc[k] = f32x16{};
-    asm volatile(FX_WGRAD_KLOOP : FX_WGRAD_OUTS : FX_WGRAD_INS : FX_WGRAD_CLOBBERS);
+    for (int k = 0; k < 4 * NJ; ++k) acc[k] = f32x16{};
+    if constexpr (NJ == 4)
+        asm volatile(FX_WGRAD_KLOOP : FX_WGRAD_OUTS : FX_WGRAD_INS : FX_WGRAD_CLOBBERS);
+    else
+        asm volatile(FX_WGRAD_NJ3_KLOOP : FX_WGRAD_NJ3_OUTS : FX_WGRAD_NJ3_INS : FX_WGRAD_NJ3_CLOBBERS);
     (void)m0save;
 
     // lane holds column n = n0 + wn + 32 j + lane%32 and rows m0 + wm + 32 i + 8 (e/4) + 4 g
@@ -803,7 +819,7 @@ __global__ void __launch_bounds__(256, 1) gemm_wgrad_fast_kernel(WgradArgs a) {
     const int g = lane >> 5;
     auto store = [&](auto* out, int64_t ldo) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < NJ; ++j) {
             const uint32_t voff = (uint32_t)(4 * g * ldo + wn + 32 * j + (lane & 31));
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -1169,20 +1185,41 @@ extern "C" int fx_linear_fwd_ex(const fxLinearArgs* args, void* stream) {
     return linear_fwd(a, (hipStream_t)stream);
 }
 
-// K steps of 64 tokens per slice at least 4, at most 32 slices, and no more workgroups
-// than CUs (one 147 KB workgroup per CU)
-static int wgrad_slices(int64_t M, int64_t N, int64_t K) {
-    const int64_t tiles = ((M + kGBM - 1) / kGBM) * ((N + kGBN - 1) / kGBN);
+// The weight gradient's plan: the tile width (0: the general kernel's 256 x 256 tiles, or
+// the whole-tile kernel's 256 x 64 NJ) and the K split.  Slices: at least 4 K steps of 64
+// tokens each, at most 32, and no more workgroups than CUs (one workgroup per CU).  The
+// whole-tile kernel takes M % 256 == 0, N % (64 NJ) == 0, K % 32 == 0, K >= 128.  With
+// FX_GEMM_GENERAL selecting the general kernel the slices stay those of the whole-tile plan,
+// so the two produce the same partials.  256 x 192 tiles wherever N % 192 == 0: more tiles,
+// hence fewer slices and less fp32 partial traffic (5 slices instead of 7 at the cfg5 fc
+// shapes); measured 67.9 / 43.1 / 80.4 / 78.5 µs against 80.3 / 47.6 / 92.9 / 81.9 for
+// 256 x 256 tiles (qkv / proj / fc / fc2 weight gradients, reduce included) and 18.05
+// against 18.47 ms per cfg5 step.  FX_WGRAD_TILE=256 keeps 256 x 256 tiles (comparisons).
+struct WgradPlan {
+    int nj, slices;
+    bool fast;
+};
+static WgradPlan wgrad_plan(int64_t M, int64_t N, int64_t K) {
+    WgradPlan p{0, 1, false};
+    const char* tw = getenv("FX_WGRAD_TILE");
+    const bool want4 = tw && tw[0] == '2' && tw[1] == '5' && tw[2] == '6';
+    if (M % 256 == 0 && K % 32 == 0 && K >= 32 * kAsmStages) {
+        if (!want4 && N % 192 == 0) p.nj = 3;
+        else if (N % 256 == 0) p.nj = 4;
+    }
+    const int64_t tiles = p.nj ? (M / 256) * (N / (64 * p.nj)) : ((M + kGBM - 1) / kGBM) * ((N + kGBN - 1) / kGBN);
     const int64_t nk = (K + kWBK - 1) / kWBK;
     int64_t s = device_cus() / tiles;
     if (s > nk / 4) s = nk / 4;
     if (s > 32) s = 32;
-    return s < 1 ? 1 : (int)s;
+    p.slices = s < 1 ? 1 : (int)s;
+    p.fast = p.nj != 0 && whole_tile_kernels_enabled('w');
+    return p;
 }
 
 extern "C" int64_t fx_linear_wgrad_workspace(int64_t M, int64_t N, int64_t K) {
     if (M <= 0 || N <= 0 || K <= 0) return 0;
-    const int s = wgrad_slices(M, N, K);
+    const int s = wgrad_plan(M, N, K).slices;
     return s > 1 ? (int64_t)s * M * N * (int64_t)sizeof(float) : 0;
 }
 
@@ -1199,7 +1236,8 @@ extern "C" int fx_linear_wgrad(const uint16_t* dY, int64_t ldy, const uint16_t* 
                (long long)ldx, (long long)ldw);
     FX_REQUIRE(((((uintptr_t)dY) | ((uintptr_t)X) | ((uintptr_t)dW) | ((uintptr_t)work)) & 15) == 0,
                "fx_linear_wgrad: dY, X, dW and work must be 16-byte aligned");
-    const int slices = K > 0 ? wgrad_slices(M, N, K) : 1;
+    const WgradPlan plan = K > 0 ? wgrad_plan(M, N, K) : WgradPlan{0, 1, false};
+    const int slices = plan.slices;
     FX_REQUIRE(slices == 1 || work != nullptr, "fx_linear_wgrad: null workspace (%d slices)", slices);
     WgradArgs a;
     a.A = dY;
@@ -1213,15 +1251,19 @@ extern "C" int fx_linear_wgrad(const uint16_t* dY, int64_t ldy, const uint16_t* 
     a.N = (int)N;
     a.K = (int)K;
     a.slices = slices;
-    const int64_t tiles = ((M + kGBM - 1) / kGBM) * ((N + kGBN - 1) / kGBN);
     hipStream_t s = (hipStream_t)stream;
     // whole tiles and 32-token steps, every slice at least 4 steps: the generated loop (with
     // several slices each spans at least 4 64-token steps, the last perhaps 32 tokens short)
-    const bool fast = M % 256 == 0 && N % 256 == 0 && K % 32 == 0 && K >= 32 * kAsmStages && whole_tile_kernels_enabled('w');
-    if (fast)
-        hipLaunchKernelGGL(gemm_wgrad_fast_kernel, dim3((unsigned)(tiles * slices)), dim3(256), 0, s, a);
-    else
+    if (plan.fast) {
+        const int64_t tiles = (M / 256) * (N / (64 * plan.nj));
+        if (plan.nj == 4)
+            hipLaunchKernelGGL(gemm_wgrad_fast_kernel<4>, dim3((unsigned)(tiles * slices)), dim3(256), 0, s, a);
+        else
+            hipLaunchKernelGGL(gemm_wgrad_fast_kernel<3>, dim3((unsigned)(tiles * slices)), dim3(256), 0, s, a);
+    } else {
+        const int64_t tiles = ((M + kGBM - 1) / kGBM) * ((N + kGBN - 1) / kGBN);
         hipLaunchKernelGGL(gemm_wgrad_kernel, dim3((unsigned)(tiles * slices)), dim3(kGThreads), 0, s, a);
+    }
     if (int e = check_launch("gemm_wgrad")) return e;
     if (slices == 1) return 0;
     int64_t blocks = (M * N / 8 + 255) / 256;

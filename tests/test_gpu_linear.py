@@ -384,14 +384,17 @@ def test_whole_tile_kernel_matches_general_kernel(dev, M, K, N, act, bias, want_
     (224, 256, 256, 0),      # 7 steps: enters at the second
     (544, 256, 512, 0),      # 2 slices of 8 and 9 steps
     (4096, 768, 768, 0),     # proj-shaped: 9 tiles x 28 slices
-    (16384, 3072, 768, 0),   # the cfg5 fc weight (7 slices of 36-37 64-token steps)
+    (16384, 3072, 768, 0),   # the cfg5 fc weight (7 slices of 36-37 64-token steps; 5 with 192-wide tiles)
+    (2048, 768, 2304, 0),    # qkv widths, 192-wide tiles divide both
 ])
-def test_wgrad_whole_tile_kernel_matches_general(dev, monkeypatch, T, M, N, ld_pad):
+@pytest.mark.parametrize("tile", ["256", "192"])   # FX_WGRAD_TILE=256: 256 x 256 tiles; else 256 x 192 where N allows
+def test_wgrad_whole_tile_kernel_matches_general(dev, monkeypatch, T, M, N, ld_pad, tile):
     from fxgpu.fused_linear import linear_wgrad
+    monkeypatch.setenv("FX_WGRAD_TILE", tile)
     g = torch.Generator(device=dev).manual_seed(T + M + N)
     dy = torch.randn(T, M + ld_pad, device=dev, generator=g).bfloat16()[:, :M]
     x = torch.randn(T, N + ld_pad, device=dev, generator=g).bfloat16()[:, :N]
-    print(f"whole-tile wgrad T={T} M={M} N={N} ldy={dy.stride(0)}", flush=True)
+    print(f"whole-tile wgrad T={T} M={M} N={N} ldy={dy.stride(0)} tile={tile}", flush=True)
     dw = linear_wgrad(dy, x)
     monkeypatch.setenv("FX_GEMM_GENERAL", "1")
     dw_gen = linear_wgrad(dy, x)
