@@ -115,13 +115,16 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 __device__ __forceinline__ float log2_fast(float x) { return __builtin_amdgcn_logf(x); }
 
 // GELU, tanh approximation: 0.5 h (1 + tanh(u)), u = sqrt(2/pi) (h + 0.044715 h^3),
-// evaluated as h - h / (e + 1) with e = exp(2u) (= h * sigmoid(2u)); the reciprocal is
-// v_rcp_f32 (1 ulp), not a correctly rounded division (a ten-instruction sequence).
-// e = inf gives h, e = 0 gives 0.
+// evaluated as h / (1 + e) with e = exp(-2u) (= h * sigmoid(2u)): e = 2^(h (k0 + k1 h^2)),
+// the constants -2 log2(e) sqrt(2/pi) (1, 0.044715) folded, so three multiplies / fmas,
+// v_exp_f32, one add, v_rcp_f32 (1 ulp, not a correctly rounded division, a
+// ten-instruction sequence) and one multiply.  e = 0 gives h, e = inf gives h * 0 (-0 for
+// negative h, as 0.5 h (1 + tanh(u)) gives); h = +inf gives +inf.
 __device__ __forceinline__ float gelu_tanh(float h) {
-    const float u = 0.7978845608028654f * fmaf(0.044715f * h, h * h, h);
-    const float e = exp2_fast(2.f * kLog2e * u);
-    return h - h * __builtin_amdgcn_rcpf(e + 1.f);
+    constexpr float k0 = -2.f * 1.4426950408889634f * 0.7978845608028654f;
+    constexpr float k1 = k0 * 0.044715f;
+    const float e = exp2_fast(h * fmaf(h * h, k1, k0));
+    return h * __builtin_amdgcn_rcpf(e + 1.f);
 }
 
 // d/dh of the above: 0.5 (1 + t) + 0.5 h (1 - t^2) u'(h), t = tanh(u) = 1 - 2 / (e + 1)
