@@ -1,7 +1,7 @@
 """Benchmark: the fxlm GPT 12L-d768 training step on one MI355X, plus the hot-path kernels.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-    python bench.py --only {attention,ce,norm,adamw,linear,wgrad,step,copy,decode,cpu,fc-ours,fc-library,
+    python bench.py --only {attention,ce,norm,adamw,linear,wgrad,head,step,copy,decode,cpu,fc-ours,fc-library,
                             fc-ours-cold,fc-library-cold}   (profiling runs)
     python bench.py --counter-table p_counter_collection.csv [...]   (per-kernel counter table)
     python bench.py --traffic-table FETCH.csv WRITE.csv COPY_FETCH.csv COPY_WRITE.csv
@@ -23,6 +23,7 @@ are launched on (torch's current stream):
   FlatAdamW cfg4: one step over 124,373,760 parameters
   fused linear + GELU: the cfg5 MLP fc (16384 x 768 x 3072)
   weight gradients: the four cfg5 dW = dy^T x products over 16384 tokens
+  linear-CE head: the cfg5 tied head, unfused chunk loop against the fused kernels
 and, on the host CPU, the reference's naive-PyTorch fp32 training step
 (oracle/gpt.py) on a bounded sample.  Prints ONE JSON line.
 """
@@ -249,6 +250,49 @@ def bench_wgrad(torch):
                      "frac_of_bf16_peak": round(f / t / 1e6 / BF16_PEAK_TFLOPS, 4),
                      "general_kernel_us": round(t_gen, 2), "library_mm_us": round(t_mm, 2)}
         del dy, x
+    return out
+
+
+def bench_head(torch):
+    """The cfg5 tied head, linear_cross_entropy over x (16384, 768) and E (50304, 768): the
+    unfused chunk loop (library logits GEMM, fx_ce_fwd_grad, dx and dW GEMMs) against the
+    fused kernels (fx_lce_fwd: the GEMM with the online CE in its epilogue; fx_lce_grad: the
+    GEMM again with the dlogits in its epilogue), for training (forward + backward) and for
+    the loss-only path (no grad)."""
+    import fxlm.cross_entropy as ce
+    N, D, V = 16384, 768, 50304
+    g = torch.Generator(device="cuda").manual_seed(12)
+    x = torch.randn(N, D, device="cuda", generator=g).bfloat16().requires_grad_()
+    w = (torch.randn(V, D, device="cuda", generator=g) * 0.02).bfloat16().requires_grad_()
+    tg = torch.randint(0, V, (N,), device="cuda", generator=g)
+    old = ce.FUSED_LINEAR_CE_LOSS, ce.FUSED_LINEAR_CE_TRAIN
+
+    def train():
+        ce.linear_cross_entropy(x, w, tg).backward()
+        x.grad = w.grad = None
+
+    def loss_only():
+        with torch.no_grad():
+            ce.linear_cross_entropy(x, w, tg)
+    out = {"shape_NDV": [N, D, V], "gemm_flop": 2 * N * D * V}
+    try:
+        for fused in (False, True):
+            ce.FUSED_LINEAR_CE_LOSS = ce.FUSED_LINEAR_CE_TRAIN = fused
+            tag = "fused" if fused else "unfused"
+            out[f"train_{tag}_us"] = round(time_us(torch, train, iters=5, warm=2), 1)
+            out[f"loss_only_{tag}_us"] = round(time_us(torch, loss_only, iters=5, warm=2), 1)
+        # the fused loss pass alone: the logits GEMM with its online-CE epilogue + the merge
+        row_loss = torch.empty(N, device="cuda", dtype=torch.float32)
+        xd = x.detach()
+        t = time_us(torch, lambda: ce._lce_fwd(xd, w.detach(), tg, -100, row_loss), iters=10, warm=3)
+        out["lce_fwd_us"] = round(t, 1)
+        out["lce_fwd_tflops"] = round(out["gemm_flop"] / t / 1e6, 1)
+        out["lce_fwd_frac_of_bf16_peak"] = round(out["gemm_flop"] / t / 1e6 / BF16_PEAK_TFLOPS, 4)
+        t_mm = time_us(torch, lambda: torch.mm(xd, w.detach().t()), iters=10, warm=3)
+        out["library_logits_mm_us"] = round(t_mm, 1)
+    finally:
+        ce.FUSED_LINEAR_CE_LOSS, ce.FUSED_LINEAR_CE_TRAIN = old
+    del x, w
     return out
 
 
@@ -585,7 +629,8 @@ def main():
     # counts, so a batch's first step can allocate; 42 ms once when it fell in the timed steps)
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU baseline")
-    ap.add_argument("--only", choices=["attention", "ce", "norm", "adamw", "linear", "wgrad", "step", "copy", "decode",
+    ap.add_argument("--only", choices=["attention", "ce", "norm", "adamw", "linear", "wgrad", "head", "step", "copy",
+                                       "decode",
                                        "cpu", "fc-ours", "fc-library", "fc-ours-cold", "fc-library-cold"],
                     help="run one workload and print its figures (for profiling runs)")
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV",
@@ -618,7 +663,8 @@ def main():
     lib()
     if args.only:
         fn = {"attention": bench_attention, "ce": bench_ce, "norm": bench_norm, "adamw": bench_adamw,
-              "linear": bench_linear, "wgrad": bench_wgrad, "copy": bench_copy, "decode": bench_decode,
+              "linear": bench_linear, "wgrad": bench_wgrad, "head": bench_head, "copy": bench_copy,
+              "decode": bench_decode,
               "cpu": cpu_baseline,
               "step": lambda t: gpu_step_bench(t, args.steps, args.warmup),
               "fc-ours": lambda t: bench_fc_product(t, "ours", False),
@@ -635,6 +681,8 @@ def main():
     adamw = bench_adamw(torch)
     lin = bench_linear(torch)
     wg = bench_wgrad(torch)
+    head = bench_head(torch)
+    torch.cuda.empty_cache()
     dec = bench_decode(torch)
     torch.cuda.empty_cache()
     step = gpu_step_bench(torch, args.steps, args.warmup)
@@ -665,7 +713,8 @@ def main():
         "gpu_over_cpu": (round(step["tok_s"] / cpu["value"], 1) if cpu else None),
         "kernels": {"attention_cfg2": {k: v for k, v in attn.items() if not k.startswith("flop")},
                     "cross_entropy_cfg3": ce, "rmsnorm_cfg4": norm, "flat_adamw_cfg4": adamw,
-                    "fused_linear_gelu_cfg5_fc": lin, "linear_wgrad_cfg5": wg, "decode": dec},
+                    "fused_linear_gelu_cfg5_fc": lin, "linear_wgrad_cfg5": wg,
+                    "linear_ce_head_cfg5": head, "decode": dec},
         "final_loss": round(step["loss"], 4),
     }
     print(json.dumps(out))

@@ -363,6 +363,33 @@ int fx_linear_wgrad(const uint16_t* dY, int64_t ldy, const uint16_t* X, int64_t 
 int fx_linear_dgrad(const uint16_t* dY, int64_t ldy, const uint16_t* W, int64_t ldw, const uint16_t* H,
                     uint16_t* dX, int64_t ldx, int64_t M, int64_t N, int64_t K, void* stream);
 
+/* ---- fused linear cross-entropy ------------------------------------------- */
+
+/* Bytes of workspace fx_lce_fwd needs for M rows of an (V, K) head, or 0 when the fused
+ * kernels do not take the shape (they need V % 256 == 0 or V % 192 == 0, K % 32 == 0 and
+ * K >= 128); such heads stay on the mm + fx_ce_fwd_grad chunk loop. */
+int64_t fx_lce_workspace(int64_t M, int64_t V, int64_t K);
+
+/* Loss half of a linear cross-entropy with the logits never stored: logits = X E^T
+ * (X (M, K) bf16 with row stride ldx, E (V, K) bf16 contiguous) are formed tile by tile in
+ * MFMA accumulators, rounded to bf16 as a stored logit is, and reduced on the spot to a
+ * (max, sum exp(x - max)) pair per row and tile plus the target's logit; a second kernel
+ * merges the pairs in a fixed order into stat[r] = (M_r, Z_r) (fp32 pairs) and writes
+ * row_loss[r] = M_r + log Z_r - x_t (0 for rows whose target is ignore_index or outside
+ * [0, V)).  work: fx_lce_workspace bytes, 16-byte aligned.  Replaces the chunk loop's
+ * torch.mm + ce_fwd_grad loss pass (ml/fxlm/cross_entropy.py:127-130, :170-183). */
+int fx_lce_fwd(const uint16_t* X, int64_t ldx, const uint16_t* E, const int64_t* target, int64_t ignore_index,
+               void* work, float* stat, float* row_loss, int64_t M, int64_t V, int64_t K, void* stream);
+
+/* Gradient half: the same product again, and dl = exp(x - M_r) (mul / Z_r) - mul [c == t]
+ * written as bf16 (row stride ldd, zero rows for ignored targets), given fx_lce_fwd's stat
+ * and the device scalar mul (grad_scale / n_valid): the dlogits of fx_ce_fwd_grad without
+ * the logits in memory.  Replaces the chunk loop's torch.mm + ce_fwd_grad gradient pass
+ * (ml/fxlm/cross_entropy.py:127-130). */
+int fx_lce_grad(const uint16_t* X, int64_t ldx, const uint16_t* E, const int64_t* target, int64_t ignore_index,
+                const float* stat, const float* mul, uint16_t* dl, int64_t ldd, int64_t M, int64_t V, int64_t K,
+                void* stream);
+
 #ifdef __cplusplus
 }
 #endif

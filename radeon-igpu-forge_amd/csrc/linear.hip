@@ -316,12 +316,13 @@ struct TileSrc {
     bool col;
     int cols;
     uint64_t step;
+    int rmax = 1 << 30;  // row operand: tile rows past this one load this row (a ragged last tile)
 };
 
 __device__ __forceinline__ const uint16_t* slot_addr(const TileSrc& t, int s) {
     if (!t.col) {
         const int r = s / 5;
-        return t.base + (int64_t)r * t.ld + 8 * min(s - 5 * r, 3);
+        return t.base + (int64_t)min(r, t.rmax) * t.ld + 8 * min(s - 5 * r, 3);
     }
     const int spr = t.cols / 8 + 4;
     const int r = s / spr;
@@ -386,7 +387,7 @@ __device__ __forceinline__ void asm_gemm_schedule(int nsteps, uint32_t& phase, u
 constexpr int kStgExtra = 8;  // staging row padding (elements)
 template <int NJ, class Value>
 __device__ __forceinline__ void ct_store_block(uint16_t* stg, int lane, int i, uint16_t* out, int64_t ld, int64_t row0,
-                                               int col0, const f32x16 (&acc)[4 * NJ], Value&& value) {
+                                               int col0, const f32x16 (&acc)[4 * NJ], Value&& value, int nrows = 32) {
     constexpr int LDE = 32 * NJ + kStgExtra;
     const int g = lane >> 5;
 #pragma unroll
@@ -404,7 +405,7 @@ __device__ __forceinline__ void ct_store_block(uint16_t* stg, int lane, int i, u
     for (int k = 0; k < 2 * NJ; ++k) {
         const int idx = lane + 64 * k;
         const int r = idx / (4 * NJ), c = idx - r * (4 * NJ);
-        st16(out + (row0 + r) * ld + col0 + 8 * c, *reinterpret_cast<const uint4*>(stg + r * LDE + 8 * c));
+        if (r < nrows) st16(out + (row0 + r) * ld + col0 + 8 * c, *reinterpret_cast<const uint4*>(stg + r * LDE + 8 * c));
     }
 }
 
@@ -417,26 +418,22 @@ struct FastGemm {
     static_assert(32 * (32 * NJ + kStgExtra) * 2 <= kWaveLds && kWaveLds % 16 == 0, "staging fits a wave's share");
 };
 
-// Forward: C = act(X W^T + bias), with the pre-activation H.  EPI: bit 0 GELU, bit 1 H out,
-// bit 2 bias (no residual, gather or Xg)
-template <int NJ, int EPI>
-__global__ void __launch_bounds__(256, 1) gemm_fast_kernel(GemmArgs a) {
+// The product of one 256 x (64 NJ) tile: acc = A[m0.., :] B[n0.., :]^T over K (A rows past
+// m0 + rmax read row m0 + rmax), in the C^T layout ct_store_block describes.  Every wave is
+// done with the LDS stages when it returns.
+template <int NJ>
+__device__ __forceinline__ void fast_tile_product(const uint16_t* A, int64_t lda, const uint16_t* B, int64_t ldb, int K,
+                                                  int m0, int n0, int rmax, unsigned char* lds, int wave, int lane,
+                                                  f32x16 (&acc)[4 * NJ]) {
     using G = FastGemm<NJ>;
     constexpr int L = G::kLoads;
-    constexpr bool kGelu = EPI & 1, kH = EPI & 2, kBias = EPI & 4;
-    __shared__ __attribute__((aligned(16))) unsigned char lds[kAsmStages * G::kStage];
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int g = lane >> 5;
     const int wm = (wave >> 1) * 128, wn = (wave & 1) * 32 * NJ;
-    int m0, n0, nt;
-    gemm_tile(blockIdx.x, a.M / 256, a.N / G::kTN, m0, n0, nt);
-    n0 = nt * G::kTN;
     const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(lds));
     uint32_t phase, iters;
-    asm_gemm_schedule(a.K / 32, phase, iters);
-    const TileSrc ms{a.A + (int64_t)m0 * a.lda, a.lda, false, 0, 64};
-    const TileSrc ns{a.B + (int64_t)n0 * a.ldb, a.ldb, false, 0, 64};
+    asm_gemm_schedule(K / 32, phase, iters);
+    TileSrc ms{A + (int64_t)m0 * lda, lda, false, 0, 64};
+    ms.rmax = rmax;
+    const TileSrc ns{B + (int64_t)n0 * ldb, ldb, false, 0, 64};
     uint64_t P[L], S[L];
     if constexpr (NJ == 4)
         asm_gemm_prologue<L, FX_FWD_NJ4_M_INS, FX_FWD_NJ4_N_INS>(ms, ns, wave, lane, phase, base, G::kStage, P, S);
@@ -451,7 +448,6 @@ __global__ void __launch_bounds__(256, 1) gemm_fast_kernel(GemmArgs a) {
     }
     const uint32_t sbase = base + wave * 1024;
     uint32_t m0save;
-    f32x16 acc[4 * NJ];
 #pragma unroll
     for (int k = 0; k < 4 * NJ; ++k) acc[k] = f32x16{};
     if constexpr (NJ == 4)
@@ -459,10 +455,28 @@ __global__ void __launch_bounds__(256, 1) gemm_fast_kernel(GemmArgs a) {
     else
         asm volatile(FX_FWD_NJ3_KLOOP : FX_FWD_NJ3_OUTS : FX_FWD_NJ3_INS : FX_FWD_NJ3_CLOBBERS);
     (void)m0save;
+    raw_barrier();  // every wave is done reading the stages (the loop ends with no load in flight)
+}
+
+// Forward: C = act(X W^T + bias), with the pre-activation H.  EPI: bit 0 GELU, bit 1 H out,
+// bit 2 bias (no residual, gather or Xg)
+template <int NJ, int EPI>
+__global__ void __launch_bounds__(256, 1) gemm_fast_kernel(GemmArgs a) {
+    using G = FastGemm<NJ>;
+    constexpr bool kGelu = EPI & 1, kH = EPI & 2, kBias = EPI & 4;
+    __shared__ __attribute__((aligned(16))) unsigned char lds[kAsmStages * G::kStage];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 5;
+    const int wm = (wave >> 1) * 128, wn = (wave & 1) * 32 * NJ;
+    int m0, n0, nt;
+    gemm_tile(blockIdx.x, a.M / 256, a.N / G::kTN, m0, n0, nt);
+    n0 = nt * G::kTN;
+    f32x16 acc[4 * NJ];
+    fast_tile_product<NJ>(a.A, a.lda, a.B, a.ldb, a.K, m0, n0, 1 << 30, lds, wave, lane, acc);
 
     // epilogue: h = acc + bias (H, when wanted), then C = act(h), rounded as
     // gemm_bias_act_kernel rounds them
-    raw_barrier();  // every wave is done reading the stages (the loop ends with no load in flight)
     uint16_t* stg = reinterpret_cast<uint16_t*>(lds + wave * G::kWaveLds);
     float bias[NJ][4][4];
 #pragma unroll
@@ -489,6 +503,212 @@ __global__ void __launch_bounds__(256, 1) gemm_fast_kernel(GemmArgs a) {
                                    o[e] = kGelu ? gelu_tanh(h) : h;
                                }
                            });
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Linear cross-entropy on the whole-tile product: the logits X E^T (E the (V, K) head
+// weight) exist only in the accumulators of one 256 x (64 NJ) tile.  Each logit is rounded
+// to bf16, as the unfused path stores it, and then used in fp32 exactly as ce_row_kernel
+// uses a stored one:
+//   lce_stats_kernel: per row and column tile, (max, sum exp(x - max)) into part[tile][row]
+//     (the two waves of a row block merged in LDS), and the target's logit into xt[row]
+//     from the one lane that holds it;
+//   lce_combine_kernel: per row, the tiles' pairs merged in a fixed order into (M, Z), and
+//     the row loss M + log Z - x_t (0 for ignored rows);
+//   lce_grad_kernel: the product again, and dl = exp(x - M) (mul / Z) - mul [col == t]
+//     stored as bf16, zero rows for ignored targets: the dlogits of ce_row_kernel without
+//     the logits ever reaching memory.
+// Semantics: the chunk loop of ml/fxlm/cross_entropy.py:107-149 (mm, then ce_fwd_grad)
+// with the target rules of ml/fxlm/kernels/ce.hip:32-116 (valid = t != ignore_index and
+// 0 <= t < V; out-of-range targets give no loss and a zero gradient row).
+struct LceArgs {
+    const uint16_t* X;   // (M, K), row stride ldx
+    int64_t ldx;
+    const uint16_t* E;   // (V, K), contiguous
+    const int64_t* target;
+    int64_t ignore_index;
+    float2* part;        // stats: (V / (64 NJ), M)
+    float* xt;           // stats: (M,)
+    float2* stat;        // combine: out, grad: in; (M,) pairs (M, Z)
+    const float* mul;    // grad: device scalar
+    uint16_t* dl;        // grad: (M, V), row stride ldd
+    int64_t ldd;
+    int M, V, K;
+};
+
+// (max, sum of exp(x - max)) pairs: merge (m2, s2) into (m, s); -inf sides carry s == 0
+__device__ __forceinline__ void lce_merge(float& m, float& s, float m2, float s2) {
+    const float mn = fmaxf(m, m2);
+    const float ea = (m == mn) ? 1.f : exp2_fast((m - mn) * kLog2e);
+    const float eb = (m2 == mn) ? 1.f : exp2_fast((m2 - mn) * kLog2e);
+    s = s * ea + s2 * eb;
+    m = mn;
+}
+
+// the value lanes l and l ^ 32 hold for one row, combined (same operand order in both
+// lanes, so both end with the same bits)
+__device__ __forceinline__ float lce_pair_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float lce_pair_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// bf16 rounding of a pair (round-to-nearest-even, as the unfused path stores the logits)
+__device__ __forceinline__ void round2(float& x, float& y) {
+    const uint32_t w = pack_bf16x2(x, y);
+    x = bf16_lo(w);
+    y = bf16_hi(w);
+}
+
+// Where the target column t of a row lies among a lane's accumulators: lane l holds columns
+// c0 + 32 j + 8 q + 4 (l / 32) + e of its row (c0 = the wave's first column).  Returns
+// 16 j + 4 q + e, or -1 when another lane (or tile) holds it.
+template <int NJ>
+__device__ __forceinline__ int lce_target_slot(int64_t t, int64_t c0, int g) {
+    const int64_t o = t - c0;
+    if (o < 0 || o >= 32 * NJ || ((o >> 2) & 1) != g) return -1;
+    return (int)(((o >> 5) << 4) | (((o >> 3) & 3) << 2) | (o & 3));
+}
+
+template <int NJ>
+__global__ void __launch_bounds__(256, 1) lce_stats_kernel(LceArgs a) {
+    using G = FastGemm<NJ>;
+    __shared__ __attribute__((aligned(16))) unsigned char lds[kAsmStages * G::kStage];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 5, ln = lane & 31;
+    const int wm = (wave >> 1) * 128, wn = (wave & 1) * 32 * NJ;
+    int m0, n0, nt;
+    gemm_tile(blockIdx.x, (a.M + 255) / 256, a.V / G::kTN, m0, n0, nt);
+    n0 = nt * G::kTN;
+    f32x16 acc[4 * NJ];
+    fast_tile_product<NJ>(a.X, a.ldx, a.E, a.K, a.K, m0, n0, a.M - 1 - m0, lds, wave, lane, acc);
+
+    float2* red = reinterpret_cast<float2*>(lds);  // [wave][128 rows] (the stages are free)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = m0 + wm + 32 * i + ln;
+        // the rounded maximum is the maximum of the rounded logits (rounding is monotonic)
+        float m = acc[i][0];
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) m = fmaxf(m, acc[4 * j + i][e]);
+        m = bf16_to_f32(f32_to_bf16(m));
+        m = lce_pair_max(m);
+        const float ml = m * kLog2e;
+        float s4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; e += 2) {
+                float x = acc[4 * j + i][e], y = acc[4 * j + i][e + 1];
+                round2(x, y);
+                s4[e & 3] += exp2_fast(fmaf(x, kLog2e, -ml));
+                s4[(e + 1) & 3] += exp2_fast(fmaf(y, kLog2e, -ml));
+            }
+        const float s = lce_pair_sum((s4[0] + s4[1]) + (s4[2] + s4[3]));
+        if (g == 0) red[wave * 128 + 32 * i + ln] = make_float2(m, s);
+        // the target's logit, from the lane that holds it
+        const int64_t t = row < a.M ? a.target[row] : -1;
+        const bool valid = t != a.ignore_index && t >= 0 && t < a.V;
+        const int k = valid ? lce_target_slot<NJ>(t, (int64_t)n0 + wn, g) : -1;
+        if (__builtin_amdgcn_ballot_w64(k >= 0)) {
+            float xv = 0.f;
+#pragma unroll
+            for (int j = 0; j < NJ; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+                    if (k == 16 * j + e) xv = acc[4 * j + i][e];
+            if (k >= 0) a.xt[row] = bf16_to_f32(f32_to_bf16(xv));
+        }
+    }
+    __syncthreads();
+    // thread r: tile row r, the pairs of its two waves merged (left columns first)
+    const int r = tid, wp = (r >> 7) * 2;
+    float m = red[wp * 128 + (r & 127)].x, s = red[wp * 128 + (r & 127)].y;
+    const float2 o = red[(wp + 1) * 128 + (r & 127)];
+    lce_merge(m, s, o.x, o.y);
+    if (m0 + r < a.M) a.part[(int64_t)nt * a.M + m0 + r] = make_float2(m, s);
+}
+
+// One workgroup per 16 rows: thread (slice, row) merges the pairs of tiles slice,
+// slice + 16, ... in order, then the 16 slices merge in order: a fixed summation order.
+__global__ void __launch_bounds__(256) lce_combine_kernel(LceArgs a, int ntiles, float* row_loss) {
+    __shared__ float2 sh[16][16];
+    const int rr = threadIdx.x & 15, slice = threadIdx.x >> 4;
+    const int row = blockIdx.x * 16 + rr;
+    float m = -__builtin_huge_valf(), s = 0.f;
+    if (row < a.M) {
+        int p = slice;
+        for (; p + 48 < ntiles; p += 64) {  // four loads in flight
+            const float2 v0 = a.part[(int64_t)p * a.M + row], v1 = a.part[(int64_t)(p + 16) * a.M + row];
+            const float2 v2 = a.part[(int64_t)(p + 32) * a.M + row], v3 = a.part[(int64_t)(p + 48) * a.M + row];
+            lce_merge(m, s, v0.x, v0.y);
+            lce_merge(m, s, v1.x, v1.y);
+            lce_merge(m, s, v2.x, v2.y);
+            lce_merge(m, s, v3.x, v3.y);
+        }
+        for (; p < ntiles; p += 16) {
+            const float2 v = a.part[(int64_t)p * a.M + row];
+            lce_merge(m, s, v.x, v.y);
+        }
+    }
+    sh[slice][rr] = make_float2(m, s);
+    __syncthreads();
+    if (slice == 0 && row < a.M) {
+#pragma unroll
+        for (int k = 1; k < 16; ++k) lce_merge(m, s, sh[k][rr].x, sh[k][rr].y);
+        const int64_t t = a.target[row];
+        const bool valid = t != a.ignore_index && t >= 0 && t < a.V;
+        a.stat[row] = make_float2(m, s);
+        row_loss[row] = valid ? m + logf(s) - a.xt[row] : 0.f;
+    }
+}
+
+template <int NJ>
+__global__ void __launch_bounds__(256, 1) lce_grad_kernel(LceArgs a) {
+    using G = FastGemm<NJ>;
+    __shared__ __attribute__((aligned(16))) unsigned char lds[kAsmStages * G::kStage];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 5, ln = lane & 31;
+    const int wm = (wave >> 1) * 128, wn = (wave & 1) * 32 * NJ;
+    int m0, n0, nt;
+    gemm_tile(blockIdx.x, (a.M + 255) / 256, a.V / G::kTN, m0, n0, nt);
+    n0 = nt * G::kTN;
+    f32x16 acc[4 * NJ];
+    fast_tile_product<NJ>(a.X, a.ldx, a.E, a.K, a.K, m0, n0, a.M - 1 - m0, lds, wave, lane, acc);
+
+    uint16_t* stg = reinterpret_cast<uint16_t*>(lds + wave * G::kWaveLds);
+    const float mul = *a.mul;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int64_t row0 = m0 + wm + 32 * i;
+        const int row = (int)row0 + ln;
+        const int64_t t = row < a.M ? a.target[row] : -1;
+        const bool valid = t != a.ignore_index && t >= 0 && t < a.V;
+        const float2 st = valid ? a.stat[row] : make_float2(0.f, 1.f);
+        // ignored rows: exp2(-inf) = 0 everywhere and no target column
+        const float ml = valid ? st.x * kLog2e : __builtin_huge_valf();
+        const float sc = valid ? mul / st.y : 0.f;
+        const int k = valid ? lce_target_slot<NJ>(t, (int64_t)n0 + wn, g) : -1;
+        ct_store_block<NJ>(stg, lane, i, a.dl, a.ldd, row0, n0 + wn, acc,
+                           [&](int j, int q, const float (&v)[4], float (&o)[4]) {
+                               float x[4] = {v[0], v[1], v[2], v[3]};
+                               round2(x[0], x[1]);
+                               round2(x[2], x[3]);
+#pragma unroll
+                               for (int e = 0; e < 4; ++e) {
+                                   o[e] = exp2_fast(fmaf(x[e], kLog2e, -ml)) * sc;
+                                   if (k == 16 * j + 4 * q + e) o[e] -= mul;
+                               }
+                           },
+                           (int)min<int64_t>(32, a.M - row0));
     }
 }
 
@@ -1325,4 +1545,91 @@ extern "C" int fx_gelu_bwd(const uint16_t* dy, const uint16_t* h, uint16_t* dh, 
     if (blocks < 1) blocks = 1;
     hipLaunchKernelGGL(gelu_bwd_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, dy, h, dh, n);
     return check_launch("gelu_bwd");
+}
+
+// ---------------------------------------------------------------------------
+// fused linear cross-entropy
+
+// the tile width (64-column units) of the linear-CE kernels for V columns, or 0 when the
+// shape is not theirs (V a multiple of 256 or 192, K % 32 == 0, K >= 128)
+static int lce_nj(int64_t M, int64_t V, int64_t K) {
+    if (M < 1 || V < 1 || K % 32 || K < 32 * kAsmStages) return 0;
+    if (M >= 0x7fffffffLL || V >= 0x7fffffffLL || K >= 0x7fffffffLL) return 0;
+    const int64_t cus = device_cus();
+    int64_t best = 0, nj = 0;
+    for (int w : {4, 3}) {
+        if (V % (64 * w)) continue;
+        const int64_t tiles = ((M + 255) / 256) * (V / (64 * w));
+        if (tiles >= 0x7fffffffLL) continue;
+        const int64_t cost = (tiles + cus - 1) / cus * w;
+        if (nj == 0 || cost < best) best = cost, nj = w;
+    }
+    return (int)nj;
+}
+
+static int64_t lce_part_bytes(int64_t M, int64_t V, int nj) { return ((V / (64 * nj)) * M * 8 + 255) / 256 * 256; }
+
+extern "C" int64_t fx_lce_workspace(int64_t M, int64_t V, int64_t K) {
+    const int nj = lce_nj(M, V, K);
+    return nj ? lce_part_bytes(M, V, nj) + (M * 4 + 255) / 256 * 256 : 0;
+}
+
+static int lce_check(const char* fn, const uint16_t* X, int64_t ldx, const uint16_t* E, const int64_t* target,
+                     int64_t M, int64_t V, int64_t K, int& nj) {
+    FX_REQUIRE(X && E && target, "%s: null pointer", fn);
+    FX_REQUIRE(M >= 0 && V >= 1 && K >= 1, "%s: bad shape M=%lld V=%lld K=%lld", fn, (long long)M, (long long)V,
+               (long long)K);
+    nj = M == 0 ? 0 : lce_nj(M, V, K);
+    FX_REQUIRE(M == 0 || nj != 0,
+               "%s: V %% 256 or %% 192 == 0, K %% 32 == 0 and K >= 128 only: M=%lld V=%lld K=%lld", fn, (long long)M,
+               (long long)V, (long long)K);
+    FX_REQUIRE(ldx >= K && ldx % 8 == 0, "%s: ldx=%lld", fn, (long long)ldx);
+    FX_REQUIRE(((((uintptr_t)X) | ((uintptr_t)E)) & 15) == 0, "%s: X and E must be 16-byte aligned", fn);
+    return 0;
+}
+
+extern "C" int fx_lce_fwd(const uint16_t* X, int64_t ldx, const uint16_t* E, const int64_t* target,
+                          int64_t ignore_index, void* work, float* stat, float* row_loss, int64_t M, int64_t V,
+                          int64_t K, void* stream) {
+    int nj;
+    if (int e = lce_check("fx_lce_fwd", X, ldx, E, target, M, V, K, nj)) return e;
+    if (M == 0) return 0;
+    FX_REQUIRE(work && stat && row_loss, "fx_lce_fwd: null workspace or output");
+    FX_REQUIRE(((((uintptr_t)work) | ((uintptr_t)stat)) & 15) == 0, "fx_lce_fwd: work and stat must be 16-byte aligned");
+    LceArgs a{};
+    a.X = X, a.ldx = ldx, a.E = E, a.target = target, a.ignore_index = ignore_index;
+    a.part = reinterpret_cast<float2*>(work);
+    a.xt = reinterpret_cast<float*>((char*)work + lce_part_bytes(M, V, nj));
+    a.stat = reinterpret_cast<float2*>(stat);
+    a.M = (int)M, a.V = (int)V, a.K = (int)K;
+    const int ntiles = (int)(V / (64 * nj));
+    const unsigned tiles = (unsigned)(((M + 255) / 256) * ntiles);
+    hipStream_t s = (hipStream_t)stream;
+    if (nj == 4) hipLaunchKernelGGL(lce_stats_kernel<4>, dim3(tiles), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(lce_stats_kernel<3>, dim3(tiles), dim3(256), 0, s, a);
+    if (int e = check_launch("lce_stats")) return e;
+    hipLaunchKernelGGL(lce_combine_kernel, dim3((unsigned)((M + 15) / 16)), dim3(256), 0, s, a, ntiles, row_loss);
+    return check_launch("lce_combine");
+}
+
+extern "C" int fx_lce_grad(const uint16_t* X, int64_t ldx, const uint16_t* E, const int64_t* target,
+                           int64_t ignore_index, const float* stat, const float* mul, uint16_t* dl, int64_t ldd,
+                           int64_t M, int64_t V, int64_t K, void* stream) {
+    int nj;
+    if (int e = lce_check("fx_lce_grad", X, ldx, E, target, M, V, K, nj)) return e;
+    if (M == 0) return 0;
+    FX_REQUIRE(stat && mul && dl, "fx_lce_grad: null stat, mul or dl");
+    FX_REQUIRE(ldd >= V && ldd % 8 == 0 && ((uintptr_t)dl & 15) == 0 && ((uintptr_t)stat & 7) == 0,
+               "fx_lce_grad: dl needs a row stride >= V, a multiple of 8, and 16-byte alignment (ldd=%lld)",
+               (long long)ldd);
+    LceArgs a{};
+    a.X = X, a.ldx = ldx, a.E = E, a.target = target, a.ignore_index = ignore_index;
+    a.stat = const_cast<float2*>(reinterpret_cast<const float2*>(stat));
+    a.mul = mul, a.dl = dl, a.ldd = ldd;
+    a.M = (int)M, a.V = (int)V, a.K = (int)K;
+    const unsigned tiles = (unsigned)(((M + 255) / 256) * (V / (64 * nj)));
+    hipStream_t s = (hipStream_t)stream;
+    if (nj == 4) hipLaunchKernelGGL(lce_grad_kernel<4>, dim3(tiles), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(lce_grad_kernel<3>, dim3(tiles), dim3(256), 0, s, a);
+    return check_launch("lce_grad");
 }

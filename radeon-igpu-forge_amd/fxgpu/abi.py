@@ -133,6 +133,10 @@ SIGNATURES = {
     "fx_linear_wgrad_workspace": (c_int64, [c_int64, c_int64, c_int64]),
     "fx_linear_wgrad": (c_int32, [_P, c_int64, _P, c_int64, _P, c_int64, _P, c_int64, c_int64, c_int64,
                                   _P]),
+    "fx_lce_workspace": (c_int64, [c_int64, c_int64, c_int64]),
+    "fx_lce_fwd": (c_int32, [_P, c_int64, _P, _P, c_int64, _P, _P, _P, c_int64, c_int64, c_int64, _P]),
+    "fx_lce_grad": (c_int32, [_P, c_int64, _P, _P, c_int64, _P, _P, _P, c_int64, c_int64, c_int64, c_int64,
+                              _P]),
 }
 
 _LIB = None

@@ -8,7 +8,12 @@ Surface of ml/fxlm/cross_entropy.py:41-199 with bf16 logits:
   incoming gradient only when it is not 1.
 * ``linear_cross_entropy(x, weight, target, grad_scale=1.0, ...)``: CE(x W^T)
   whose backward is computed inside the forward, chunk by chunk; each chunk's
-  logits are overwritten in place by their gradient.
+  logits are overwritten in place by their gradient.  Heads whose shape the fused
+  kernels take (V % 256 or % 192 == 0, D % 32 == 0, D >= 128) can instead form the
+  logits only in MFMA accumulators (fx_lce_fwd: the GEMM with the online
+  (max, sum exp) reduction in its epilogue, then fx_lce_grad: the GEMM again with the
+  dlogits in its epilogue): always for the loss-only path (FUSED_LINEAR_CE_LOSS), and
+  for training with FUSED_LINEAR_CE_TRAIN.
 
 n_valid counts targets != ignore_index (out-of-range targets count, but their
 rows get no loss and no gradient); n_valid == 0 gives loss 0 (reference
@@ -18,7 +23,7 @@ import ctypes
 
 import torch
 
-from fxgpu.abi import call, fxCEArgs, ptr, stream_of
+from fxgpu.abi import call, fxCEArgs, lib, ptr, stream_of
 
 # rows per linear-CE chunk: bound the chunk's bf16 logits to this many bytes
 _CHUNK_BYTES = 2 << 30
@@ -61,6 +66,46 @@ def _finalize(row_loss, inv_n):
     call("fx_ce_loss_finalize", ptr(row_loss), row_loss.numel(), ptr(inv_n), ptr(loss),
          stream_of(row_loss))
     return loss
+
+
+# Fused linear-CE head (fx_lce_fwd / fx_lce_grad), where fx_lce_workspace takes the shape.
+# FUSED_LINEAR_CE_LOSS: the no-grad (loss-only) path, which then allocates no logits at all.
+# FUSED_LINEAR_CE_TRAIN: the training path; its chunk still holds the bf16 dlogits (the
+# dx / dW products read them), and the logits GEMM runs twice (loss pass, gradient pass)
+# where the unfused loop runs it once and streams the stored logits through
+# fx_ce_fwd_grad, so on MI355X it is the slower of the two at the cfg5 head.
+FUSED_LINEAR_CE_LOSS = True
+FUSED_LINEAR_CE_TRAIN = False
+
+
+def _lce_fused_ok(x, weight):
+    """True when the fused linear-CE kernels take x (N, D) and weight (V, D)."""
+    N, D = x.shape
+    V = weight.shape[0]
+    return (x.is_cuda and N > 0 and x.stride(1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0
+            and weight.is_contiguous() and weight.data_ptr() % 16 == 0
+            and int(lib().fx_lce_workspace(N, V, D)) > 0)
+
+
+def _lce_fwd(xc, weight, tc, ignore_index, row_loss):
+    """Loss pass of the fused head over the rows of xc: row_loss, and the per-row
+    (max, sum exp) pairs the gradient pass needs, as a (C, 2) fp32 tensor."""
+    C, D = xc.shape
+    V = weight.shape[0]
+    nbytes = int(lib().fx_lce_workspace(C, V, D))
+    work = torch.empty((nbytes + 3) // 4, device=xc.device, dtype=torch.float32)
+    stat = torch.empty(C, 2, device=xc.device, dtype=torch.float32)
+    call("fx_lce_fwd", ptr(xc), xc.stride(0), ptr(weight), ptr(tc), int(ignore_index), ptr(work), ptr(stat),
+         ptr(row_loss), C, V, D, stream_of(xc))
+    return stat
+
+
+def _lce_grad(xc, weight, tc, ignore_index, stat, mul, dl):
+    """Gradient pass of the fused head: dl (C, V) bf16 = the chunk's dlogits times mul."""
+    C, D = xc.shape
+    V = weight.shape[0]
+    call("fx_lce_grad", ptr(xc), xc.stride(0), ptr(weight), ptr(tc), int(ignore_index), ptr(stat), ptr(mul),
+         ptr(dl), dl.stride(0), C, V, D, stream_of(xc))
 
 
 def _check_logits(logits, target):
@@ -152,11 +197,18 @@ class _LinearCE(torch.autograd.Function):
         row_loss = torch.empty(N, device=dev, dtype=torch.float32)
         dx = torch.empty(N, D, device=dev, dtype=torch.bfloat16)
         dW = None
+        fused = FUSED_LINEAR_CE_TRAIN and _lce_fused_ok(x, weight)
+        dl_buf = torch.empty(min(chunk_rows, N), V, device=dev, dtype=torch.bfloat16) if fused else None
         for r0 in range(0, N, chunk_rows):
             r1 = min(r0 + chunk_rows, N)
             xc = x[r0:r1]
-            lg = torch.mm(xc, weight.t())                       # (C, V) bf16
-            _ce_rows(lg, target[r0:r1], lg, row_loss[r0:r1], mul, ignore_index)  # in place
+            if fused:   # the logits only in MFMA accumulators: loss pass, then gradient pass
+                stat = _lce_fwd(xc, weight, target[r0:r1], ignore_index, row_loss[r0:r1])
+                lg = dl_buf[:r1 - r0]
+                _lce_grad(xc, weight, target[r0:r1], ignore_index, stat, mul, lg)
+            else:
+                lg = torch.mm(xc, weight.t())                   # (C, V) bf16
+                _ce_rows(lg, target[r0:r1], lg, row_loss[r0:r1], mul, ignore_index)  # in place
             torch.mm(lg, weight, out=dx[r0:r1])                 # dx_c
             # the reference's dW.add_(torch.mm(dl.t(), xc).float()): a bf16 product,
             # accumulated over the chunks in fp32 (ml/fxlm/cross_entropy.py:135); a single
@@ -218,6 +270,10 @@ def _linear_ce_loss_only(x, weight, target, ignore_index, chunk_rows):
         chunk_rows = _auto_chunk(D, V)
     inv_n, _mul = _inv_nvalid(target, ignore_index)
     row_loss = torch.empty(N, device=x.device, dtype=torch.float32)
+    if FUSED_LINEAR_CE_LOSS and _lce_fused_ok(x, weight):
+        # one pass over all rows: the workspace is a (max, sum) pair per row and column tile
+        _lce_fwd(x, weight, target, ignore_index, row_loss)
+        return _finalize(row_loss, inv_n)
     for r0 in range(0, N, chunk_rows):
         r1 = min(r0 + chunk_rows, N)
         lg = torch.mm(x[r0:r1], weight.t())

@@ -118,6 +118,29 @@ def test_rms_norm_rejects_misaligned_vectors(abi):
         assert lib.fx_rms_norm_bwd_add(x, dy, ok, w, ok, dx, ok, ok, ok, 4, 64, None) == abi.FX_EINVAL
 
 
+def test_lce_workspace_and_checks(abi):
+    # the fused linear-CE kernels take V % 256 or % 192 == 0, K % 32 == 0, K >= 128; the
+    # workspace is one (max, sum) fp32 pair per row and column tile plus one fp32 per row
+    lib = abi.lib()
+    assert lib.fx_lce_workspace(16384, 50304, 768) == 262 * 16384 * 8 + 16384 * 4
+    assert lib.fx_lce_workspace(300, 1024, 128) == ((4 * 300 * 8 + 255) // 256 * 256
+                                                    + (300 * 4 + 255) // 256 * 256)
+    for M, V, K in ((100, 1000, 128), (100, 768, 96), (100, 768, 100), (0, 768, 128)):
+        assert lib.fx_lce_workspace(M, V, K) == 0
+    fake = ctypes.c_void_p(4096)     # never dereferenced: the checks fail first
+    odd = ctypes.c_void_p(4096 + 2)
+    assert lib.fx_lce_fwd(fake, 128, fake, fake, -100, fake, fake, fake, 8, 1000, 128, None) == abi.FX_EINVAL
+    assert b"V % 256" in lib.fx_last_error()
+    assert lib.fx_lce_fwd(odd, 128, fake, fake, -100, fake, fake, fake, 8, 768, 128, None) == abi.FX_EINVAL
+    assert b"16-byte aligned" in lib.fx_last_error()
+    assert lib.fx_lce_fwd(None, 128, fake, fake, -100, fake, fake, fake, 8, 768, 128, None) == abi.FX_EINVAL
+    assert lib.fx_lce_grad(fake, 128, fake, fake, -100, fake, fake, fake, 700, 8, 768, 128, None) == abi.FX_EINVAL
+    assert b"row stride" in lib.fx_last_error()
+    assert lib.fx_lce_grad(fake, 120, fake, fake, -100, fake, fake, fake, 768, 8, 768, 128, None) == abi.FX_EINVAL
+    # an empty batch launches nothing
+    assert lib.fx_lce_fwd(fake, 128, fake, fake, -100, None, None, None, 0, 768, 128, None) == 0
+
+
 def test_adamw_workspace_counts_chunks(abi):
     tl = abi.fxTensorList()
     tl.count = 3
