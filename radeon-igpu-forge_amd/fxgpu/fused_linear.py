@@ -89,6 +89,9 @@ def whole_tiles(M, N, K):
 # NATIVE_PROJ_FWD: the whole_tiles() forwards on fx_linear_fwd.  False: the library GEMM.
 NATIVE_INPUT_GRAD = False
 NATIVE_PROJ_FWD = False
+# NATIVE_GELU_INPUT_GRAD: only the input gradient with the GELU derivative folded in (the
+# GPT MLP's fc2, where fx_linear_dgrad also saves fx_gelu_bwd's pass over three tensors)
+NATIVE_GELU_INPUT_GRAD = False
 
 
 def dgrad_tiles(M, N, K):
@@ -106,7 +109,8 @@ def input_grad(dy2, weight, h=None):
     torch.mm, then fx_gelu_bwd for h."""
     M, K = dy2.shape
     N = weight.shape[1]
-    native = (NATIVE_INPUT_GRAD and dy2.is_cuda and dgrad_tiles(M, N, K) and (h is not None or N <= 1024)
+    wanted = (NATIVE_INPUT_GRAD and (h is not None or N <= 1024)) or (NATIVE_GELU_INPUT_GRAD and h is not None)
+    native = (wanted and dy2.is_cuda and dgrad_tiles(M, N, K)
               and weight.is_contiguous() and weight.data_ptr() % 16 == 0
               and dy2.stride(1) == 1 and dy2.stride(0) % 8 == 0 and dy2.data_ptr() % 16 == 0
               and (h is None or (h.is_contiguous() and h.data_ptr() % 16 == 0)))
