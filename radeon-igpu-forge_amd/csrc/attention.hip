@@ -343,25 +343,33 @@ __global__ void __launch_bounds__(kAttThreads) attn_fwd_kernel(fxAttnArgs a) {
             mloc = pair_max(mloc);
             const float m_new = fmaxf(m_run, mloc * sl2);
             const bool need = m_new > m_run + kLazyRescale;
+            // wave-uniform: the rescale (its exp, the l and O multiplies) only runs in the
+            // rare tiles where some row's max moved
+            const bool any_need = __ballot(need) != 0;
             float alpha = 1.f;
-            if (need) {
+            if (any_need && need) {
                 alpha = exp2_fast(m_run - m_new);
                 m_run = m_new;
             }
             const float mu = (m_run == kNegInfA) ? 0.f : m_run;
-            float r4[4] = {0.f, 0.f, 0.f, 0.f};
+            // row sum in four partial sums, each started from its first term (no adds of 0)
+            float r4[4];
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const float p = exp2_fast(fmaf(sc[i], sl2, -mu));
                 sc[i] = p;
-                r4[i & 3] += p;
+                if (i < 4) r4[i] = p;
+                else r4[i & 3] += p;
             }
-            l_run = l_run * alpha + ((r4[0] + r4[1]) + (r4[2] + r4[3]));
-            if (__ballot(need)) {
+            const float rs = (r4[0] + r4[1]) + (r4[2] + r4[3]);
+            if (any_need) {
+                l_run = l_run * alpha + rs;
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
                     for (int i = 0; i < 16; ++i) acc[dt][i] *= alpha;
+            } else {
+                l_run += rs;
             }
             const bf16x8 p0 = pack_op(sc, 0), p1 = pack_op(sc, 1);
 #pragma unroll
