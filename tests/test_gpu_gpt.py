@@ -127,6 +127,15 @@ def _parity_vs_oracle(dev, V, T, L, H, D, B, seed):
         assert bool(torch.isfinite(p.grad).all()), name
         ok, e, et = _rule_ok(p.grad, rp[name].grad, tp[name].grad)
         assert ok, (name, e, et)
+    # the evaluation loss (no grad): the loss-only linear-CE path, on the fused head kernels
+    # at these shapes, under the same rule and next to the training path's loss
+    from fxlm.cross_entropy import _lce_fused_ok
+    assert _lce_fused_ok(torch.empty(8, D, device=dev, dtype=torch.bfloat16), m_f.tok_emb.weight)
+    with torch.no_grad():
+        l_e = m_f(idx.to(dev), tgt.to(dev))
+    ok, e, et = _rule_ok(l_e, l_r.detach(), l_t.detach())
+    assert ok, ("eval loss", e, et)
+    assert abs(float(l_e) - float(l_f)) <= 1e-4 * abs(float(l_f))
 
 
 def test_cfg1_gpt_vs_oracle(dev):
