@@ -1,7 +1,7 @@
 """Benchmark: the fxlm GPT 12L-d768 training step on one MI355X, plus the hot-path kernels.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-    python bench.py --only {attention,ce,norm,adamw,linear,wgrad,head,step,copy,decode,cpu,fc-ours,fc-library,
+    python bench.py --only {attention,ce,norm,adamw,linear,wgrad,head,library,step,copy,decode,cpu,fc-ours,fc-library,
                             fc-ours-cold,fc-library-cold}   (profiling runs)
     python bench.py --counter-table p_counter_collection.csv [...]   (per-kernel counter table)
     python bench.py --traffic-table FETCH.csv WRITE.csv COPY_FETCH.csv COPY_WRITE.csv
@@ -24,6 +24,9 @@ are launched on (torch's current stream):
   fused linear + GELU: the cfg5 MLP fc (16384 x 768 x 3072)
   weight gradients: the four cfg5 dW = dy^T x products over 16384 tokens
   linear-CE head: the cfg5 tied head, unfused chunk loop against the fused kernels
+  library comparisons: attention, CE, RMSNorm and the optimizer step next to SDPA,
+    F.cross_entropy, F.rms_norm and fused torch AdamW at the same shapes (each kernel
+    line's "library" entry)
 and, on the host CPU, the reference's naive-PyTorch fp32 training step
 (oracle/gpt.py) on a bounded sample.  Prints ONE JSON line.
 """
@@ -193,6 +196,141 @@ def bench_adamw(torch):
     del opt, m
     return {"params": n, "step_us": round(t, 2), "gbs": round(nbytes / t / 1e3, 1),
             "frac_of_hbm": round(nbytes / t / 1e3 / HBM_PEAK_GBS, 4), "bytes": nbytes}
+
+
+def bench_library(torch):
+    """Each bandwidth / attention op next to its PyTorch equivalent at the same shape, as the
+    reference's microbench compares them (ml/fxlm/bench_kernels.py:49-190): flash attention
+    against scaled_dot_product_attention, fused CE against F.cross_entropy (on fp32 logits, as
+    the reference times it, and on the bf16 logits), RMSNorm against F.rms_norm, and the
+    FlatAdamW step against GradScaler unscale + clip_grad_norm_ + fused torch AdamW.  Both
+    sides go through autograd where the reference's do (fwd + bwd).  SDPA runs on its flash or
+    memory-efficient backend only: its math backend is never timed here (its bf16 batched
+    products take transposed operands, which this GPU's library path is not trusted with)."""
+    import torch.nn.functional as Fn
+
+    from fxlm.attention import flash_attention
+    from fxlm.cross_entropy import fused_cross_entropy
+    from fxlm.norm import rms_norm
+    out = {}
+    g = torch.Generator(device="cuda").manual_seed(6)
+
+    # attention, cfg2: this build's autograd op against SDPA (B, H, T, D) on the same values
+    B, T, H, D = 16, 1024, 12, 64
+    q, k, v, do = (torch.randn(B, T, H, D, device="cuda", generator=g).bfloat16() for _ in range(4))
+    qa, ka, va = (t.clone().requires_grad_() for t in (q, k, v))
+
+    def ours_fwd():
+        with torch.no_grad():
+            flash_attention(qa, ka, va, causal=True)
+
+    def ours_fb():
+        flash_attention(qa, ka, va, causal=True).backward(do)
+        qa.grad = ka.grad = va.grad = None
+    att = {"ours_fwd_us": round(time_us(torch, ours_fwd), 2), "ours_fwdbwd_us": round(time_us(torch, ours_fb), 2)}
+    qs, ks, vs = (t.transpose(1, 2).contiguous().requires_grad_() for t in (q, k, v))
+    dos = do.transpose(1, 2).contiguous()
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    err = None
+    for be, name in ((SDPBackend.FLASH_ATTENTION, "flash"), (SDPBackend.EFFICIENT_ATTENTION, "efficient")):
+        try:
+            with sdpa_kernel([be]):
+                def s_fwd():
+                    with torch.no_grad():
+                        Fn.scaled_dot_product_attention(qs, ks, vs, is_causal=True)
+
+                def s_fb():
+                    Fn.scaled_dot_product_attention(qs, ks, vs, is_causal=True).backward(dos)
+                    qs.grad = ks.grad = vs.grad = None
+                s_fb()
+                torch.cuda.synchronize()
+                att.update({"sdpa_backend": name, "sdpa_fwd_us": round(time_us(torch, s_fwd), 2),
+                            "sdpa_fwdbwd_us": round(time_us(torch, s_fb), 2)})
+            err = None
+            break
+        except RuntimeError as e:
+            err = str(e).splitlines()[0][:160]
+    if err:
+        att["sdpa_error"] = err
+    elif "sdpa_fwd_us" in att:
+        att["speedup_fwd"] = round(att["sdpa_fwd_us"] / att["ours_fwd_us"], 2)
+        att["speedup_fwdbwd"] = round(att["sdpa_fwdbwd_us"] / att["ours_fwdbwd_us"], 2)
+    out["attention_cfg2"] = att
+    del q, k, v, do, qa, ka, va, qs, ks, vs, dos
+
+    # cross-entropy, cfg3
+    N, V = 16384, 50304
+    lg = (torch.randn(N, V, device="cuda", generator=g) * 2).bfloat16().requires_grad_()
+    tg = torch.randint(0, V, (N,), device="cuda", generator=g)
+    tg[torch.rand(N, device="cuda", generator=g) < 0.05] = -100
+
+    def ce_ours():
+        fused_cross_entropy(lg, tg).backward()
+        lg.grad = None
+
+    def ce_f32():
+        Fn.cross_entropy(lg.float(), tg, ignore_index=-100).backward()
+        lg.grad = None
+
+    def ce_bf16():
+        Fn.cross_entropy(lg, tg, ignore_index=-100).backward()
+        lg.grad = None
+    ce = {"ours_fwdbwd_us": round(time_us(torch, ce_ours, iters=10, warm=3), 1),
+          "torch_fp32_fwdbwd_us": round(time_us(torch, ce_f32, iters=10, warm=3), 1),
+          "torch_bf16_fwdbwd_us": round(time_us(torch, ce_bf16, iters=10, warm=3), 1)}
+    ce["speedup_vs_fp32"] = round(ce["torch_fp32_fwdbwd_us"] / ce["ours_fwdbwd_us"], 2)
+    ce["speedup_vs_bf16"] = round(ce["torch_bf16_fwdbwd_us"] / ce["ours_fwdbwd_us"], 2)
+    out["cross_entropy_cfg3"] = ce
+    del lg, tg
+    torch.cuda.empty_cache()
+
+    # RMSNorm, cfg4
+    N, D = 65536, 768
+    x = torch.randn(N, D, device="cuda", generator=g).bfloat16().requires_grad_()
+    w = (torch.randn(D, device="cuda", generator=g) * 0.1 + 1).bfloat16().requires_grad_()
+    dy = torch.randn(N, D, device="cuda", generator=g).bfloat16()
+
+    def n_ours_f():
+        with torch.no_grad():
+            rms_norm(x, w, 1e-6)
+
+    def n_ours_fb():
+        rms_norm(x, w, 1e-6).backward(dy)
+        x.grad = w.grad = None
+
+    def n_t_f():
+        with torch.no_grad():
+            Fn.rms_norm(x, (D,), w, 1e-6)
+
+    def n_t_fb():
+        Fn.rms_norm(x, (D,), w, 1e-6).backward(dy)
+        x.grad = w.grad = None
+    nm = {"ours_fwd_us": round(time_us(torch, n_ours_f), 2), "ours_fwdbwd_us": round(time_us(torch, n_ours_fb), 2),
+          "torch_fwd_us": round(time_us(torch, n_t_f), 2), "torch_fwdbwd_us": round(time_us(torch, n_t_fb), 2)}
+    nm["speedup_fwd"] = round(nm["torch_fwd_us"] / nm["ours_fwd_us"], 2)
+    nm["speedup_fwdbwd"] = round(nm["torch_fwdbwd_us"] / nm["ours_fwdbwd_us"], 2)
+    out["rmsnorm_cfg4"] = nm
+    del x, w, dy
+
+    # optimizer, cfg4 size: the reference's torch comparator (fp32 params and gradients,
+    # GradScaler unscale, clip to 1.0, fused AdamW, scaler update)
+    n = 124373760
+    p = torch.nn.Parameter(torch.empty(n // 768, 768, device="cuda").normal_(0, 0.02, generator=g))
+    p.grad = torch.randn(n // 768, 768, device="cuda", generator=g) * 1e-3
+    opt2 = torch.optim.AdamW([p], lr=6e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, fused=True)
+    scaler = torch.amp.GradScaler("cuda", init_scale=1.0)
+    dummy = torch.ones((), device="cuda")
+
+    def t_step():
+        scaler.scale(dummy)
+        scaler.unscale_(opt2)
+        torch.nn.utils.clip_grad_norm_([p], 1.0)
+        scaler.step(opt2)
+        scaler.update()
+    out["flat_adamw_cfg4"] = {"torch_fused_adamw_clip_scaler_us": round(time_us(torch, t_step, iters=10, warm=3), 1)}
+    del p, opt2, scaler
+    torch.cuda.empty_cache()
+    return out
 
 
 def bench_linear(torch):
@@ -629,7 +767,7 @@ def main():
     # counts, so a batch's first step can allocate; 42 ms once when it fell in the timed steps)
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU baseline")
-    ap.add_argument("--only", choices=["attention", "ce", "norm", "adamw", "linear", "wgrad", "head", "step", "copy",
+    ap.add_argument("--only", choices=["attention", "ce", "norm", "adamw", "linear", "wgrad", "head", "library", "step", "copy",
                                        "decode",
                                        "cpu", "fc-ours", "fc-library", "fc-ours-cold", "fc-library-cold"],
                     help="run one workload and print its figures (for profiling runs)")
@@ -664,6 +802,7 @@ def main():
     if args.only:
         fn = {"attention": bench_attention, "ce": bench_ce, "norm": bench_norm, "adamw": bench_adamw,
               "linear": bench_linear, "wgrad": bench_wgrad, "head": bench_head, "copy": bench_copy,
+              "library": bench_library,
               "decode": bench_decode,
               "cpu": cpu_baseline,
               "step": lambda t: gpu_step_bench(t, args.steps, args.warmup),
@@ -683,6 +822,13 @@ def main():
     wg = bench_wgrad(torch)
     head = bench_head(torch)
     torch.cuda.empty_cache()
+    libs = bench_library(torch)
+    attn["library"] = libs["attention_cfg2"]
+    ce["library"] = libs["cross_entropy_cfg3"]
+    norm["library"] = libs["rmsnorm_cfg4"]
+    adamw["library"] = dict(libs["flat_adamw_cfg4"],
+                            speedup=round(libs["flat_adamw_cfg4"]["torch_fused_adamw_clip_scaler_us"]
+                                          / adamw["step_us"], 2))
     dec = bench_decode(torch)
     torch.cuda.empty_cache()
     step = gpu_step_bench(torch, args.steps, args.warmup)
