@@ -5,6 +5,7 @@
                             fc-ours-cold,fc-library-cold}   (profiling runs)
     python bench.py --counter-table p_counter_collection.csv [...]   (per-kernel counter table)
     python bench.py --traffic-table FETCH.csv WRITE.csv COPY_FETCH.csv COPY_WRITE.csv
+    python bench.py --trace-table kernel_trace.csv [ONCE_PER_STEP_KERNEL]   (kernel-trace table)
     python bench.py --pmc-summary FETCH.csv WRITE.csv COPY_FETCH.csv COPY_WRITE.csv
 
 Workload (the headline metric's fifth config): GPT with 12 layers, d_model 768, 12 heads of
@@ -711,6 +712,50 @@ def counter_table(csv_paths, top=12):
     return "\n".join(lines)
 
 
+def trace_table(trace_csv, per_step=None, skip=2, top=40):
+    """Per-kernel durations from a rocprofv3 --kernel-trace kernel_trace.csv as a markdown
+    table.  With per_step (a kernel name fragment that runs once per training step, e.g. the
+    CE row kernel), only the windows between consecutive dispatches of that kernel count,
+    after `skip` windows: each holds one step's kernels, and the table is per step, with the
+    span (first start to last end) beside the summed kernel time."""
+    import csv
+    rows = []
+    with open(trace_csv) as f:
+        for r in csv.DictReader(f):
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
+    rows.sort()
+    note = f"{len(rows)} dispatches"
+    if per_step:
+        marks = [i for i, (_, _, k) in enumerate(rows) if per_step in k]
+        wins = list(zip(marks[skip:], marks[skip + 1:]))
+        if not wins:
+            raise SystemExit(f"fewer than {skip + 2} dispatches of {per_step!r}")
+        sel = [rows[i] for a, b in wins for i in range(a, b)]
+        nwin = len(wins)
+        span = sum(rows[b][0] - rows[a][0] for a, b in wins) / nwin / 1e3
+        note = (f"{nwin} steps (windows between consecutive `{per_step}` dispatches, the first {skip} "
+                f"skipped): {sum(e - s for s, e, _ in sel) / nwin / 1e3:.1f} µs of kernels per step in a "
+                f"span of {span:.1f} µs, {len(sel) / nwin:.0f} dispatches per step")
+    else:
+        sel, nwin = rows, 1
+    agg = {}
+    for s, e, k in sel:
+        d = agg.setdefault(k, [0, 0, float("inf"), 0])
+        d[0] += 1
+        d[1] += e - s
+        d[2] = min(d[2], e - s)
+        d[3] = max(d[3], e - s)
+    total = sum(d[1] for d in agg.values())
+    unit = "per step" if per_step else "total"
+    lines = [note, "", f"| kernel | calls {unit} | avg µs | min µs | max µs | µs {unit} | % |",
+             "|---|---:|---:|---:|---:|---:|---:|"]
+    for k, (n, t, lo, hi) in sorted(agg.items(), key=lambda kv: -kv[1][1])[:top]:
+        kn = k if len(k) < 90 else k[:87] + "..."
+        lines.append(f"| `{kn}` | {n / nwin:.1f} | {t / n / 1e3:.2f} | {lo / 1e3:.2f} | {hi / 1e3:.2f} | "
+                     f"{t / nwin / 1e3:.1f} | {100 * t / total:.1f} |")
+    return "\n".join(lines)
+
+
 def traffic_table(fetch_csv, write_csv, copy_fetch_csv, copy_write_csv, top=12):
     """HBM bytes per dispatch of every kernel in a FETCH_SIZE and a WRITE_SIZE pass, each
     scaled by what the same counter reads for torch's 1 GiB copy (bench.py --only copy), as a
@@ -776,6 +821,9 @@ def main():
                     help="write the fx_attn_bwd HBM traffic from rocprofv3 --pmc csv files")
     ap.add_argument("--counter-table", nargs="+", metavar="CSV",
                     help="print per-kernel counter averages from rocprofv3 --pmc csv files")
+    ap.add_argument("--trace-table", nargs="+", metavar=("TRACE_CSV", "PER_STEP_KERNEL"),
+                    help="print per-kernel durations from a rocprofv3 --kernel-trace csv (per step when a "
+                         "once-per-step kernel name is given)")
     ap.add_argument("--traffic-table", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV",
                                                          "COPY_WRITE_CSV"),
                     help="print per-kernel HBM bytes from FETCH_SIZE / WRITE_SIZE passes")
@@ -785,6 +833,9 @@ def main():
         return
     if args.traffic_table:
         print(traffic_table(*args.traffic_table))
+        return
+    if args.trace_table:
+        print(trace_table(args.trace_table[0], args.trace_table[1] if len(args.trace_table) > 1 else None))
         return
     if args.pmc_summary:
         res = pmc_summary(*args.pmc_summary)
