@@ -336,6 +336,20 @@ int fx_linear_fwd_ex(const fxLinearArgs* args, void* stream);
  * of F.gelu(approximate="tanh"), ml/fxlm/model.py:71). */
 int fx_gelu_bwd(const uint16_t* dy, const uint16_t* h, uint16_t* dh, int64_t n, void* stream);
 
+/* Bytes of workspace fx_embedding_bwd needs for n positions and a V-row table (0 when n or V
+ * is not positive). */
+int64_t fx_embedding_bwd_workspace(int64_t n, int64_t V);
+
+/* Token-embedding gradient: grad (V, D) bf16, row-major, = for every row v the sum, in
+ * increasing t, of dy[t] over the positions t with idx[t] == v (fp32 accumulation, one bf16
+ * rounding); rows no position selects are zero and ids outside [0, V) select nothing.  idx
+ * int64 (n,), dy (n, D) with row stride ldy (16-byte aligned rows, D a multiple of 8), work of
+ * fx_embedding_bwd_workspace(n, V) bytes (16-byte aligned).  Deterministic (a stable counting
+ * sort, no atomics), with launch sizes that depend on n and V only.  Replaces torch's
+ * nn.Embedding backward behind the reference's tok_emb(idx) (ml/fxlm/model.py:82,118). */
+int fx_embedding_bwd(const int64_t* idx, int64_t n, const uint16_t* dy, int64_t ldy, uint16_t* grad, int64_t V,
+                     int64_t D, void* work, void* stream);
+
 /* Bytes of fp32 workspace fx_linear_wgrad needs for an (M, N) weight gradient over K
  * tokens (0: none; the K split depends on the device's CU count). */
 int64_t fx_linear_wgrad_workspace(int64_t M, int64_t N, int64_t K);

@@ -20,6 +20,7 @@ from fxgpu.fused_linear import FEW_ROWS, fused_linear, fused_mlp, linear, linear
 
 from .attention import decode_attention, flash_attention_qkv
 from .cross_entropy import linear_cross_entropy
+from .embedding import token_embedding
 from .norm import add_pre_norm, pre_norm, rms_norm
 
 
@@ -36,7 +37,7 @@ class GPTConfig:
     norm_impl: str = "fused"      # "fused" | "torch"
     ce_impl: str = "fused"        # "fused" | "torch"
     mlp_impl: str = "fused"       # "fused" | "torch"
-    linear_impl: str = "fused"    # qkv / proj / fc2: "fused" (split-K dW) | "torch"
+    linear_impl: str = "fused"    # qkv / proj / fc2 (split-K dW) and tok_emb's gradient: "fused" | "torch"
     eps: float = 1e-6
 
 
@@ -197,6 +198,15 @@ class GPT(nn.Module):
             return add_pre_norm(x, r, self.lnf_w, self.cfg.eps)[1]
         return self._norm_f(x + r)
 
+    def _tok(self, idx):
+        """tok_emb(idx) (ml/fxlm/model.py:118); on the fused path its weight gradient is
+        fx_embedding_bwd's (deterministic, launch sizes independent of the ids)."""
+        w = self.tok_emb.weight
+        if (self.cfg.linear_impl == "fused" and idx.is_cuda and w.dtype == torch.bfloat16
+                and w.shape[1] % 8 == 0):
+            return token_embedding(idx, w)
+        return self.tok_emb(idx)
+
     def _head_w(self):
         return self.tok_emb.weight if self.cfg.tie_embeddings else self.head.weight
 
@@ -207,7 +217,7 @@ class GPT(nn.Module):
         B, T = idx.shape
         if T > self.cfg.seq_len:
             raise ValueError(f"T={T} > seq_len={self.cfg.seq_len}")
-        x = self.tok_emb(idx) + self.pos_emb[:T]
+        x = self._tok(idx) + self.pos_emb[:T]
         branch = None
         for blk in self.blocks:
             x, branch = blk.forward_pair(x, branch)

@@ -100,6 +100,25 @@ def test_argument_checks_reject_before_launch(abi):
     assert lib.fx_rms_norm_bwd_workspace(0, 768) == 0
 
 
+def test_embedding_bwd_checks_and_workspace(abi):
+    lib = abi.lib()
+    fake = ctypes.c_void_p(4096)     # never dereferenced: the checks fail first
+    # D must be a multiple of 8, V positive, grad 16-byte aligned, dy rows aligned
+    assert lib.fx_embedding_bwd(fake, 4, fake, 12, fake, 10, 12, fake, None) == abi.FX_EINVAL
+    assert b"D=12" in lib.fx_last_error()
+    assert lib.fx_embedding_bwd(fake, 4, fake, 8, fake, 0, 8, fake, None) == abi.FX_EINVAL
+    assert lib.fx_embedding_bwd(fake, 4, fake, 8, ctypes.c_void_p(4098), 10, 8, fake, None) == abi.FX_EINVAL
+    assert lib.fx_embedding_bwd(fake, 4, fake, 12, fake, 10, 8, fake, None) == abi.FX_EINVAL
+    assert lib.fx_embedding_bwd(fake, -1, fake, 8, fake, 10, 8, fake, None) == abi.FX_EINVAL
+    # workspace: per-chunk counts (1024 positions a chunk), offsets, one sum per 256 ids,
+    # ranks and the order, each rounded up to 16 bytes
+    ws = lib.fx_embedding_bwd_workspace
+    assert ws(0, 100) == 0 and ws(5, 0) == 0
+    assert ws(1024, 100) == 400 + 416 + 16 + 2 * 4096
+    assert ws(1025, 100) == 800 + 416 + 16 + 2 * 4112
+    assert ws(16384, 50304) == 16 * 50304 * 4 + (50305 * 4 + 12) + 800 + 2 * 16384 * 4
+
+
 def test_rms_norm_rejects_misaligned_vectors(abi):
     # x / w / y / dy / dx are read and written as 16-byte vectors: an address that is
     # only 2-byte aligned is rejected before any launch (never dereferenced)

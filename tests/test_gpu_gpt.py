@@ -409,7 +409,7 @@ def test_deferred_residual_sums_bitwise(dev):
     loss_a.backward()
     ga = [p.grad.clone() for p in model.parameters()]
     model.zero_grad(set_to_none=True)
-    x = model.tok_emb(idx) + model.pos_emb[:64]
+    x = model._tok(idx) + model.pos_emb[:64]   # the lookup GPT.forward makes (same gradient path)
     for blk in model.blocks:
         x = blk(x)
     x = model._norm_f(x)

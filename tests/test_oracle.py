@@ -16,6 +16,7 @@ import torch.nn.functional as F
 from oracle import adamw as oadam
 from oracle import attention as oatt
 from oracle import cross_entropy as oce
+from oracle import embedding as oemb
 from oracle import gpt as ogpt
 from oracle import linear as olin
 from oracle import norm as onorm
@@ -450,3 +451,52 @@ def test_gather_windows_against_unfold_and_outside_zero():
     for b, st in enumerate(idx.tolist()):
         want = unf[st] if 0 <= st <= 26 else torch.zeros(32, dtype=torch.float64)
         assert torch.equal(Xg[b], want)
+
+
+# -- token embedding gradient -------------------------------------------------------------
+
+def test_embedding_grad_matches_torch_autograd():
+    g = torch.Generator().manual_seed(11)
+    V, D = 37, 24
+    idx = torch.randint(0, V, (5, 29), generator=g)
+    dy = torch.randn(5, 29, D, generator=g, dtype=torch.float64)
+    w = torch.zeros(V, D, dtype=torch.float64, requires_grad=True)
+    F.embedding(idx, w).backward(dy)
+    assert torch.allclose(oemb.embedding_grad(idx, dy, V), w.grad, rtol=0, atol=1e-12)
+
+
+def test_embedding_grad_special_cases():
+    V, D = 6, 8
+    dy = torch.arange(4 * D, dtype=torch.float64).reshape(4, D)
+    # ids outside [0, V) add nothing; unused ids are zero rows; a single position is its row
+    idx = torch.tensor([2, -1, 6, 2])
+    got = oemb.embedding_grad(idx, dy, V)
+    assert torch.equal(got[2], dy[0] + dy[3])
+    assert torch.count_nonzero(got[[0, 1, 3, 4, 5]]) == 0
+    one = oemb.embedding_grad(torch.tensor([4]), dy[1:2], V)
+    assert torch.equal(one[4], dy[1])
+
+
+def test_embedding_grad_seq_is_the_position_ordered_fp32_sum():
+    g = torch.Generator().manual_seed(12)
+    V, D, n = 9, 16, 300
+    idx = torch.randint(-2, V, (n,), generator=g)
+    dy = torch.randn(n, D, generator=g).bfloat16()
+    seq = oemb.embedding_grad_seq(idx, dy, V)
+    exact = oemb.embedding_grad(idx, dy, V)
+    # within one bf16 rounding plus the fp32 accumulation of up to n terms
+    bound = 2.0 ** -8 * exact.abs() + n * 2.0 ** -24 * oemb.embedding_grad(idx, dy.abs(), V) + 1e-30
+    assert bool(((seq.double() - exact).abs() <= bound).all())
+    acc = torch.zeros(V, D, dtype=torch.float32)
+    for t in range(n):
+        v = int(idx[t])
+        if 0 <= v < V:
+            acc[v] += dy[t].float()
+    assert torch.equal(seq, acc.bfloat16())
+    # the order is position order: 2^24 + 1 rounds back to 2^24 in fp32, so the three terms
+    # below sum to 0 forwards, where the exact sum (or the reverse order) is 1
+    dy3 = torch.zeros(3, 8).bfloat16()
+    dy3[:, 0] = torch.tensor([2.0 ** 24, 1.0, -(2.0 ** 24)])
+    idx3 = torch.zeros(3, dtype=torch.int64)
+    assert float(oemb.embedding_grad_seq(idx3, dy3, 1)[0, 0]) == 0.0
+    assert float(oemb.embedding_grad(idx3, dy3, 1)[0, 0]) == 1.0
