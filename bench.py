@@ -1,8 +1,8 @@
 """Benchmark: the fxlm GPT 12L-d768 training step on one MI355X, plus the hot-path kernels.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-    python bench.py --only {attention,ce,norm,adamw,linear,wgrad,head,library,step,copy,decode,cpu,fc-ours,fc-library,
-                            fc-ours-cold,fc-library-cold}   (profiling runs)
+    python bench.py --only {attention,ce,norm,adamw,linear,wgrad,head,library,step,copy,decode,embedding,cpu,
+                            fc-ours,fc-library,fc-ours-cold,fc-library-cold}   (profiling runs)
     python bench.py --counter-table p_counter_collection.csv [...]   (per-kernel counter table)
     python bench.py --traffic-table FETCH.csv WRITE.csv COPY_FETCH.csv COPY_WRITE.csv
     python bench.py --trace-table kernel_trace.csv [ONCE_PER_STEP_KERNEL]   (kernel-trace table)
@@ -171,6 +171,23 @@ def bench_norm(torch):
             "fwd_gbs": round(bf / tf / 1e3, 1), "bwd_gbs": round(bb / tb / 1e3, 1),
             "fwd_frac_of_hbm": round(bf / tf / 1e3 / HBM_PEAK_GBS, 4),
             "bwd_frac_of_hbm": round(bb / tb / 1e3 / HBM_PEAK_GBS, 4)}
+
+
+def bench_embedding(torch):
+    """The token-embedding weight gradient at the cfg5 step's lookup (16,384 ids, V 50,304,
+    D 768): fx_embedding_bwd against torch's embedding backward on the same ids and rows.
+    Algorithmic bytes: dy read once and the (V, D) gradient written once."""
+    from fxlm.embedding import embedding_grad
+    n, V, D = 16384, 50304, 768
+    g = torch.Generator(device="cuda").manual_seed(6)
+    idx = torch.randint(0, V, (n,), device="cuda", generator=g)
+    dy = torch.randn(n, D, device="cuda", generator=g).bfloat16()
+    t = time_us(torch, lambda: embedding_grad(idx, dy, V))
+    tl = time_us(torch, lambda: torch.ops.aten.embedding_dense_backward(dy, idx, V, -1, False))
+    b = n * D * 2 + V * D * 2
+    return {"shape_nVD": [n, V, D], "bwd_us": round(t, 2), "bytes": b, "gbs": round(b / t / 1e3, 1),
+            "frac_of_hbm": round(b / t / 1e3 / HBM_PEAK_GBS, 4),
+            "library": {"torch_embedding_backward_us": round(tl, 2), "speedup": round(tl / t, 2)}}
 
 
 def bench_adamw(torch):
@@ -807,13 +824,12 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
-    # 4 warm-up steps: one pass over each of the 4 synthetic batches the step cycles
-    # through (torch's embedding backward sizes its temporaries from the batch's token
-    # counts, so a batch's first step can allocate; 42 ms once when it fell in the timed steps)
+    # 4 warm-up steps: one pass over each of the 4 synthetic batches the step cycles through,
+    # so that no batch's first step (and no first allocation of a size) falls in the timed steps
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU baseline")
     ap.add_argument("--only", choices=["attention", "ce", "norm", "adamw", "linear", "wgrad", "head", "library", "step", "copy",
-                                       "decode",
+                                       "decode", "embedding",
                                        "cpu", "fc-ours", "fc-library", "fc-ours-cold", "fc-library-cold"],
                     help="run one workload and print its figures (for profiling runs)")
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV",
@@ -854,7 +870,7 @@ def main():
         fn = {"attention": bench_attention, "ce": bench_ce, "norm": bench_norm, "adamw": bench_adamw,
               "linear": bench_linear, "wgrad": bench_wgrad, "head": bench_head, "copy": bench_copy,
               "library": bench_library,
-              "decode": bench_decode,
+              "decode": bench_decode, "embedding": bench_embedding,
               "cpu": cpu_baseline,
               "step": lambda t: gpu_step_bench(t, args.steps, args.warmup),
               "fc-ours": lambda t: bench_fc_product(t, "ours", False),
@@ -881,6 +897,7 @@ def main():
                             speedup=round(libs["flat_adamw_cfg4"]["torch_fused_adamw_clip_scaler_us"]
                                           / adamw["step_us"], 2))
     dec = bench_decode(torch)
+    emb = bench_embedding(torch)
     torch.cuda.empty_cache()
     step = gpu_step_bench(torch, args.steps, args.warmup)
     torch.cuda.empty_cache()
@@ -911,7 +928,8 @@ def main():
         "kernels": {"attention_cfg2": {k: v for k, v in attn.items() if not k.startswith("flop")},
                     "cross_entropy_cfg3": ce, "rmsnorm_cfg4": norm, "flat_adamw_cfg4": adamw,
                     "fused_linear_gelu_cfg5_fc": lin, "linear_wgrad_cfg5": wg,
-                    "linear_ce_head_cfg5": head, "decode": dec},
+                    "linear_ce_head_cfg5": head, "decode": dec,
+                    "embedding_grad_cfg5": emb},
         "final_loss": round(step["loss"], 4),
     }
     print(json.dumps(out))
