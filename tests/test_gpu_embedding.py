@@ -78,3 +78,19 @@ def test_rejects_bad_inputs():
     with pytest.raises(TypeError):
         token_embedding(torch.zeros(4, dtype=torch.int64, device="cuda"),
                         torch.zeros(10, 8, dtype=torch.float32, device="cuda"))
+
+
+def test_workspace_and_output_contents_do_not_matter():
+    # every workspace word the kernels read is written first in the same call, and every
+    # gradient row is stored: buffers filled with garbage give the same bits
+    from fxgpu.abi import call, lib, ptr, stream_of
+    idx, rows = _case(5000, 600, 48, lo=-2, seed=9)
+    ids, dy = idx.cuda(), rows.cuda()
+    nbytes = int(lib().fx_embedding_bwd_workspace(5000, 600))
+    ref = oemb.embedding_grad_seq(idx, rows, 600)
+    for fill in (-1, 0x3F800000, 7):
+        work = torch.full(((nbytes + 3) // 4,), fill, dtype=torch.int32, device="cuda")
+        grad = torch.full((600, 48), float("nan"), dtype=torch.bfloat16, device="cuda")
+        call("fx_embedding_bwd", ptr(ids), 5000, ptr(dy), 48, ptr(grad), 600, 48, ptr(work), stream_of(dy))
+        torch.cuda.synchronize()
+        assert torch.equal(grad.cpu(), ref)
