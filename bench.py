@@ -173,21 +173,53 @@ def bench_norm(torch):
             "bwd_frac_of_hbm": round(bb / tb / 1e3 / HBM_PEAK_GBS, 4)}
 
 
+def _zipf_ids(torch, n, V, seed, a=1.1):
+    g = torch.Generator().manual_seed(seed)
+    p = 1.0 / torch.arange(1, V + 1, dtype=torch.float64) ** a
+    return torch.multinomial(p / p.sum(), n, replacement=True, generator=g)
+
+
+def _byte_text_ids(torch, n):
+    """n byte-level tokens (V = 256) of this repository's own prose (DESIGN/README text; a
+    fixed English sentence when those are absent): the space byte holds ~15 % of them."""
+    text = b""
+    for name in ("DESIGN.md", "README.md", "INTEGRATION.md"):
+        try:
+            with open(os.path.join(ROOT, name), "rb") as fh:
+                text += fh.read()
+        except OSError:
+            pass
+    if len(text) < n:
+        text += b"the quick brown fox jumps over the lazy dog " * (n // 44 + 1)
+    return torch.tensor(list(text[:n]), dtype=torch.int64)
+
+
 def bench_embedding(torch):
-    """The token-embedding weight gradient at the cfg5 step's lookup (16,384 ids, V 50,304,
-    D 768): fx_embedding_bwd against torch's embedding backward on the same ids and rows.
+    """The token-embedding weight gradient at the cfg5 step's lookup (16,384 ids, D 768):
+    fx_embedding_bwd against torch's embedding backward on the same ids and rows, for three id
+    distributions: uniform ids over V 50,304 (the bench's synthetic batches), Zipf ids over
+    V 50,304 (exponent 1.1, as BPE token counts fall off) and byte-level text over V 256 (the
+    reference's prepare_bytes tokens: the space byte alone is ~15 % of the positions).
     Algorithmic bytes: dy read once and the (V, D) gradient written once."""
     from fxlm.embedding import embedding_grad
-    n, V, D = 16384, 50304, 768
+    n, D = 16384, 768
     g = torch.Generator(device="cuda").manual_seed(6)
-    idx = torch.randint(0, V, (n,), device="cuda", generator=g)
     dy = torch.randn(n, D, device="cuda", generator=g).bfloat16()
-    t = time_us(torch, lambda: embedding_grad(idx, dy, V))
-    tl = time_us(torch, lambda: torch.ops.aten.embedding_dense_backward(dy, idx, V, -1, False))
-    b = n * D * 2 + V * D * 2
-    return {"shape_nVD": [n, V, D], "bwd_us": round(t, 2), "bytes": b, "gbs": round(b / t / 1e3, 1),
-            "frac_of_hbm": round(b / t / 1e3 / HBM_PEAK_GBS, 4),
-            "library": {"torch_embedding_backward_us": round(tl, 2), "speedup": round(tl / t, 2)}}
+    cases = {"uniform": (50304, torch.randint(0, 50304, (n,), device="cuda", generator=g)),
+             "zipf": (50304, _zipf_ids(torch, n, 50304, 6).cuda()),
+             "byte_text": (256, _byte_text_ids(torch, n).cuda())}
+    out = {}
+    for name, (V, idx) in cases.items():
+        t = time_us(torch, lambda: embedding_grad(idx, dy, V))
+        tl = time_us(torch, lambda: torch.ops.aten.embedding_dense_backward(dy, idx, V, -1, False))
+        b = n * D * 2 + V * D * 2
+        top = int(torch.bincount(idx, minlength=V).max())
+        out[name] = {"shape_nVD": [n, V, D], "max_positions_per_id": top, "bwd_us": round(t, 2), "bytes": b,
+                     "gbs": round(b / t / 1e3, 1), "frac_of_hbm": round(b / t / 1e3 / HBM_PEAK_GBS, 4),
+                     "library": {"torch_embedding_backward_us": round(tl, 2), "speedup": round(tl / t, 2)}}
+    res = dict(out["uniform"])
+    res["id_distributions"] = out
+    return res
 
 
 def bench_adamw(torch):

@@ -207,7 +207,8 @@ int fx_adamw_step(const fxAdamWState* state, const fxTensorList* lists, int32_t 
  * threads) share that buffer and race; calls in stream order do not.  The buffer's device
  * address is looked up on the first call on each device.
  * No counterpart in the reference: it is for callers that cannot allocate device memory
- * (HIP graph capture of a training step, serving loops, allocation-free harnesses). */
+ * (code under HIP graph capture, serving loops, allocation-free harnesses).  This build does
+ * not support or verify capturing a whole training step in a HIP graph; the step runs eagerly. */
 int fx_adamw_step_noalloc(const fxAdamWState* state, const fxTensorList* lists, int32_t nlists,
                           void* stream);
 
@@ -336,17 +337,20 @@ int fx_linear_fwd_ex(const fxLinearArgs* args, void* stream);
  * of F.gelu(approximate="tanh"), ml/fxlm/model.py:71). */
 int fx_gelu_bwd(const uint16_t* dy, const uint16_t* h, uint16_t* dh, int64_t n, void* stream);
 
-/* Bytes of workspace fx_embedding_bwd needs for n positions and a V-row table (0 when n or V
- * is not positive). */
-int64_t fx_embedding_bwd_workspace(int64_t n, int64_t V);
+/* Bytes of workspace fx_embedding_bwd needs for n positions, a V-row table and rows of D
+ * values (0 when n, V or D is not positive). */
+int64_t fx_embedding_bwd_workspace(int64_t n, int64_t V, int64_t D);
 
-/* Token-embedding gradient: grad (V, D) bf16, row-major, = for every row v the sum, in
- * increasing t, of dy[t] over the positions t with idx[t] == v (fp32 accumulation, one bf16
- * rounding); rows no position selects are zero and ids outside [0, V) select nothing.  idx
- * int64 (n,), dy (n, D) with row stride ldy (16-byte aligned rows, D a multiple of 8), work of
- * fx_embedding_bwd_workspace(n, V) bytes (16-byte aligned).  Deterministic (a stable counting
- * sort, no atomics), with launch sizes that depend on n and V only.  Replaces torch's
- * nn.Embedding backward behind the reference's tok_emb(idx) (ml/fxlm/model.py:82,118). */
+/* Token-embedding gradient: grad (V, D) bf16, row-major, = for every row v the sum of dy[t]
+ * over the positions t with idx[t] == v; rows no position selects are zero and ids outside
+ * [0, V) select nothing.  The positions are sorted by (id, t) into slots 0.. (stable), cut
+ * into segments of 32 slots; an id's rows are summed in fp32 in increasing t within each
+ * segment, its segments' sums are added in segment order, and the total is rounded once to
+ * bf16.  idx int64 (n,), dy (n, D) with row stride ldy (16-byte aligned rows, D a multiple of
+ * 8), work of fx_embedding_bwd_workspace(n, V, D) bytes (16-byte aligned).  Deterministic (a
+ * stable counting sort, no atomics), with launch sizes that depend on n and V only, and no
+ * wave summing more than 32 rows whatever the ids.  Replaces torch's nn.Embedding backward
+ * behind the reference's tok_emb(idx) (ml/fxlm/model.py:82,118). */
 int fx_embedding_bwd(const int64_t* idx, int64_t n, const uint16_t* dy, int64_t ldy, uint16_t* grad, int64_t V,
                      int64_t D, void* work, void* stream);
 

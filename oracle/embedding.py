@@ -5,9 +5,13 @@ whose backward torch computes): grad[v] = sum of dy[t] over the positions t with
 rows no position selects are zero.  Ids outside [0, V) add nothing (torch's lookup rejects
 them; the GPU kernel skips them).
 
-embedding_grad_seq sums in increasing t in fp32 and rounds once to bf16, the order the GPU
-kernel (fx_embedding_bwd) uses, so the two agree bit for bit; embedding_grad gives the exact
-sum in fp64.  Both are pinned in tests/test_oracle.py against torch's own embedding backward.
+embedding_grad_seq restates the summation order of the GPU kernel (fx_embedding_bwd), so the
+two agree bit for bit: the valid positions sorted stably by id form slots 0, 1, ...; the slots
+are cut into segments of SEG = 32 (at global slot multiples of 32, not per id); an id's rows
+are summed in fp32 in increasing position within each segment, its segment sums are added in
+segment order, and the total is rounded once to bf16.  embedding_grad gives the exact sum in
+fp64.  Both are pinned in tests/test_oracle.py: against torch's own embedding backward, and the
+segment rule by fp32 sums that come out differently under any other cut or order.
 """
 import numpy as np
 import torch
@@ -24,15 +28,34 @@ def embedding_grad(idx, dy, V, dtype=torch.float64):
     return out
 
 
-def embedding_grad_seq(idx, dy, V):
-    """(V, D) bf16: each id's rows of dy summed one by one in increasing position in fp32,
-    then rounded to bf16 (round to nearest even)."""
+SEG = 32  # slots per segment (kEmbSeg in embedding.hip)
+
+
+def embedding_grad_seq(idx, dy, V, seg=SEG):
+    """(V, D) bf16: per id, fp32 sums of its rows in increasing position over each segment of
+    `seg` id-sorted slots, the segment sums added in segment order, rounded once to bf16 (round
+    to nearest even)."""
     D = dy.shape[-1]
     ids = idx.detach().to("cpu").reshape(-1).numpy()
     rows = dy.detach().to("cpu", torch.float32).reshape(-1, D).numpy()
-    acc = np.zeros((V, D), dtype=np.float32)
-    for t in range(ids.shape[0]):
-        v = int(ids[t])
-        if 0 <= v < V:
-            acc[v] += rows[t]          # one fp32 add per element, in position order
-    return torch.from_numpy(acc).to(torch.bfloat16)
+    valid = np.nonzero((ids >= 0) & (ids < V))[0]
+    order = valid[np.argsort(ids[valid], kind="stable")]  # slot s -> position, (id, t) order
+    out = np.zeros((V, D), dtype=np.float32)
+    s = 0
+    while s < order.shape[0]:
+        v = int(ids[order[s]])
+        e = s
+        while e < order.shape[0] and int(ids[order[e]]) == v:
+            e += 1
+        total = None
+        a = s
+        while a < e:                    # pieces of the run [s, e) cut at multiples of seg
+            b = min(e, (a // seg + 1) * seg)
+            piece = np.zeros(D, dtype=np.float32)
+            for k in range(a, b):
+                piece += rows[order[k]]  # one fp32 add per element, in position order
+            total = piece if total is None else total + piece
+            a = b
+        out[v] = total
+        s = e
+    return torch.from_numpy(out).to(torch.bfloat16)

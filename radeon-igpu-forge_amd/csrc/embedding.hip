@@ -16,15 +16,25 @@
 //                each block of 256 ids, with the block's sum;
 //   emb_offsets  per block of 256 ids, the sum of the earlier blocks added: offs[v] is the first
 //                slot of id v, offs[V] the count of valid positions;
-//   emb_scatter  position t to slot offs[id] + its chunk's first slot + its rank;
-//   emb_sum      one wave per id: the dy rows of its slots summed in slot order (increasing t),
-//                16 bytes per lane, then stored (zeros when the id has no position).
+//   emb_scatter  position t to slot offs[id] + its chunk's first slot + its rank, and the id
+//                of every slot into sid;
+//   emb_part     one wave per segment of kEmbSeg consecutive slots, for the runs that cross
+//                its edges: the run entering from the previous segment leaves the fp32 sum of
+//                its rows here (in slot order, i.e. increasing t) as a "head" partial row, the
+//                run continuing into the next segment a "tail" partial row;
+//   emb_final    one wave per id: zeros when the id has no position; a run inside one segment
+//                summed in slot order; a longer run its first segment's tail partial plus the
+//                later segments' head partials, in segment order; rounded once.
+// So no wave sums more than kEmbSeg rows, whatever the ids: one id holding 15 % of the
+// positions (the space byte of byte-level text) is 77 segments summed side by side and one
+// combine of 77 partial rows, where one wave per id would walk its 2,500 rows one by one.
 #include "fx_device.h"
 
 namespace fx {
 
 constexpr int kEmbChunk = 1024;  // positions per emb_rank workgroup (the key keeps 10 bits of it)
 constexpr int kEmbBlock = 256;   // ids per emb_colscan / emb_offsets workgroup
+constexpr int kEmbSeg = 32;      // slots per emb_part wave
 
 __global__ void __launch_bounds__(256) emb_zero_kernel(uint32_t* __restrict__ p, int64_t n) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -152,20 +162,105 @@ __global__ void __launch_bounds__(kEmbBlock) emb_offsets_kernel(int32_t* __restr
 __global__ void __launch_bounds__(256) emb_scatter_kernel(const int64_t* __restrict__ idx, int64_t n, int64_t V,
                                                          const int32_t* __restrict__ cnt,
                                                          const int32_t* __restrict__ offs,
-                                                         const int32_t* __restrict__ rank, int32_t* __restrict__ order) {
+                                                         const int32_t* __restrict__ rank, int32_t* __restrict__ order,
+                                                         int32_t* __restrict__ sid) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= n) return;
     const int32_t r = rank[t];
     if (r < 0) return;
     const int64_t v = idx[t];
     const int64_t pos = (int64_t)offs[v] + cnt[(t / kEmbChunk) * V + v] + r;
-    if (pos >= 0 && pos < n) order[pos] = (int32_t)t;
+    if (pos >= 0 && pos < n) {
+        order[pos] = (int32_t)t;
+        sid[pos] = (int32_t)v;
+    }
 }
 
-__global__ void __launch_bounds__(256) emb_sum_kernel(const uint16_t* __restrict__ dy, int64_t ldy,
-                                                     const int32_t* __restrict__ order,
-                                                     const int32_t* __restrict__ offs, int64_t n,
-                                                     uint16_t* __restrict__ grad, int64_t V, int64_t D) {
+// acc (this lane's 16-byte vector ch of a row, 8 fp32) += the rows of slots b .. e - 1 in slot
+// order; `tl` holds slot j's position in lane j (0 <= b < e <= 64).  Batches of 8 rows: a batch's
+// loads are issued before its adds.
+__device__ __forceinline__ void emb_sum_slots(float (&acc)[8], const uint16_t* __restrict__ dy, int64_t ldy,
+                                              int32_t tl, int b, int e, int64_t ch) {
+    for (int q = b; q < e; q += 8) {
+        uint4 r[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int32_t t = __builtin_amdgcn_readlane(tl, q + u < e ? q + u : q);
+            if (q + u < e) r[u] = ld16(dy + (int64_t)t * ldy + 8 * ch);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (q + u < e) {
+                float f[8];
+                unpack8(r[u], f);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) acc[k] += f[k];
+            }
+    }
+}
+
+// One wave per segment c of kEmbSeg slots: the partial sums of the (at most two) runs that
+// cross the segment's edges.  The first run, if its id also holds slot s0 - 1, leaves its rows'
+// sum in head row 2c; the last run, if its id also holds slot s0 + kEmbSeg and it did not start
+// before s0, leaves its sum in tail row 2c + 1.  Runs inside the segment are emb_final's.
+__global__ void __launch_bounds__(256) emb_part_kernel(const uint16_t* __restrict__ dy, int64_t ldy,
+                                                      const int32_t* __restrict__ order,
+                                                      const int32_t* __restrict__ sid,
+                                                      const int32_t* __restrict__ offs, int64_t n, int64_t nseg,
+                                                      float* __restrict__ part, int64_t V, int64_t D) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int64_t c = (int64_t)blockIdx.x * 4 + wave;
+    if (c >= nseg) return;
+    const int64_t s0 = c * kEmbSeg;
+    int64_t nvalid = offs[V];
+    if (nvalid > n) nvalid = n;
+    const int ns = (int)(nvalid - s0 < kEmbSeg ? nvalid - s0 : kEmbSeg);  // slots of this segment
+    if (ns <= 0) return;
+    // lane u < ns: slot s0 + u's position and id; lane ns: the id of the slot after the segment
+    // (-1 past the last); lane 63: the id of the slot before it (-1 for the first segment)
+    int32_t tl = 0, vl = -1;
+    if (lane < ns) {
+        tl = order[s0 + lane];
+        vl = sid[s0 + lane];
+    } else if (lane == ns && s0 + ns < nvalid) {
+        vl = sid[s0 + ns];
+    } else if (lane == 63 && s0 > 0) {
+        vl = sid[s0 - 1];
+    }
+    const int v0 = __builtin_amdgcn_readlane(vl, 0), vlast = __builtin_amdgcn_readlane(vl, ns - 1);
+    const bool head = s0 > 0 && __builtin_amdgcn_readlane(vl, 63) == v0;
+    const bool tail = __builtin_amdgcn_readlane(vl, ns) == vlast && !(head && vlast == v0);
+    if (!head && !tail) return;
+    int e0 = 1;  // the first run: slots 0 .. e0 - 1
+    while (e0 < ns && __builtin_amdgcn_readlane(vl, e0) == v0) ++e0;
+    int b1 = ns - 1;  // the last run: slots b1 .. ns - 1
+    while (b1 > 0 && __builtin_amdgcn_readlane(vl, b1 - 1) == vlast) --b1;
+    for (int64_t ch = lane; ch < D / 8; ch += 64) {
+        if (head) {
+            float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            emb_sum_slots(acc, dy, ldy, tl, 0, e0, ch);
+            float4* o = reinterpret_cast<float4*>(part + 2 * c * D + 8 * ch);
+            o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+            o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+        }
+        if (tail) {
+            float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            emb_sum_slots(acc, dy, ldy, tl, b1, ns, ch);
+            float4* o = reinterpret_cast<float4*>(part + (2 * c + 1) * D + 8 * ch);
+            o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+            o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+        }
+    }
+}
+
+// One wave per id v, run = slots offs[v] .. offs[v + 1] - 1: zeros when empty; a run inside one
+// segment summed here in slot order (at most kEmbSeg rows); a longer one is its first segment's
+// tail partial plus the later segments' head partials, in segment order.  One bf16 rounding.
+__global__ void __launch_bounds__(256) emb_final_kernel(const uint16_t* __restrict__ dy, int64_t ldy,
+                                                       const int32_t* __restrict__ order,
+                                                       const int32_t* __restrict__ offs, int64_t n,
+                                                       const float* __restrict__ part, uint16_t* __restrict__ grad,
+                                                       int64_t V, int64_t D) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int64_t v = (int64_t)blockIdx.x * 4 + wave;
     if (v >= V) return;
@@ -173,15 +268,44 @@ __global__ void __launch_bounds__(256) emb_sum_kernel(const uint16_t* __restrict
     if (beg < 0) beg = 0;
     if (end > n) end = n;
     uint16_t* out = grad + v * D;
+    if (end <= beg) {  // no position has this id
+        for (int64_t ch = lane; ch < D / 8; ch += 64) st16(out + 8 * ch, make_uint4(0u, 0u, 0u, 0u));
+        return;
+    }
+    const int64_t c0 = beg / kEmbSeg, c1 = (end - 1) / kEmbSeg;
+    if (c0 == c1) {  // inside one segment: at most kEmbSeg rows
+        const int len = (int)(end - beg);
+        const int32_t tl = lane < len ? order[beg + lane] : 0;
+        for (int64_t ch = lane; ch < D / 8; ch += 64) {
+            float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            emb_sum_slots(acc, dy, ldy, tl, 0, len, ch);
+            st16(out + 8 * ch, pack8(acc));
+        }
+        return;
+    }
     for (int64_t ch = lane; ch < D / 8; ch += 64) {
-        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        for (int64_t i = beg; i < end; ++i) {
-            const int64_t t = order[i];
-            if (t < 0 || t >= n) continue;
-            float f[8];
-            unpack8(ld16(dy + t * ldy + 8 * ch), f);
+        const float4* t0 = reinterpret_cast<const float4*>(part + (2 * c0 + 1) * D + 8 * ch);
+        float acc[8];
+        {
+            const float4 a = t0[0], b = t0[1];
+            acc[0] = a.x; acc[1] = a.y; acc[2] = a.z; acc[3] = a.w;
+            acc[4] = b.x; acc[5] = b.y; acc[6] = b.z; acc[7] = b.w;
+        }
+        for (int64_t c = c0 + 1; c <= c1; c += 8) {
+            float4 h[8][2];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) acc[e] += f[e];
+            for (int u = 0; u < 8; ++u)
+                if (c + u <= c1) {
+                    const float4* p = reinterpret_cast<const float4*>(part + 2 * (c + u) * D + 8 * ch);
+                    h[u][0] = p[0];
+                    h[u][1] = p[1];
+                }
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (c + u <= c1) {
+                    acc[0] += h[u][0].x; acc[1] += h[u][0].y; acc[2] += h[u][0].z; acc[3] += h[u][0].w;
+                    acc[4] += h[u][1].x; acc[5] += h[u][1].y; acc[6] += h[u][1].z; acc[7] += h[u][1].w;
+                }
         }
         st16(out + 8 * ch, pack8(acc));
     }
@@ -193,10 +317,12 @@ static int64_t emb_align16(int64_t b) { return (b + 15) / 16 * 16; }
 
 using namespace fx;
 
-extern "C" int64_t fx_embedding_bwd_workspace(int64_t n, int64_t V) {
-    if (n <= 0 || V <= 0) return 0;
+extern "C" int64_t fx_embedding_bwd_workspace(int64_t n, int64_t V, int64_t D) {
+    if (n <= 0 || V <= 0 || D <= 0) return 0;
     const int64_t nch = (n + kEmbChunk - 1) / kEmbChunk, nb = (V + kEmbBlock - 1) / kEmbBlock;
-    return emb_align16(nch * V * 4) + emb_align16((V + 1) * 4) + emb_align16(nb * 4) + 2 * emb_align16(n * 4);
+    const int64_t nseg = (n + kEmbSeg - 1) / kEmbSeg;
+    return emb_align16(nch * V * 4) + emb_align16((V + 1) * 4) + emb_align16(nb * 4) + 3 * emb_align16(n * 4) +
+           emb_align16(2 * nseg * D * 4);
 }
 
 extern "C" int fx_embedding_bwd(const int64_t* idx, int64_t n, const uint16_t* dy, int64_t ldy, uint16_t* grad,
@@ -227,7 +353,13 @@ extern "C" int fx_embedding_bwd(const int64_t* idx, int64_t n, const uint16_t* d
     int32_t* bsum = reinterpret_cast<int32_t*>(w);
     w += emb_align16(nb * 4);
     int32_t* rank = reinterpret_cast<int32_t*>(w);
-    int32_t* order = reinterpret_cast<int32_t*>(w + emb_align16(n * 4));
+    w += emb_align16(n * 4);
+    int32_t* order = reinterpret_cast<int32_t*>(w);
+    w += emb_align16(n * 4);
+    int32_t* sid = reinterpret_cast<int32_t*>(w);
+    w += emb_align16(n * 4);
+    float* part = reinterpret_cast<float*>(w);  // per segment: head row, then tail row
+    const int64_t nseg = (n + kEmbSeg - 1) / kEmbSeg;
     hipLaunchKernelGGL(emb_rank_kernel, dim3((unsigned)nch), dim3(kEmbChunk), 0, s, idx, n, V, cnt, rank);
     if (int e = check_launch("emb_rank")) return e;
     hipLaunchKernelGGL(emb_colscan_kernel, dim3((unsigned)nb), dim3(kEmbBlock), 0, s, cnt, (int)nch, V, offs, bsum);
@@ -235,9 +367,12 @@ extern "C" int fx_embedding_bwd(const int64_t* idx, int64_t n, const uint16_t* d
     hipLaunchKernelGGL(emb_offsets_kernel, dim3((unsigned)nb), dim3(kEmbBlock), 0, s, offs, bsum, V);
     if (int e = check_launch("emb_offsets")) return e;
     hipLaunchKernelGGL(emb_scatter_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, idx, n, V, cnt, offs,
-                       rank, order);
+                       rank, order, sid);
     if (int e = check_launch("emb_scatter")) return e;
-    hipLaunchKernelGGL(emb_sum_kernel, dim3((unsigned)((V + 3) / 4)), dim3(256), 0, s, dy, ldy, order, offs, n, grad,
-                       V, D);
-    return check_launch("emb_sum");
+    hipLaunchKernelGGL(emb_part_kernel, dim3((unsigned)((nseg + 3) / 4)), dim3(256), 0, s, dy, ldy, order, sid, offs, n,
+                       nseg, part, V, D);
+    if (int e = check_launch("emb_part")) return e;
+    hipLaunchKernelGGL(emb_final_kernel, dim3((unsigned)((V + 3) / 4)), dim3(256), 0, s, dy, ldy, order, offs, n, part,
+                       grad, V, D);
+    return check_launch("emb_final");
 }

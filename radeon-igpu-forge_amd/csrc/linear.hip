@@ -38,6 +38,16 @@ constexpr int kGWM = 64, kGWN = 64;         // wave tile: 16 waves in 4 (M) x 4 
 constexpr int kGTI = kGWM / 32, kGTJ = kGWN / 32;  // 32 x 32 MFMA tiles per wave
 static_assert(kGBM == kGBN && kGBM * kGSPR % 64 == 0, "tile shape");
 static_assert((kGBM / kGWM) * (kGBN / kGWN) == kGWaves, "wave layout");
+// The general forward kernel: 8 waves of 64 x 128 in 4 (M) x 2 (N), two waves per SIMD.
+// Its epilogue variants (bias, GELU, pre-activation H, residual) kept 16 waves of 64 x 64
+// past the 128 registers of four waves per SIMD and into scratch; 128 accumulators of 256
+// registers leave them room.
+constexpr int kFThreads = 512;
+constexpr int kFWaves = kFThreads / 64;
+constexpr int kFPW = (2 * kGNI + kFWaves - 1) / kFWaves;  // wave loads per wave per stage (A and W)
+constexpr int kFWM = 64, kFWN = 128;
+constexpr int kFTI = kFWM / 32, kFTJ = kFWN / 32;
+static_assert((kGBM / kFWM) * (kGBN / kFWN) == kFWaves, "forward wave layout");
 
 struct GemmArgs {
     const uint16_t* A;
@@ -61,6 +71,7 @@ struct GemmArgs {
     const uint16_t* nw;  // RMSNorm weight (K,) applied to the A rows first (few-row kernel), or null
     float eps;
     bool vec_c, vec_h;   // C / H rows start 16-byte aligned (16-byte epilogue stores)
+    bool vec_r;          // residual rows start 16-byte aligned (16-byte epilogue loads)
 };
 
 // tile t -> (row panel, column tile).  Workgroups are dealt round-robin to the 8 XCDs, so
@@ -98,6 +109,29 @@ __device__ __forceinline__ void epi_put(uint16_t* tmp, int q, const float (&v)[4
     *reinterpret_cast<uint2*>(tmp + (lane & 31) * kEpiLD + 8 * q + 4 * (lane >> 5)) =
         make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
 }
+// The 32 x 32 bf16 block of `src` at (mb, nb) into `tmp`, in the layout epi_flush reads (rows
+// r = ch / 4, 16-byte chunks 8 (ch % 4)); elements past M or N are not read (their outputs
+// are not stored).
+__device__ __forceinline__ void epi_load(uint16_t* tmp, const uint16_t* src, int64_t ld, int mb, int nb, int M, int N,
+                                         bool vec, int lane) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int ch = h * 64 + lane;
+        const int r = ch >> 2, c = (ch & 3) * 8;
+        const int m = mb + r, n = nb + c;
+        if (m >= M || n >= N) continue;
+        const uint16_t* p = src + (int64_t)m * ld + n;
+        uint4 u;
+        if (vec && n + 8 <= N) {
+            u = ld16(p);
+        } else {
+            uint32_t w[4] = {0u, 0u, 0u, 0u};
+            for (int e = 0; e < 8 && n + e < N; ++e) w[e >> 1] |= (uint32_t)p[e] << (16 * (e & 1));
+            u = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+        *reinterpret_cast<uint4*>(tmp + r * kEpiLD + c) = u;
+    }
+}
 __device__ __forceinline__ void epi_flush(const uint16_t* tmp, uint16_t* out, int64_t ld, int mb, int nb, int M,
                                           int N, bool vec, int lane) {
 #pragma unroll
@@ -123,10 +157,14 @@ __device__ __forceinline__ void epi_flush(const uint16_t* tmp, uint16_t* out, in
 // EPI selects the epilogue at compile time (fewer live registers than runtime switches):
 // bit 0 GELU, bit 1 pre-activation H out, bit 2 bias, bit 3 residual
 template <int EPI>
-__global__ void __launch_bounds__(kGThreads, 1) gemm_bias_act_kernel(GemmArgs a) {
+__global__ void __launch_bounds__(kFThreads, 1) gemm_bias_act_kernel(GemmArgs a) {
     constexpr bool kGelu = EPI & 1, kH = EPI & 2, kBias = EPI & 4, kRes = EPI & 8;
     __shared__ __attribute__((aligned(16))) uint16_t sa[2][kGBM * kGLD];
     __shared__ __attribute__((aligned(16))) uint16_t sb[2][kGBN * kGLD];
+    // the bias of the current tile's columns (0 past N), read by the epilogue at
+    // compile-time offsets from one per-lane address: per-element global loads of the bias
+    // made the compiler keep 16 64-bit column offsets live across the tile and spill them
+    __shared__ __attribute__((aligned(16))) uint16_t sbias[kBias ? kGBN : 1];
 
     const int nm = (a.M + kGBM - 1) / kGBM, nn = (a.N + kGBN - 1) / kGBN;
     const int ntiles = nm * nn;
@@ -135,18 +173,18 @@ __global__ void __launch_bounds__(kGThreads, 1) gemm_bias_act_kernel(GemmArgs a)
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = (wave / (kGBN / kGWN)) * kGWM, wn = (wave % (kGBN / kGWN)) * kGWN;
+    const int wm = (wave / (kGBN / kFWN)) * kFWM, wn = (wave % (kGBN / kFWN)) * kFWN;
     const int g = lane >> 5;
     const int nk = (a.K + kGBK - 1) / kGBK;
 
     // this wave's slot loads: instruction i = wave + 16k covers 64 slots of the A tile
     // (i < kGNI) or the W tile; per lane a row pointer (null: row past M / N, or a
     // gathered window that leaves X, read as zeros) and the slot's column
-    const uint16_t* src[kGPW];
-    int kcol[kGPW], trow[kGPW];
+    const uint16_t* src[kFPW];
+    int kcol[kFPW], trow[kFPW];
 #pragma unroll
-    for (int k = 0; k < kGPW; ++k) {
-        const int i = wave + kGWaves * k;
+    for (int k = 0; k < kFPW; ++k) {
+        const int i = wave + kFWaves * k;
         const int sl = (i % kGNI) * 64 + lane;
         const int r = sl / kGSPR;
         int c = sl - r * kGSPR;
@@ -156,8 +194,8 @@ __global__ void __launch_bounds__(kGThreads, 1) gemm_bias_act_kernel(GemmArgs a)
     }
     auto set_rows = [&](int m0, int n0) {
 #pragma unroll
-        for (int k = 0; k < kGPW; ++k) {
-            const int i = wave + kGWaves * k;
+        for (int k = 0; k < kFPW; ++k) {
+            const int i = wave + kFWaves * k;
             const uint16_t* row = nullptr;
             if (i < kGNI) {
                 const int m = m0 + trow[k];
@@ -180,8 +218,8 @@ __global__ void __launch_bounds__(kGThreads, 1) gemm_bias_act_kernel(GemmArgs a)
         const int k0 = kt * kGBK;
         const bool full = k0 + kGBK <= a.K;
 #pragma unroll
-        for (int k = 0; k < kGPW; ++k) {
-            const int i = wave + kGWaves * k;
+        for (int k = 0; k < kFPW; ++k) {
+            const int i = wave + kFWaves * k;
             if (i >= 2 * kGNI) break;
             const uint16_t* tile = (i < kGNI) ? sa[st] : sb[st];
             const uint32_t dst = lds_addr(tile + (i % kGNI) * 64 * 8);
@@ -196,11 +234,11 @@ __global__ void __launch_bounds__(kGThreads, 1) gemm_bias_act_kernel(GemmArgs a)
     issue(0, 0);
     int st = 0;  // stage of the next K step to consume
     for (; t < ntiles; t += gridDim.x) {
-        f32x16 acc[kGTJ][kGTI];  // [j: 32 columns of W][i: 32 rows of A]
+        f32x16 acc[kFTJ][kFTI];  // [j: 32 columns of W][i: 32 rows of A]
 #pragma unroll
-        for (int j = 0; j < kGTJ; ++j)
+        for (int j = 0; j < kFTJ; ++j)
 #pragma unroll
-            for (int i = 0; i < kGTI; ++i) acc[j][i] = f32x16{};
+            for (int i = 0; i < kFTI; ++i) acc[j][i] = f32x16{};
         const bool write_xg = a.Xg != nullptr && nt == 0;
         const int cm0 = m0, cn0 = n0;
         for (int kt = 0; kt < nk; ++kt, st ^= 1) {
@@ -217,8 +255,8 @@ __global__ void __launch_bounds__(kGThreads, 1) gemm_bias_act_kernel(GemmArgs a)
             if (write_xg) {
                 // the gathered rows of this K stage, from LDS to Xg (first column of tiles)
 #pragma unroll
-                for (int q = 0; q < kGBM * (kGBK / 8) / kGThreads; ++q) {
-                    const int v = tid + kGThreads * q;
+                for (int q = 0; q < kGBM * (kGBK / 8) / kFThreads; ++q) {
+                    const int v = tid + kFThreads * q;
                     const int r = v / (kGBK / 8), c = v - r * (kGBK / 8);
                     const int m = cm0 + r, k = kt * kGBK + c * 8;
                     if (m < a.M && k < a.K)
@@ -227,17 +265,17 @@ __global__ void __launch_bounds__(kGThreads, 1) gemm_bias_act_kernel(GemmArgs a)
             }
 #pragma unroll
             for (int c = 0; c < kGBK / 16; ++c) {
-                bf16x8 av[kGTI], bv[kGTJ];
+                bf16x8 av[kFTI], bv[kFTJ];
 #pragma unroll
-                for (int i = 0; i < kGTI; ++i)
+                for (int i = 0; i < kFTI; ++i)
                     av[i] = *reinterpret_cast<const bf16x8*>(A + (wm + 32 * i + (lane & 31)) * kGLD + 16 * c + 8 * g);
 #pragma unroll
-                for (int j = 0; j < kGTJ; ++j)
+                for (int j = 0; j < kFTJ; ++j)
                     bv[j] = *reinterpret_cast<const bf16x8*>(Bt + (wn + 32 * j + (lane & 31)) * kGLD + 16 * c + 8 * g);
 #pragma unroll
-                for (int j = 0; j < kGTJ; ++j)
+                for (int j = 0; j < kFTJ; ++j)
 #pragma unroll
-                    for (int i = 0; i < kGTI; ++i) acc[j][i] = mfma32(bv[j], av[i], acc[j][i]);
+                    for (int i = 0; i < kFTI; ++i) acc[j][i] = mfma32(bv[j], av[i], acc[j][i]);
             }
         }
 
@@ -249,30 +287,45 @@ __global__ void __launch_bounds__(kGThreads, 1) gemm_bias_act_kernel(GemmArgs a)
         // accumulators measured 8 % slower).  `st` now names the next tile's first stage
         // (its loads are in flight): the stage just consumed, st ^ 1, is the scratch once
         // every wave is done reading it.
+        if constexpr (kBias) {
+            if (tid < kGBN) sbias[tid] = cn0 + tid < a.N ? a.bias[cn0 + tid] : (uint16_t)0;
+        }
         __syncthreads();
         uint16_t* tmp = (wave < 8 ? sa[st ^ 1] : sb[st ^ 1]) + (wave & 7) * (32 * kEpiLD);
 #pragma unroll
-        for (int j = 0; j < kGTJ; ++j) {
+        for (int j = 0; j < kFTJ; ++j) {
             const int nb = cn0 + wn + 32 * j;  // first column of the block
+            const uint16_t* bcol = sbias + wn + 32 * j + 4 * g;  // bias of columns nb + 4 g + ...
 #pragma unroll
-            for (int i = 0; i < kGTI; ++i) {
+            for (int i = 0; i < kFTI; ++i) {
                 const int mb = cm0 + wm + 32 * i;  // first row of the block
                 const int m = mb + (lane & 31);
-                // pre-activation h = acc + bias (H, when wanted), then y = act(h) (+ residual)
+                (void)m;
+                // pre-activation h = acc + bias (H, when wanted), then y = act(h) (+ residual).
+                // The residual block is staged in tmp by coalesced row loads; each lane reads
+                // its 4 values of a q group back from the position it then writes.
 #pragma unroll
                 for (int pass = 0; pass < 2; ++pass) {
                     if (pass == 0 && !kH) continue;
+                    if (pass == 1 && kRes) epi_load(tmp, a.res, a.ldres, mb, nb, a.M, a.N, a.vec_r, lane);
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
+                        float rv[4] = {0.f, 0.f, 0.f, 0.f};
+                        if (pass == 1 && kRes) {
+                            const uint2 u = *reinterpret_cast<const uint2*>(tmp + (lane & 31) * kEpiLD + 8 * q + 4 * g);
+                            rv[0] = bf16_to_f32((uint16_t)u.x);
+                            rv[1] = bf16_to_f32((uint16_t)(u.x >> 16));
+                            rv[2] = bf16_to_f32((uint16_t)u.y);
+                            rv[3] = bf16_to_f32((uint16_t)(u.y >> 16));
+                        }
                         float v[4];
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
-                            const int n = nb + 8 * q + 4 * g + e;
                             float h = acc[j][i][4 * q + e];
-                            if (kBias && n < a.N) h += bf16_to_f32(a.bias[n]);
+                            if (kBias) h += bf16_to_f32(bcol[8 * q + e]);
                             if (pass == 1) {
                                 if (kGelu) h = gelu_tanh(h);
-                                if (kRes && m < a.M && n < a.N) h += bf16_to_f32(a.res[(int64_t)m * a.ldres + n]);
+                                if (kRes) h += rv[e];
                             }
                             v[e] = h;
                         }
@@ -282,6 +335,9 @@ __global__ void __launch_bounds__(kGThreads, 1) gemm_bias_act_kernel(GemmArgs a)
                         epi_flush(tmp, a.H, a.ldh, mb, nb, a.M, a.N, a.vec_h, lane);
                     else
                         epi_flush(tmp, a.C, a.ldc, mb, nb, a.M, a.N, a.vec_c, lane);
+                    // one block at a time: interleaving the blocks' loads and stores raised
+                    // the register pressure of the widest epilogues past the budget
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
         }
@@ -1289,6 +1345,7 @@ static int linear_fwd(GemmArgs a, hipStream_t stream) {
     if (a.M <= kSKMaxM) return linear_skinny(a, stream);
     a.vec_c = a.ldc % 8 == 0 && ((uintptr_t)a.C & 15) == 0;
     a.vec_h = a.H && a.ldh % 8 == 0 && ((uintptr_t)a.H & 15) == 0;
+    a.vec_r = a.res && a.ldres % 8 == 0 && ((uintptr_t)a.res & 15) == 0;
     const int64_t tiles = ((int64_t)(a.M + kGBM - 1) / kGBM) * ((a.N + kGBN - 1) / kGBN);
     FX_REQUIRE(tiles < 0x7fffffffLL, "fx_linear_fwd: too many tiles");
     if (const int nj = fast_gemm_nj(a)) {
@@ -1311,7 +1368,7 @@ static int linear_fwd(GemmArgs a, hipStream_t stream) {
     const int64_t grid = tiles < cus ? tiles : cus;
     const int epi = (a.act == 1 ? 1 : 0) | (a.H ? 2 : 0) | (a.bias ? 4 : 0) | (a.res ? 8 : 0);
 #define FX_GEMM_EPI(E) \
-    case E: hipLaunchKernelGGL(gemm_bias_act_kernel<E>, dim3((unsigned)grid), dim3(kGThreads), 0, stream, a); break;
+    case E: hipLaunchKernelGGL(gemm_bias_act_kernel<E>, dim3((unsigned)grid), dim3(kFThreads), 0, stream, a); break;
     switch (epi) {
         FX_GEMM_EPI(0) FX_GEMM_EPI(1) FX_GEMM_EPI(2) FX_GEMM_EPI(3) FX_GEMM_EPI(4) FX_GEMM_EPI(5) FX_GEMM_EPI(6)
         FX_GEMM_EPI(7) FX_GEMM_EPI(8) FX_GEMM_EPI(9) FX_GEMM_EPI(10) FX_GEMM_EPI(11) FX_GEMM_EPI(12)

@@ -182,10 +182,10 @@ __global__ void __launch_bounds__(NT, MW)
 rms_bwd_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ dy,
                const uint16_t* __restrict__ w, const float* __restrict__ rstd,
                const uint16_t* __restrict__ dres, uint16_t* __restrict__ dx, float* __restrict__ part, int64_t N,
-               int D, int per_wave) {
+               int D) {
     constexpr int G = NT / LPR;
     constexpr int NW = NT / 64;
-    extern __shared__ float red[];  // NW x D floats (per_wave) or D floats
+    extern __shared__ float red[];  // NW x D floats
     const int lane = threadIdx.x % LPR;
     const int grp = threadIdx.x / LPR;
     const int V8 = D >> 3;
@@ -220,47 +220,138 @@ rms_bwd_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ dy,
         for (int i = 0; i < NV; ++i)
 #pragma unroll
             for (int j = 0; j < 8; ++j) acc[i][j] += __shfl_xor(acc[i][j], off, 64);
-    // waves: with per_wave, each writes its partial row to LDS, one barrier, then every
-    // column is summed over the waves in order (1 us faster at [65536, 768] than the
-    // wave-by-wave fold with a barrier per wave, which wide rows use: NW x D floats
-    // would not fit in LDS)
+    // waves: each writes its partial row to LDS, one barrier, then every column is summed
+    // over the waves in order (1 us faster at [65536, 768] than a wave-by-wave fold with a
+    // barrier per wave)
     const int wave = threadIdx.x >> 6;
     float* pr = part + (int64_t)blockIdx.x * D;
-    if (per_wave) {
-        if ((threadIdx.x & 63) < LPR) {
+    if ((threadIdx.x & 63) < LPR) {
 #pragma unroll
-            for (int i = 0; i < NV; ++i) {
-                const int c = i * LPR + lane;
-                if (c < V8) {
-                    float4* r = reinterpret_cast<float4*>(red + wave * D + c * 8);
-                    r[0] = make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
-                    r[1] = make_float4(acc[i][4], acc[i][5], acc[i][6], acc[i][7]);
-                }
+        for (int i = 0; i < NV; ++i) {
+            const int c = i * LPR + lane;
+            if (c < V8) {
+                float4* r = reinterpret_cast<float4*>(red + wave * D + c * 8);
+                r[0] = make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+                r[1] = make_float4(acc[i][4], acc[i][5], acc[i][6], acc[i][7]);
             }
         }
-        __syncthreads();
-        for (int c = threadIdx.x; c < D; c += NT) {
-            float sum = red[c];
-            for (int k = 1; k < NW; ++k) sum += red[k * D + c];
-            pr[c] = sum;
-        }
-        return;
     }
-    for (int wv = 0; wv < NW; ++wv) {
-        if (wave == wv && (threadIdx.x & 63) < LPR) {
+    __syncthreads();
+    for (int c = threadIdx.x; c < D; c += NT) {
+        float sum = red[c];
+        for (int k = 1; k < NW; ++k) sum += red[k * D + c];
+        pr[c] = sum;
+    }
+}
+
+// Backward for D > 1536: the whole 512-thread block owns one row at a time (thread t holds
+// the row's 16-byte vectors t and t + 512, so NV <= 2 covers D <= 8192) and loads the
+// block's next row while it computes the current one.  The row sum of x * w * dy is a lane
+// butterfly per wave and then the 8 wave sums in a fixed order through LDS (double-buffered
+// by row parity: one barrier per row).  Each column's dw partial belongs to one thread, so
+// the block's partial row is written without a reduction.  The register kernel above held
+// up to 16 vectors of x, dy and dw per lane at these widths and spilled up to 1.7 KB per
+// lane; here a lane holds at most 2 of each.
+template <int NV>
+struct WideRow {
+    uint4 xv[NV], dv[NV], rv[NV];
+    float r;
+    __device__ __forceinline__ void load(const uint16_t* __restrict__ x, const uint16_t* __restrict__ dy,
+                                         const uint16_t* __restrict__ dres, const float* __restrict__ rstd,
+                                         int64_t row, int64_t n, int V8) {
+        if (row >= n) return;  // uniform per block
 #pragma unroll
-            for (int i = 0; i < NV; ++i) {
-                const int c = i * LPR + lane;
-                if (c < V8) {
-#pragma unroll
-                    for (int j = 0; j < 8; ++j)
-                        red[c * 8 + j] = (wv == 0) ? acc[i][j] : red[c * 8 + j] + acc[i][j];
-                }
+        for (int i = 0; i < NV; ++i) {
+            const int c = i * kNormBwdThreads + (int)threadIdx.x;
+            xv[i] = make_uint4(0u, 0u, 0u, 0u);
+            dv[i] = xv[i];
+            rv[i] = xv[i];
+            if (c < V8) {
+                xv[i] = ld16_nt(x + row * V8 * 8 + (int64_t)c * 8);
+                dv[i] = ld16_nt(dy + row * V8 * 8 + (int64_t)c * 8);
+                if (dres) rv[i] = ld16_nt(dres + row * V8 * 8 + (int64_t)c * 8);
             }
         }
-        __syncthreads();
+        r = rstd[row];
     }
-    for (int c = threadIdx.x; c < D; c += NT) pr[c] = red[c];
+};
+
+template <int NV>
+__global__ void __launch_bounds__(kNormBwdThreads)
+rms_bwd_wide_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ dy,
+                    const uint16_t* __restrict__ w, const float* __restrict__ rstd,
+                    const uint16_t* __restrict__ dres, uint16_t* __restrict__ dx, float* __restrict__ part,
+                    int64_t N, int D) {
+    constexpr int NW = kNormBwdThreads / 64;
+    __shared__ float red[2][NW];
+    const int V8 = D >> 3;
+    const int wave = threadIdx.x >> 6;
+    const float invD = 1.f / (float)D;
+    float acc[NV][8];
+    uint4 wv[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = i * kNormBwdThreads + (int)threadIdx.x;
+        wv[i] = c < V8 ? ld16(w + c * 8) : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = 0.f;
+    }
+    WideRow<NV> cur, nxt;
+    int par = 0;
+    for (int64_t row = blockIdx.x; row < N; row += gridDim.x, par ^= 1) {
+        if (row == blockIdx.x) cur.load(x, dy, dres, rstd, row, N, V8);
+        nxt.load(x, dy, dres, rstd, row + gridDim.x, N, V8);
+        float t = 0.f;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            float fx_[8], fd[8], fw[8];
+            unpack8(cur.xv[i], fx_);
+            unpack8(cur.dv[i], fd);
+            unpack8(wv[i], fw);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                t = fmaf(fx_[j] * fw[j], fd[j], t);
+                acc[i][j] = fmaf(fx_[j] * cur.r, fd[j], acc[i][j]);
+            }
+        }
+        t = group_sum<64>(t);
+        if ((threadIdx.x & 63) == 0) red[par][wave] = t;
+        __syncthreads();
+        float tot = red[par][0];
+#pragma unroll
+        for (int k = 1; k < NW; ++k) tot += red[par][k];
+        const float corr = cur.r * cur.r * cur.r * tot * invD;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int c = i * kNormBwdThreads + (int)threadIdx.x;
+            if (c < V8) {
+                float fx_[8], fd[8], fw[8], o[8];
+                unpack8(cur.xv[i], fx_);
+                unpack8(cur.dv[i], fd);
+                unpack8(wv[i], fw);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) o[j] = fmaf(cur.r * fw[j], fd[j], -fx_[j] * corr);
+                if (dres) {
+                    float fr[8];
+                    unpack8(cur.rv[i], fr);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) o[j] += fr[j];
+                }
+                st16_nt(dx + row * D + (int64_t)c * 8, pack8(o));
+            }
+        }
+        cur = nxt;
+    }
+    float* pr = part + (int64_t)blockIdx.x * D;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = i * kNormBwdThreads + (int)threadIdx.x;
+        if (c < V8) {
+            float4* o = reinterpret_cast<float4*>(pr + c * 8);
+            o[0] = make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+            o[1] = make_float4(acc[i][4], acc[i][5], acc[i][6], acc[i][7]);
+        }
+    }
 }
 
 // Backward for 512 <= D <= 1536 with the rows prefetched into LDS.  Each wave owns one
@@ -452,18 +543,15 @@ static RowShape pick_shape(int D) {
     return best;
 }
 
-// Backward: fewest vectors per lane first (the dw accumulators and the row's x / dy
-// stay in registers, and occupancy hides the row loads), then the narrowest group that
-// covers the row.  D = 768 runs 64-lane groups with 2 vectors (the second half-empty):
-// 51.7 us against 53.1 us for 32 lanes x 3 vectors at [65536, 768].
+// Backward, register kernel (D < 512, below the LDS-ring kernel's range): one vector per
+// lane, the narrowest row group that covers the row.
+constexpr int kNormRegMaxD = 1536;  // wider rows: rms_bwd_wide_kernel
 static RowShape pick_bwd_shape(int D) {
     static const int lprs[] = {8, 16, 32, 64};
-    static const int nvs[] = {1, 2, 3, 4, 6, 8, 12, 16};
     const int v8 = D / 8;
-    for (int n : nvs)
-        for (int l : lprs)
-            if (l * n >= v8) return {l, n};
-    return {64, 16};
+    for (int l : lprs)
+        if (l >= v8) return {l, 1};
+    return {64, 1};
 }
 
 #define FX_NORM_NV_CASES(LPR, CALL) \
@@ -599,16 +687,33 @@ static int rms_norm_bwd(const uint16_t* x, const uint16_t* dy, const uint16_t* d
                            (const float*)work, P, (int)D, dw_f32, dw);
         return check_launch("rms_dw_reduce");
     }
+    if (D > kNormRegMaxD) {
+        const int64_t P = bwd_blocks(N);  // one row per block at a time
+        if (D <= 8 * kNormBwdThreads)
+            hipLaunchKernelGGL((rms_bwd_wide_kernel<1>), dim3((unsigned)P), dim3(kNormBwdThreads), 0,
+                               (hipStream_t)stream, x, dy, w, rstd, dres, dx, work, N, (int)D);
+        else
+            hipLaunchKernelGGL((rms_bwd_wide_kernel<2>), dim3((unsigned)P), dim3(kNormBwdThreads), 0,
+                               (hipStream_t)stream, x, dy, w, rstd, dres, dx, work, N, (int)D);
+        if (int e = check_launch("rms_norm_bwd")) return e;
+        hipLaunchKernelGGL(rms_dw_reduce_kernel, dim3((D + 7) / 8), dim3(256), 0, (hipStream_t)stream,
+                           (const float*)work, P, (int)D, dw_f32, dw);
+        return check_launch("rms_dw_reduce");
+    }
     const RowShape s = pick_bwd_shape(D);
     const int G = kNormBwdThreads / s.lpr;
     const int64_t P = bwd_blocks((N + G - 1) / G);  // every block gets a row group's worth
-    // one LDS partial row per wave while two blocks' worth fits a CU's 160 KB
-    const int per_wave = (kNormBwdThreads / 64) * D * (int)sizeof(float) <= 64 * 1024;
-    const size_t lds = (size_t)(per_wave ? kNormBwdThreads / 64 : 1) * D * sizeof(float);
-#define FX_CALL(L, V)                                                                          \
-    hipLaunchKernelGGL((rms_bwd_kernel<L, V>), dim3((unsigned)P), dim3(kNormBwdThreads), lds,  \
-                       (hipStream_t)stream, x, dy, w, rstd, dres, dx, work, N, (int)D, per_wave)
-    FX_NORM_DISPATCH(s, FX_CALL)
+    // one LDS partial row per wave (D < 512: 16 KB at most)
+    const size_t lds = (size_t)(kNormBwdThreads / 64) * D * sizeof(float);
+#define FX_CALL(L)                                                                               \
+    hipLaunchKernelGGL((rms_bwd_kernel<L, 1>), dim3((unsigned)P), dim3(kNormBwdThreads), lds,     \
+                       (hipStream_t)stream, x, dy, w, rstd, dres, dx, work, N, (int)D)
+    switch (s.lpr) {
+        case 64: FX_CALL(64); break;
+        case 32: FX_CALL(32); break;
+        case 16: FX_CALL(16); break;
+        default: FX_CALL(8); break;
+    }
 #undef FX_CALL
     if (int e = check_launch("rms_norm_bwd")) return e;
     hipLaunchKernelGGL(rms_dw_reduce_kernel, dim3((D + 7) / 8), dim3(256), 0, (hipStream_t)stream,

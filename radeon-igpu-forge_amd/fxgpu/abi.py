@@ -129,7 +129,7 @@ SIGNATURES = {
                                 c_int64, c_int64, c_int64, c_int32, _P]),
     "fx_linear_fwd_ex": (c_int32, [_P, _P]),
     "fx_gelu_bwd": (c_int32, [_P, _P, _P, c_int64, _P]),
-    "fx_embedding_bwd_workspace": (c_int64, [c_int64, c_int64]),
+    "fx_embedding_bwd_workspace": (c_int64, [c_int64, c_int64, c_int64]),
     "fx_embedding_bwd": (c_int32, [_P, c_int64, _P, c_int64, _P, c_int64, c_int64, _P, _P]),
     "fx_linear_dgrad": (c_int32, [_P, c_int64, _P, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int64, _P]),
     "fx_linear_wgrad_workspace": (c_int64, [c_int64, c_int64, c_int64]),

@@ -2,11 +2,12 @@
 
 ``token_embedding(idx, weight)`` is ``torch.nn.functional.embedding(idx, weight)`` in the
 forward (a row gather of the table); its weight gradient comes from ``fx_embedding_bwd``: a
-deterministic counting sort of the ids and one pass that sums each id's rows of dy in
-increasing position, in fp32, rounded once to bf16.  It stands in for torch's nn.Embedding
-backward behind the reference's ``tok_emb(idx)`` (ml/fxlm/model.py:82,118), which sorts the
-ids and sizes its segment kernels from counts it reads back from the device, so its launches
-depend on the ids; these do not.
+deterministic counting sort of the ids, sums of each id's rows of dy in increasing position
+over segments of 32 sorted slots, and the segments' fp32 sums added in order, rounded once to
+bf16 (no wave sums more than 32 rows, so a skewed id distribution costs no long serial walk).
+It stands in for torch's nn.Embedding backward behind the reference's ``tok_emb(idx)``
+(ml/fxlm/model.py:82,118), which sorts the ids and sizes its segment kernels from counts it
+reads back from the device, so its launches depend on the ids; these do not.
 """
 import torch
 import torch.nn.functional as Fn
@@ -31,8 +32,9 @@ class _TokenEmbedding(torch.autograd.Function):
 
 def embedding_grad(idx, dy, V):
     """(V, D) bf16 weight gradient of an embedding lookup: row v = the sum of the rows of dy
-    (..., D) whose id in idx (same leading shape, int64) is v, summed in increasing position in
-    fp32 and rounded once; zero rows for ids no position has; ids outside [0, V) add nothing."""
+    (..., D) whose id in idx (same leading shape, int64) is v, in fp32 (increasing position
+    within each 32-slot segment of the id-sorted positions, the segments in order), rounded
+    once; zero rows for ids no position has; ids outside [0, V) add nothing."""
     if idx.dtype != torch.int64:
         raise TypeError(f"idx must be int64, got {idx.dtype}")
     if not (idx.is_cuda and dy.is_cuda):
@@ -52,7 +54,7 @@ def embedding_grad(idx, dy, V):
     if n != dy2.shape[0]:
         raise ValueError(f"{n} ids for {dy2.shape[0]} rows of dy")
     grad = torch.empty(V, D, device=dy.device, dtype=torch.bfloat16)
-    nbytes = int(lib().fx_embedding_bwd_workspace(n, V))
+    nbytes = int(lib().fx_embedding_bwd_workspace(n, V, D))
     work = torch.empty(max(1, (nbytes + 3) // 4), device=dy.device, dtype=torch.float32)
     call("fx_embedding_bwd", ptr(ids), n, ptr(dy2), dy2.stride(0), ptr(grad), V, D, ptr(work), stream_of(dy2))
     return grad

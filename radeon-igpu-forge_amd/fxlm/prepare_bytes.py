@@ -5,14 +5,27 @@
 Front end of ml/fxlm/prepare_bytes.py:19-99 with the same arguments and outputs:
 ``<out>_train.bin`` / ``<out>_val.bin`` (uint16, one token per byte value) and
 ``<out>.json`` {vocab_size: 256, tokenizer: "bytes", n_train, n_val, n_files}, written by
-``fxlm.train.write_byte_tokens``.  Directories are walked for the ``--ext`` suffixes;
-files whose first 8 KB hold a NUL byte are skipped as binary; ``--max-bytes`` truncates
-the concatenation.  Needs numpy and the standard library only (no GPU, no torch).
+``fxlm.train.write_byte_tokens``.  Needs numpy and the standard library only (no GPU, no
+torch).  The rules the token files follow:
+
+* inputs are taken in the order given; a directory contributes the files under it whose
+  lower-cased name ends with one of the ``--ext`` suffixes, a pattern that matches
+  something contributes its matches in sorted order, anything else is taken as a file name;
+  names that are not existing regular files are dropped;
+* a directory is walked top-down, each directory's files before its subdirectories, files
+  and subdirectories each in sorted name order.  The reference takes os.walk's listing order
+  (ml/fxlm/prepare_bytes.py:38-41), which is whatever the file system returns; sorting makes
+  the token files the same on every machine, and equal to the reference's wherever its
+  listing happens to be sorted;
+* a file whose first 8 KiB hold a NUL byte, or that cannot be read, is skipped (and counted);
+* the kept files' bytes are concatenated in that order and cut at ``--max-bytes`` (0: no cut).
 """
 import argparse
 import glob
 import os
 import sys
+
+PROBE_BYTES = 8192  # the binary test looks for a NUL byte in this many leading bytes
 
 
 def build_parser():
@@ -27,56 +40,68 @@ def build_parser():
     return ap
 
 
+def _walk(top, exts):
+    """Files under `top` whose lower-cased name ends with one of `exts`, in the sorted
+    top-down order described in the module docstring."""
+    stack = [top]
+    while stack:
+        here = stack.pop()
+        try:
+            entries = sorted(os.scandir(here), key=lambda e: e.name)
+        except OSError:
+            continue
+        subdirs = []
+        for e in entries:
+            if e.is_dir(follow_symlinks=True):
+                if not e.is_symlink():  # as os.walk: links to directories are not followed
+                    subdirs.append(e.path)
+            elif e.name.lower().endswith(exts):
+                yield e.path
+        stack.extend(reversed(subdirs))  # the first subdirectory is walked next
+
+
 def collect_files(inputs, exts):
-    """Files named by `inputs`: directories walked for `exts` (lower-case suffixes), globs
-    expanded in sorted order, plain names kept; only existing regular files remain."""
-    files = []
-    for pat in inputs:
-        if os.path.isdir(pat):
-            for root, _dirs, names in os.walk(pat):
-                for n in sorted(names):
-                    if n.lower().endswith(exts):
-                        files.append(os.path.join(root, n))
-        else:
-            hits = sorted(glob.glob(pat))
-            files += hits if hits else [pat]
-    return [f for f in files if os.path.isfile(f)]
+    """The candidate files named by `inputs` (directories, glob patterns or names), in input
+    order; only existing regular files are returned."""
+    out = []
+    for spec in inputs:
+        if os.path.isdir(spec):
+            out.extend(_walk(spec, exts))
+            continue
+        matches = sorted(glob.glob(spec))
+        out.extend(matches or [spec])
+    return [p for p in out if os.path.isfile(p)]
+
+
+def _is_text(path):
+    """True for a readable file with no NUL byte in its first PROBE_BYTES; False otherwise."""
+    try:
+        with open(path, "rb") as fh:
+            return b"\x00" not in fh.read(PROBE_BYTES)
+    except OSError:
+        return False
 
 
 def text_files(files):
-    """(kept, skipped): files whose first 8 KB contain no NUL byte, and the count of the
-    others (binary or unreadable)."""
-    kept, skipped = [], 0
-    for f in files:
-        try:
-            with open(f, "rb") as fh:
-                head = fh.read(8192)
-        except OSError:
-            skipped += 1
-            continue
-        if b"\x00" in head:
-            skipped += 1
-        else:
-            kept.append(f)
-    return kept, skipped
+    """(kept, skipped): the files that pass the text test, in order, and how many did not."""
+    kept = [p for p in files if _is_text(p)]
+    return kept, len(files) - len(kept)
 
 
 def read_bytes(files, max_bytes=0):
-    """The files' bytes concatenated in order, cut at max_bytes (0: all of them)."""
-    chunks, total = [], 0
-    for f in files:
+    """The files' contents concatenated in order, cut at max_bytes (0: no cut); a file that
+    cannot be read contributes nothing."""
+    buf = bytearray()
+    for p in files:
+        room = max_bytes - len(buf) if max_bytes else None
+        if room is not None and room <= 0:
+            break
         try:
-            with open(f, "rb") as fh:
-                data = fh.read()
+            with open(p, "rb") as fh:
+                buf += fh.read() if room is None else fh.read(room)
         except OSError:
             continue
-        if max_bytes and total + len(data) > max_bytes:
-            data = data[:max_bytes - total]
-        chunks.append(data)
-        total += len(data)
-        if max_bytes and total >= max_bytes:
-            break
-    return b"".join(chunks)
+    return bytes(buf)
 
 
 def main(argv=None):

@@ -111,12 +111,14 @@ def test_embedding_bwd_checks_and_workspace(abi):
     assert lib.fx_embedding_bwd(fake, 4, fake, 12, fake, 10, 8, fake, None) == abi.FX_EINVAL
     assert lib.fx_embedding_bwd(fake, -1, fake, 8, fake, 10, 8, fake, None) == abi.FX_EINVAL
     # workspace: per-chunk counts (1024 positions a chunk), offsets, one sum per 256 ids,
-    # ranks and the order, each rounded up to 16 bytes
+    # ranks, the order and the slots' ids, then a head and a tail fp32 row per 32-slot
+    # segment, each rounded up to 16 bytes
     ws = lib.fx_embedding_bwd_workspace
-    assert ws(0, 100) == 0 and ws(5, 0) == 0
-    assert ws(1024, 100) == 400 + 416 + 16 + 2 * 4096
-    assert ws(1025, 100) == 800 + 416 + 16 + 2 * 4112
-    assert ws(16384, 50304) == 16 * 50304 * 4 + (50305 * 4 + 12) + 800 + 2 * 16384 * 4
+    assert ws(0, 100, 8) == 0 and ws(5, 0, 8) == 0 and ws(5, 100, 0) == 0
+    assert ws(1024, 100, 8) == 400 + 416 + 16 + 3 * 4096 + 2 * 32 * 8 * 4
+    assert ws(1025, 100, 8) == 800 + 416 + 16 + 3 * 4112 + 2 * 33 * 8 * 4
+    assert ws(16384, 50304, 768) == (16 * 50304 * 4 + (50305 * 4 + 12) + 800 + 3 * 16384 * 4
+                                     + 2 * 512 * 768 * 4)
 
 
 def test_rms_norm_rejects_misaligned_vectors(abi):
@@ -167,3 +169,21 @@ def test_adamw_workspace_counts_chunks(abi):
         tl.n[i] = n
     # 1 + 2 + 1 chunks of 8192 elements, plus the 4-float header
     assert abi.lib().fx_adamw_workspace(ctypes.byref(tl), 1) == (4 + 4) * 4
+
+
+def test_adamw_noalloc_rejects_lists_beyond_its_scratch(abi):
+    # more chunks than the library's scratch holds: FX_EINVAL before the device is looked up
+    # or anything is launched (the pointers are never dereferenced)
+    lib = abi.lib()
+    fake = 4096
+    tl = abi.fxTensorList()
+    tl.count = 1
+    tl.g[0] = fake
+    tl.n[0] = 300_000 * 8192                        # 300,000 chunks > 262,140
+    st = abi.fxAdamWState()
+    st.master = st.m = st.v = st.p16 = fake
+    st.step = st.found_inf = st.grad_norm = st.scale = st.growth = fake
+    assert lib.fx_adamw_step_noalloc(ctypes.byref(st), ctypes.byref(tl), 1, None) == abi.FX_EINVAL
+    assert b"scratch" in lib.fx_last_error()
+    # the largest list that fits passes this check (and would go on to the device lookup)
+    assert (4 + 262140) * 4 == 1 << 20

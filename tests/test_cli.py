@@ -39,6 +39,31 @@ def test_prepare_bytes_walks_filters_and_truncates(tmp_path):
         pb.main([str(d / "d.py"), "--out", out + "4"])
 
 
+def test_prepare_bytes_directory_order_is_sorted_top_down(tmp_path):
+    # the walk order rule: a directory's files in sorted name order, then its subdirectories
+    # in sorted name order, each walked the same way (top-down, depth first); files are
+    # created in the reverse of that order so that a listing-order walk would differ
+    d = tmp_path / "corpus"
+    want_order = ["A.txt", "b.txt", "z.md", "a/1.txt", "a/y.txt", "a/x/0.md", "a/x/deep/q.txt",
+                  "b/0.txt", "c c/n.md"]
+    for rel in reversed(want_order):
+        f = d / rel
+        f.parent.mkdir(parents=True, exist_ok=True)
+        f.write_bytes(f"<{rel}>".encode())
+    (d / "a" / "skip.bin").write_bytes(b"not walked")
+    got = pb.collect_files([str(d)], (".txt", ".md"))
+    assert [os.path.relpath(p, d).replace(os.sep, "/") for p in got] == want_order
+    out = str(tmp_path / "tok")
+    pb.main([str(d), "--out", out, "--val-frac", "0.05"])
+    toks = np.concatenate([np.fromfile(out + "_train.bin", dtype=np.uint16),
+                           np.fromfile(out + "_val.bin", dtype=np.uint16)])
+    assert toks.astype(np.uint8).tobytes() == b"".join(f"<{r}>".encode() for r in want_order)
+    # inputs keep their given order; a glob's matches are sorted; the cut is exact
+    g = pb.collect_files([str(d / "b.txt"), str(d / "a" / "*.txt")], (".txt",))
+    assert [os.path.basename(p) for p in g] == ["b.txt", "1.txt", "y.txt"]
+    assert pb.read_bytes(g, max_bytes=9) == b"<b.txt><a"
+
+
 def test_train_lm_refuses_bad_arguments(tmp_path):
     p = train_lm.build_parser()
     with pytest.raises(SystemExit, match="tokens per micro-step"):

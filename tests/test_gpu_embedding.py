@@ -1,7 +1,9 @@
 """fx_embedding_bwd (the GPT's token-embedding gradient) against the oracle, through the C ABI.
 
-The kernel sums each id's rows of dy in increasing position in fp32 and rounds once, which is
-exactly oracle.embedding.embedding_grad_seq, so the comparison is bitwise."""
+The kernel sums each id's rows of dy in fp32 in increasing position within 32-slot segments of
+the id-sorted positions and adds the segment sums in order, rounding once: exactly
+oracle.embedding.embedding_grad_seq, so the comparison is bitwise.  Skewed id distributions
+(one id at most positions, Zipf ids, byte-level text) split long runs over many segments."""
 import pytest
 import torch
 
@@ -35,6 +37,49 @@ def test_matches_position_ordered_sum(n, V, D, lo, same, ld):
     torch.cuda.synchronize()
     assert got.shape == (V, D) and got.dtype == torch.bfloat16
     assert torch.equal(got.cpu(), ref)
+
+
+def _zipf_ids(n, V, seed, a=1.1):
+    g = torch.Generator().manual_seed(seed)
+    p = 1.0 / torch.arange(1, V + 1, dtype=torch.float64) ** a
+    return torch.multinomial(p / p.sum(), n, replacement=True, generator=g)
+
+
+@pytest.mark.parametrize("kind", ["zipf_50304", "bytes_256", "one_id_16384", "two_ids"])
+def test_skewed_ids(kind):
+    from fxlm.embedding import embedding_grad
+    g = torch.Generator().manual_seed(21)
+    if kind == "zipf_50304":
+        V, D, idx = 50304, 768, _zipf_ids(16384, 50304, 4)
+    elif kind == "bytes_256":
+        # byte-level English-like text: the space and a few letters hold most positions
+        V, D = 256, 768
+        text = (b"the quick brown fox jumps over the lazy dog and then some more words " * 300)[:16384]
+        idx = torch.tensor(list(text), dtype=torch.int64)
+    elif kind == "one_id_16384":
+        V, D, idx = 1000, 64, torch.full((16384,), 17, dtype=torch.int64)
+    else:
+        V, D = 3, 32
+        idx = torch.randint(0, 2, (5000,), generator=g)
+    rows = torch.randn(idx.numel(), D, generator=g).bfloat16()
+    got = embedding_grad(idx.cuda(), rows.cuda(), V)
+    assert torch.equal(got.cpu(), oemb.embedding_grad_seq(idx, rows, V))
+
+
+@pytest.mark.parametrize("at_one,lead,want", [(31, 0, 0.0), (32, 0, 1.0), (12, 20, 1.0), (11, 20, 0.0)])
+def test_segment_cut_matches_the_oracle_rule(at_one, lead, want):
+    # 2^24 + 1 rounds to 2^24 in fp32: the sum is 0 or the exact 1 depending on which side of a
+    # global 32-slot boundary the 1 falls (the oracle's rule, pinned on the CPU)
+    from fxlm.embedding import embedding_grad
+    n = 64 if lead == 0 else 40
+    dy = torch.zeros(lead + n, 8).bfloat16()
+    dy[lead, 0] = 2.0 ** 24
+    dy[lead + at_one, 0] = 1.0
+    dy[lead + at_one + 1, 0] = -(2.0 ** 24)
+    idx = torch.tensor([0] * lead + [1] * n)
+    got = embedding_grad(idx.cuda(), dy.cuda(), 2)
+    assert float(got[1, 0]) == want
+    assert torch.equal(got.cpu(), oemb.embedding_grad_seq(idx, dy, 2))
 
 
 def test_deterministic_and_leading_shape():
@@ -86,7 +131,7 @@ def test_workspace_and_output_contents_do_not_matter():
     from fxgpu.abi import call, lib, ptr, stream_of
     idx, rows = _case(5000, 600, 48, lo=-2, seed=9)
     ids, dy = idx.cuda(), rows.cuda()
-    nbytes = int(lib().fx_embedding_bwd_workspace(5000, 600))
+    nbytes = int(lib().fx_embedding_bwd_workspace(5000, 600, 48))
     ref = oemb.embedding_grad_seq(idx, rows, 600)
     for fill in (-1, 0x3F800000, 7):
         work = torch.full(((nbytes + 3) // 4,), fill, dtype=torch.int32, device="cuda")

@@ -441,6 +441,70 @@ def test_cpu_gpt_initial_loss_and_learning():
     assert l1 < 0.9 * l0
 
 
+def test_cpu_optimizer_decays_matrices_only():
+    # zero gradients: Adam's moments stay zero, so the step is exactly the decoupled weight
+    # decay, p * (1 - lr wd) on >= 2-D parameters and nothing on the 1-D ones (norm weights,
+    # the reference's wd groups, ml/bench/bench10_lm.py:92-99); decay on every parameter, or
+    # on none, fails here
+    torch.manual_seed(3)
+    m = ogpt.GPT(vocab_size=64, seq_len=16, n_layer=2, n_head=2, d_model=32)
+    lr, wd = 3e-3, 0.1
+    opt = ogpt.make_optimizer(m, lr=lr, weight_decay=wd)
+    before = {n: p.detach().clone() for n, p in m.named_parameters()}
+    for p in m.parameters():
+        p.grad = torch.zeros_like(p)
+    opt.step()
+    ndim1 = ndim2 = 0
+    for n, p in m.named_parameters():
+        if p.dim() >= 2:
+            assert torch.equal(p.detach(), before[n] * (1 - lr * wd)), n
+            ndim2 += 1
+        else:
+            assert torch.equal(p.detach(), before[n]), n
+            ndim1 += 1
+    assert ndim1 >= 5 and ndim2 >= 5     # both groups are populated
+
+
+class _Bilinear(torch.nn.Module):
+    """loss = sum(w * x) + sum(b * y): the gradients are exactly x and y."""
+
+    def __init__(self):
+        super().__init__()
+        self.w = torch.nn.Parameter(torch.full((4, 4), 0.5))
+        self.b = torch.nn.Parameter(torch.full((4,), -0.25))
+
+    def forward(self, x, y):
+        return (self.w * x).sum() + (self.b * y).sum()
+
+
+def test_cpu_train_step_clips_the_global_norm_to_one():
+    # a gradient of norm 4 is clipped to norm 1 before AdamW sees it
+    # (ml/bench/bench10_lm.py:104-111: clip_grad_norm_(1.0) then step): two steps, the first
+    # of norm 4 and the second of norm 1/2 (left alone), end where the same steps with the
+    # first gradient scaled to norm 1 end.  Unclipped, Adam's moments weigh the two steps
+    # differently and the parameters end elsewhere.
+    g = torch.Generator().manual_seed(8)
+    x1, y1 = torch.randn(4, 4, generator=g), torch.randn(4, generator=g)
+    n1 = math.sqrt(float((x1 ** 2).sum() + (y1 ** 2).sum()))
+    x1, y1 = x1 * (4 / n1), y1 * (4 / n1)
+    x2, y2 = torch.randn(4, 4, generator=g), torch.randn(4, generator=g)
+    n2 = math.sqrt(float((x2 ** 2).sum() + (y2 ** 2).sum()))
+    x2, y2 = x2 * (0.5 / n2), y2 * (0.5 / n2)
+
+    def run(steps, clip):
+        mod = _Bilinear()
+        opt = ogpt.make_optimizer(mod, lr=1e-2, weight_decay=0.1)
+        for x, y in steps:
+            ogpt.cpu_train_step(mod, opt, x, y, clip=clip)
+        return torch.cat([mod.w.detach().reshape(-1), mod.b.detach()])
+
+    clipped = run([(x1, y1), (x2, y2)], 1.0)
+    prescaled = run([(x1 / 4, y1 / 4), (x2, y2)], 1.0)
+    unclipped = run([(x1, y1), (x2, y2)], 1e9)
+    assert torch.allclose(clipped, prescaled, rtol=1e-5, atol=1e-7)
+    assert float((unclipped - prescaled).abs().max()) > 1e-4
+
+
 def test_gather_windows_against_unfold_and_outside_zero():
     # in-range windows are the window-major unfold of X; a window leaving X is zeros
     from oracle.linear import gather
@@ -487,16 +551,47 @@ def test_embedding_grad_seq_is_the_position_ordered_fp32_sum():
     # within one bf16 rounding plus the fp32 accumulation of up to n terms
     bound = 2.0 ** -8 * exact.abs() + n * 2.0 ** -24 * oemb.embedding_grad(idx, dy.abs(), V) + 1e-30
     assert bool(((seq.double() - exact).abs() <= bound).all())
-    acc = torch.zeros(V, D, dtype=torch.float32)
-    for t in range(n):
-        v = int(idx[t])
-        if 0 <= v < V:
-            acc[v] += dy[t].float()
-    assert torch.equal(seq, acc.bfloat16())
-    # the order is position order: 2^24 + 1 rounds back to 2^24 in fp32, so the three terms
-    # below sum to 0 forwards, where the exact sum (or the reverse order) is 1
-    dy3 = torch.zeros(3, 8).bfloat16()
-    dy3[:, 0] = torch.tensor([2.0 ** 24, 1.0, -(2.0 ** 24)])
-    idx3 = torch.zeros(3, dtype=torch.int64)
-    assert float(oemb.embedding_grad_seq(idx3, dy3, 1)[0, 0]) == 0.0
-    assert float(oemb.embedding_grad(idx3, dy3, 1)[0, 0]) == 1.0
+    # where every id's run is one whole segment (32 positions each, ids in any position
+    # order), the result is the plain position-ordered fp32 sum
+    perm = torch.randperm(32 * 5, generator=g)
+    idx5 = (torch.arange(32 * 5) // 32)[perm]
+    dy5 = torch.randn(32 * 5, D, generator=g).bfloat16()
+    acc = torch.zeros(5, D, dtype=torch.float32)
+    for t in range(32 * 5):
+        acc[int(idx5[t])] += dy5[t].float()
+    assert torch.equal(oemb.embedding_grad_seq(idx5, dy5, 5), acc.bfloat16())
+
+
+def _big_small(n, at_one, lead=0):
+    """n rows of id 1 after `lead` rows of id 0: 2^24 at id 1's first row, 1 at its row
+    `at_one`, -2^24 right after, zeros elsewhere (column 0; the other columns zero)."""
+    dy = torch.zeros(lead + n, 8).bfloat16()
+    dy[lead, 0] = 2.0 ** 24
+    dy[lead + at_one, 0] = 1.0
+    dy[lead + at_one + 1, 0] = -(2.0 ** 24)
+    idx = torch.tensor([0] * lead + [1] * n)
+    return idx, dy
+
+
+def test_embedding_grad_seq_cuts_runs_at_global_32_slot_segments():
+    # 2^24 + 1 rounds back to 2^24 in fp32, so whether the 1 meets 2^24 or -2^24 first
+    # decides between a sum of 0 and the exact 1
+    # the 1 in the first segment (slot 31): 2^24 + 1 -> 2^24, then -2^24 in the next: 0
+    idx, dy = _big_small(64, 31)
+    assert float(oemb.embedding_grad_seq(idx, dy, 2)[1, 0]) == 0.0
+    # the 1 opens the second segment (slot 32): 1 - 2^24 is exact there, and 2^24 plus that
+    # is 1; a position-ordered sum over the whole run would give 0
+    idx, dy = _big_small(64, 32)
+    assert float(oemb.embedding_grad_seq(idx, dy, 2)[1, 0]) == 1.0
+    assert float(oemb.embedding_grad(idx, dy, 2)[1, 0]) == 1.0
+    # segments are counted in global slots: after 20 slots of id 0, id 1's 13th row (index 12)
+    # is slot 32; cutting at id 1's own 32nd row instead would give 0
+    idx, dy = _big_small(40, 12, lead=20)
+    assert float(oemb.embedding_grad_seq(idx, dy, 2)[1, 0]) == 1.0
+    idx, dy = _big_small(40, 11, lead=20)
+    assert float(oemb.embedding_grad_seq(idx, dy, 2)[1, 0]) == 0.0
+    # ids outside [0, V) take no slot: 20 of them in front change nothing
+    idx, dy = _big_small(64, 32)
+    idx = torch.cat([torch.full((20,), -5), idx])
+    dy = torch.cat([torch.ones(20, 8).bfloat16(), dy])
+    assert float(oemb.embedding_grad_seq(idx, dy, 2)[1, 0]) == 1.0
