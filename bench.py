@@ -441,6 +441,36 @@ def bench_wgrad(torch):
     return out
 
 
+def bench_wgrad_step(torch, rounds=12):
+    """For profiler runs: the cfg5 step's 48 layer weight gradients (12 rounds of the qkv,
+    proj, fc and fc2 products over 16384 tokens) after a warm-up round, so that per-dispatch
+    averages weigh the four shapes as the step does."""
+    from fxgpu.fused_linear import linear_wgrad
+    T = 16384
+    g = torch.Generator(device="cuda").manual_seed(8)
+    ops = []
+    for M, N in ((2304, 768), (768, 768), (3072, 768), (768, 3072)):
+        ops.append((torch.randn(T, M, device="cuda", generator=g).bfloat16(),
+                    torch.randn(T, N, device="cuda", generator=g).bfloat16()))
+    for dy, x in ops:
+        linear_wgrad(dy, x)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(rounds):
+        for dy, x in ops:
+            linear_wgrad(dy, x)
+    torch.cuda.synchronize()
+    return {"launches": 4 * rounds, "wall_us_per_launch": round((time.perf_counter() - t0) / (4 * rounds) * 1e6, 2)}
+
+
+def wgrad_roofline(wg):
+    """fx_linear_wgrad over the step's four layer shapes (each 12 times per step): algorithmic
+    FLOPs 2 T M N per product, over the measured launch times (kernel plus split-K reduce)."""
+    flop = sum(2.0 * v["shape_TMN"][0] * v["shape_TMN"][1] * v["shape_TMN"][2] for v in wg.values())
+    us = sum(v["us"] for v in wg.values())
+    return flop / len(wg), us / len(wg)
+
+
 def bench_head(torch):
     """The cfg5 tied head, linear_cross_entropy over x (16384, 768) and E (50304, 768): the
     unfused chunk loop (library logits GEMM, fx_ce_fwd_grad, dx and dW GEMMs) against the
@@ -678,6 +708,10 @@ def bench_fc_product(torch, which, cold):
 
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "attn_bwd_cfg2_traffic.json")
 _TRAFFIC_KERNELS = ("attn_bwd_dq_kernel", "attn_bwd_dkv_kernel")
+# fx_linear_wgrad: the whole-tile kernel and its split-K reduce, averaged over the step's
+# 48 layer products (bench.py --only wgrad-step runs each of the four shapes equally often)
+WGRAD_TRAFFIC_JSON = os.path.join(ROOT, "profiles", "wgrad_cfg5_traffic.json")
+_WGRAD_TRAFFIC_KERNELS = ("gemm_wgrad_fast_kernel", "wgrad_reduce_kernel")
 
 
 def _pmc_per_dispatch(csv_path, counter, name_filter):
@@ -696,16 +730,18 @@ def _pmc_per_dispatch(csv_path, counter, name_filter):
     return sum(vals.values()) / len(vals), len(vals)
 
 
-def pmc_summary(fetch_csv, write_csv, copy_fetch_csv, copy_write_csv):
-    """HBM bytes per fx_attn_bwd launch from FETCH_SIZE / WRITE_SIZE (KiB per dispatch),
-    each scaled by what the counter reads for torch's 1 GiB copy (known bytes)."""
+def pmc_summary(fetch_csv, write_csv, copy_fetch_csv, copy_write_csv, kernels=_TRAFFIC_KERNELS):
+    """HBM bytes per launch of an entry point made of `kernels` (one dispatch of each per
+    launch: fx_attn_bwd's two, or fx_linear_wgrad's kernel and reduce) from FETCH_SIZE /
+    WRITE_SIZE (KiB per dispatch), each scaled by what the counter reads for torch's 1 GiB
+    copy (known bytes)."""
     known = 1 << 30
     cf, _ = _pmc_per_dispatch(copy_fetch_csv, "FETCH_SIZE", "copy")
     cw, _ = _pmc_per_dispatch(copy_write_csv, "WRITE_SIZE", "copy")
     sf, sw = known / (cf * 1024.0), known / (cw * 1024.0)
     out = {"scale_fetch": sf, "scale_write": sw, "kernels": {}}
     tot = 0.0
-    for k in _TRAFFIC_KERNELS:
+    for k in kernels:
         f, nf = _pmc_per_dispatch(fetch_csv, "FETCH_SIZE", k)
         w, nw = _pmc_per_dispatch(write_csv, "WRITE_SIZE", k)
         fb, wb = f * 1024.0 * sf, w * 1024.0 * sw
@@ -761,19 +797,28 @@ def counter_table(csv_paths, top=12):
     return "\n".join(lines)
 
 
-def trace_table(trace_csv, per_step=None, skip=2, top=40):
+def trace_table(trace_csv, per_step=None, skip=2, top=40, last=None):
     """Per-kernel durations from a rocprofv3 --kernel-trace kernel_trace.csv as a markdown
     table.  With per_step (a kernel name fragment that runs once per training step, e.g. the
     CE row kernel), only the windows between consecutive dispatches of that kernel count,
     after `skip` windows: each holds one step's kernels, and the table is per step, with the
-    span (first start to last end) beside the summed kernel time."""
+    span (first start to last end) beside the summed kernel time.  With `last`, only the last
+    `last` dispatches of each kernel count: the timed rounds of a bench.py kernel line (5 x 20
+    launches after the warm-up ones, whose early launches run before the clocks ramp up)."""
     import csv
     rows = []
     with open(trace_csv) as f:
         for r in csv.DictReader(f):
             rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
     rows.sort()
-    note = f"{len(rows)} dispatches"
+    if last:
+        seen, keep = {}, []
+        for r in reversed(rows):
+            seen[r[2]] = seen.get(r[2], 0) + 1
+            if seen[r[2]] <= last:
+                keep.append(r)
+        rows = keep[::-1]
+    note = f"{len(rows)} dispatches" + (f" (the last {last} of each kernel)" if last else "")
     if per_step:
         marks = [i for i, (_, _, k) in enumerate(rows) if per_step in k]
         wins = list(zip(marks[skip:], marks[skip + 1:]))
@@ -844,9 +889,9 @@ def traffic_table(fetch_csv, write_csv, copy_fetch_csv, copy_write_csv, top=12):
     return "\n".join(lines)
 
 
-def _traffic():
+def _traffic(path=TRAFFIC_JSON):
     try:
-        with open(TRAFFIC_JSON) as f:
+        with open(path) as f:
             return round(json.load(f)["traffic_bytes_per_launch"])
     except (OSError, KeyError, ValueError):
         return None
@@ -860,18 +905,24 @@ def main():
     # so that no batch's first step (and no first allocation of a size) falls in the timed steps
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU baseline")
-    ap.add_argument("--only", choices=["attention", "ce", "norm", "adamw", "linear", "wgrad", "head", "library", "step", "copy",
+    ap.add_argument("--only", choices=["attention", "ce", "norm", "adamw", "linear", "wgrad", "wgrad-step", "head",
+                                       "library", "step", "copy",
                                        "decode", "embedding",
                                        "cpu", "fc-ours", "fc-library", "fc-ours-cold", "fc-library-cold"],
                     help="run one workload and print its figures (for profiling runs)")
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV",
                                                        "COPY_WRITE_CSV"),
                     help="write the fx_attn_bwd HBM traffic from rocprofv3 --pmc csv files")
+    ap.add_argument("--pmc-summary-wgrad", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV",
+                                                             "COPY_WRITE_CSV"),
+                    help="write the fx_linear_wgrad HBM traffic (bench.py --only wgrad-step runs)")
     ap.add_argument("--counter-table", nargs="+", metavar="CSV",
                     help="print per-kernel counter averages from rocprofv3 --pmc csv files")
     ap.add_argument("--trace-table", nargs="+", metavar=("TRACE_CSV", "PER_STEP_KERNEL"),
                     help="print per-kernel durations from a rocprofv3 --kernel-trace csv (per step when a "
                          "once-per-step kernel name is given)")
+    ap.add_argument("--trace-last", type=int, default=None, metavar="N",
+                    help="--trace-table: only the last N dispatches of each kernel (bench.py's timed rounds: 100)")
     ap.add_argument("--traffic-table", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV",
                                                          "COPY_WRITE_CSV"),
                     help="print per-kernel HBM bytes from FETCH_SIZE / WRITE_SIZE passes")
@@ -883,11 +934,14 @@ def main():
         print(traffic_table(*args.traffic_table))
         return
     if args.trace_table:
-        print(trace_table(args.trace_table[0], args.trace_table[1] if len(args.trace_table) > 1 else None))
+        print(trace_table(args.trace_table[0], args.trace_table[1] if len(args.trace_table) > 1 else None,
+                          last=args.trace_last))
         return
-    if args.pmc_summary:
-        res = pmc_summary(*args.pmc_summary)
-        with open(TRAFFIC_JSON, "w") as f:
+    if args.pmc_summary or args.pmc_summary_wgrad:
+        wg = bool(args.pmc_summary_wgrad)
+        res = pmc_summary(*(args.pmc_summary_wgrad if wg else args.pmc_summary),
+                          kernels=_WGRAD_TRAFFIC_KERNELS if wg else _TRAFFIC_KERNELS)
+        with open(WGRAD_TRAFFIC_JSON if wg else TRAFFIC_JSON, "w") as f:
             json.dump(res, f, indent=1)
         print(json.dumps(res))
         return
@@ -900,7 +954,8 @@ def main():
     lib()
     if args.only:
         fn = {"attention": bench_attention, "ce": bench_ce, "norm": bench_norm, "adamw": bench_adamw,
-              "linear": bench_linear, "wgrad": bench_wgrad, "head": bench_head, "copy": bench_copy,
+              "linear": bench_linear, "wgrad": bench_wgrad, "wgrad-step": bench_wgrad_step,
+              "head": bench_head, "copy": bench_copy,
               "library": bench_library,
               "decode": bench_decode, "embedding": bench_embedding,
               "cpu": cpu_baseline,
@@ -934,15 +989,25 @@ def main():
     step = gpu_step_bench(torch, args.steps, args.warmup)
     torch.cuda.empty_cache()
 
+    # the dominant kernel of the step among this build's own: fx_linear_wgrad (48 launches,
+    # ~3.3 ms of the step's kernel time against ~1.75 ms for the attention backward), per
+    # average launch of the step's mix; the attention figures stay under kernels
+    wf, wus = wgrad_roofline(wg)
     roofline = {
-        "kernel": "fx_attn_bwd (attn_bwd_dq + attn_bwd_dkv), cfg2 [16,12,1024,64] causal",
-        "bound": "mfma", "achieved": round(attn["flop_bwd"] / attn["bwd_us"] / 1e6, 1),
+        "kernel": "fx_linear_wgrad (gemm_wgrad_fast_kernel<3> + wgrad_reduce), the cfg5 step's layer "
+                  "weight gradients dW = dy^T x over 16384 tokens (qkv, proj, fc, fc2), per average launch",
+        "bound": "mfma", "achieved": round(wf / wus / 1e6, 1),
         "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-        "frac": round(attn["flop_bwd"] / attn["bwd_us"] / 1e6 / BF16_PEAK_TFLOPS, 4),
-        # HBM bytes per fx_attn_bwd launch: rocprofv3 FETCH_SIZE + WRITE_SIZE of the two
-        # kernels, calibrated on a copy of known size (profiles/attn_bwd_cfg2_traffic.*)
-        "traffic": _traffic(),
+        "frac": round(wf / wus / 1e6 / BF16_PEAK_TFLOPS, 4),
+        # HBM bytes per average launch: rocprofv3 FETCH_SIZE + WRITE_SIZE of the kernel and
+        # its reduce, calibrated on a copy of known size (profiles/wgrad_cfg5_traffic.*)
+        "traffic": _traffic(WGRAD_TRAFFIC_JSON),
+        "flop_per_launch": round(wf),
     }
+    attn_roof = {"kernel": "fx_attn_bwd (attn_bwd_dq + attn_bwd_dkv), cfg2 [16,12,1024,64] causal",
+                 "achieved": round(attn["flop_bwd"] / attn["bwd_us"] / 1e6, 1),
+                 "frac": round(attn["flop_bwd"] / attn["bwd_us"] / 1e6 / BF16_PEAK_TFLOPS, 4),
+                 "traffic": _traffic()}
     cpu = None if args.no_cpu else cpu_baseline(torch)
     out = {
         "metric": "train tokens/sec (GPT 12L-d768, S=1024) + attn fwd/bwd TFLOPS, % roofline",
@@ -957,7 +1022,8 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "gpu_over_cpu": (round(step["tok_s"] / cpu["value"], 1) if cpu else None),
-        "kernels": {"attention_cfg2": {k: v for k, v in attn.items() if not k.startswith("flop")},
+        "kernels": {"attention_cfg2": dict({k: v for k, v in attn.items() if not k.startswith("flop")},
+                                           bwd_roofline=attn_roof),
                     "cross_entropy_cfg3": ce, "rmsnorm_cfg4": norm, "flat_adamw_cfg4": adamw,
                     "fused_linear_gelu_cfg5_fc": lin, "linear_wgrad_cfg5": wg,
                     "linear_ce_head_cfg5": head, "decode": dec,

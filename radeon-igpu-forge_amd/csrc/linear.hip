@@ -373,6 +373,7 @@ struct TileSrc {
     int cols;
     uint64_t step;
     int rmax = 1 << 30;  // row operand: tile rows past this one load this row (a ragged last tile)
+    int cmax = 1 << 30;  // col operand: 8-column chunks past this one load this chunk (a ragged last tile)
 };
 
 __device__ __forceinline__ const uint16_t* slot_addr(const TileSrc& t, int s) {
@@ -384,7 +385,7 @@ __device__ __forceinline__ const uint16_t* slot_addr(const TileSrc& t, int s) {
     const int r = s / spr;
     int c = s - spr * r;
     if (c >= t.cols / 8) c -= t.cols / 8;
-    return t.base + (int64_t)r * t.ld + 8 * c;
+    return t.base + (int64_t)r * t.ld + 8 * min(c, t.cmax);
 }
 
 // Load pointers, their strides and the prologue: wave-instruction q = wave + 4 t of a stage
@@ -1051,7 +1052,7 @@ __global__ void __launch_bounds__(256, 1) gemm_wgrad_fast_kernel(WgradArgs a) {
     constexpr int L = G::kLoads;
     __shared__ __attribute__((aligned(16))) unsigned char lds[kAsmStages * G::kStage];
     const int nn = a.N / (64 * NJ);
-    const int ntiles = (a.M / 256) * nn;
+    const int ntiles = ((a.M + 255) / 256) * nn;  // the last row panel may be partial (M % 256 != 0)
     const int sl = blockIdx.x / ntiles, t = blockIdx.x - sl * ntiles;
     const int m0 = (t / nn) * 256, n0 = (t - (t / nn) * nn) * 64 * NJ;
     const int nk64 = (a.K + 63) / 64;
@@ -1063,7 +1064,8 @@ __global__ void __launch_bounds__(256, 1) gemm_wgrad_fast_kernel(WgradArgs a) {
     const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(lds));
     uint32_t phase, iters;
     asm_gemm_schedule(nsteps, phase, iters);
-    const TileSrc ms{a.A + (int64_t)t0 * a.lda + m0, a.lda, true, 256, (uint64_t)a.lda * 64};
+    TileSrc ms{a.A + (int64_t)t0 * a.lda + m0, a.lda, true, 256, (uint64_t)a.lda * 64};
+    ms.cmax = (min(256, a.M - m0) >> 3) - 1;  // columns past M load the last chunk (never stored)
     const TileSrc ns{a.B + (int64_t)t0 * a.ldb + n0, a.ldb, true, 64 * NJ, (uint64_t)a.ldb * 64};
     uint64_t P[L], S[L];
     if constexpr (NJ == 4)
@@ -1102,6 +1104,7 @@ __global__ void __launch_bounds__(256, 1) gemm_wgrad_fast_kernel(WgradArgs a) {
                 const int64_t row0 = m0 + wm + 32 * i;
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
+                    if (row0 + 8 * (e >> 2) + (e & 3) + 4 * g >= a.M) continue;  // past a ragged last panel
                     auto* o = out + (row0 + 8 * (e >> 2) + (e & 3)) * ldo + n0;
                     if constexpr (sizeof(*out) == 4)
                         o[voff] = acc[4 * j + i][e];
@@ -1465,7 +1468,8 @@ extern "C" int fx_linear_fwd_ex(const fxLinearArgs* args, void* stream) {
 // The weight gradient's plan: the tile width (0: the general kernel's 256 x 256 tiles, or
 // the whole-tile kernel's 256 x 64 NJ) and the K split.  Slices: at least 4 K steps of 64
 // tokens each, at most 32, and no more workgroups than CUs (one workgroup per CU).  The
-// whole-tile kernel takes M % 256 == 0, N % (64 NJ) == 0, K % 32 == 0, K >= 128.  With
+// whole-tile kernel takes N % (64 NJ) == 0, K % 32 == 0, K >= 128 (any M, a partial last
+// 256-row panel clamped on load and masked on store).  With
 // FX_GEMM_GENERAL selecting the general kernel the slices stay those of the whole-tile plan,
 // so the two produce the same partials.  256 x 192 tiles wherever N % 192 == 0: more tiles,
 // hence fewer slices and less fp32 partial traffic (5 slices instead of 7 at the cfg5 fc
@@ -1480,11 +1484,14 @@ static WgradPlan wgrad_plan(int64_t M, int64_t N, int64_t K) {
     WgradPlan p{0, 1, false};
     const char* tw = getenv("FX_WGRAD_TILE");
     const bool want4 = tw && tw[0] == '2' && tw[1] == '5' && tw[2] == '6';
-    if (M % 256 == 0 && K % 32 == 0 && K >= 32 * kAsmStages) {
+    // M need not divide into whole 256-row panels: the last panel's loads are clamped and its
+    // rows past M are not stored (the tied head's (50304, 768) gradient has a half panel)
+    if (K % 32 == 0 && K >= 32 * kAsmStages) {
         if (!want4 && N % 192 == 0) p.nj = 3;
         else if (N % 256 == 0) p.nj = 4;
     }
-    const int64_t tiles = p.nj ? (M / 256) * (N / (64 * p.nj)) : ((M + kGBM - 1) / kGBM) * ((N + kGBN - 1) / kGBN);
+    const int64_t tiles = p.nj ? ((M + 255) / 256) * (N / (64 * p.nj))
+                               : ((M + kGBM - 1) / kGBM) * ((N + kGBN - 1) / kGBN);
     const int64_t nk = (K + kWBK - 1) / kWBK;
     int64_t s = device_cus() / tiles;
     if (s > nk / 4) s = nk / 4;
@@ -1532,7 +1539,7 @@ extern "C" int fx_linear_wgrad(const uint16_t* dY, int64_t ldy, const uint16_t* 
     // whole tiles and 32-token steps, every slice at least 4 steps: the generated loop (with
     // several slices each spans at least 4 64-token steps, the last perhaps 32 tokens short)
     if (plan.fast) {
-        const int64_t tiles = (M / 256) * (N / (64 * plan.nj));
+        const int64_t tiles = ((M + 255) / 256) * (N / (64 * plan.nj));
         if (plan.nj == 4)
             hipLaunchKernelGGL(gemm_wgrad_fast_kernel<4>, dim3((unsigned)(tiles * slices)), dim3(256), 0, s, a);
         else

@@ -24,6 +24,7 @@ import ctypes
 import torch
 
 from fxgpu.abi import call, fxCEArgs, lib, ptr, stream_of
+from fxgpu.fused_linear import linear_wgrad
 
 # rows per linear-CE chunk: bound the chunk's bf16 logits to this many bytes
 _CHUNK_BYTES = 2 << 30
@@ -76,6 +77,11 @@ def _finalize(row_loss, inv_n):
 # fx_ce_fwd_grad, so on MI355X it is the slower of the two at the cfg5 head.
 FUSED_LINEAR_CE_LOSS = True
 FUSED_LINEAR_CE_TRAIN = False
+# True: the head's weight gradient lg^T x on this build's weight-gradient GEMM
+# (fx_linear_wgrad: 256 x 192 tiles, a partial last row panel at V = 50304, one K slice).
+# Off: at the cfg5 head its 788 tiles take four rounds of 256 CUs for 3.08 rounds of work,
+# 1376 against 1302 us for torch.mm (hipBLASLt), and the step 18.18 against 18.03 ms.
+NATIVE_HEAD_WGRAD = False
 
 
 def _lce_fused_ok(x, weight):
@@ -213,7 +219,7 @@ class _LinearCE(torch.autograd.Function):
             # the reference's dW.add_(torch.mm(dl.t(), xc).float()): a bf16 product,
             # accumulated over the chunks in fp32 (ml/fxlm/cross_entropy.py:135); a single
             # chunk's product stays bf16 (exact in fp32) and the backward reads it as such
-            part = torch.mm(lg.t(), xc)                         # (V, D) bf16
+            part = linear_wgrad(lg, xc) if NATIVE_HEAD_WGRAD else torch.mm(lg.t(), xc)  # (V, D) bf16
             if dW is None:
                 dW = part if r1 >= N else part.float()
             else:

@@ -25,6 +25,20 @@ def _write(path, header, rows):
     return str(path)
 
 
+def test_trace_table_last_dispatches_only(bench, tmp_path):
+    # 5 slow warm-up launches (clocks ramping) then 3 timed ones of 2 us: with last=3 only
+    # the timed ones count
+    rows = [(i * 100, i * 100 + 50_000, "k") for i in range(5)]
+    rows += [(10_000_000 + i * 10_000, 10_000_000 + i * 10_000 + 2_000, "k") for i in range(3)]
+    rows += [(20_000_000, 20_004_000, "other")]
+    p = _write(tmp_path / "t.csv", ["Start_Timestamp", "End_Timestamp", "Kernel_Name"], rows)
+    out = bench.trace_table(p, last=3)
+    line = next(l for l in out.splitlines() if l.startswith("| `k`"))
+    cells = [c.strip() for c in line.strip("|").split("|")]
+    assert cells[1] == "3.0" and cells[2] == "2.00"
+    assert "the last 3 of each kernel" in out
+
+
 def test_trace_table_per_step_windows(bench, tmp_path):
     # three steps delimited by "ce_row" (once per step); the first window is skipped
     rows = []
@@ -81,6 +95,30 @@ def test_pmc_summary_scales_by_the_copy(bench, tmp_path):
     assert dq["fetch_kib"] == pytest.approx(120.0) and dq["dispatches"] == [2, 1]
     expect = (120.0 * 2 + 10.0 + 300.0 * 2 + 20.0) * 1024
     assert res["traffic_bytes_per_launch"] == pytest.approx(expect)
+
+
+def test_pmc_summary_wgrad_kernel_set(bench, tmp_path):
+    # fx_linear_wgrad's launch: one whole-tile kernel and one reduce dispatch; the general
+    # kernel (gemm_wgrad_kernel) is not part of it
+    gib_kib = (1 << 30) / 1024
+    cf = _write(tmp_path / "cf.csv", PMC_HDR, _pmc_rows("FETCH_SIZE", [(1, "copy_kernel", gib_kib / 2)]))
+    cw = _write(tmp_path / "cw.csv", PMC_HDR, _pmc_rows("WRITE_SIZE", [(1, "copy_kernel", gib_kib)]))
+    f = _write(tmp_path / "f.csv", PMC_HDR, _pmc_rows("FETCH_SIZE", [
+        (1, "void fx::gemm_wgrad_fast_kernel<3>(fx::WgradArgs)", 1000.0),
+        (2, "fx::wgrad_reduce_kernel(float const*, int, long, int)", 500.0),
+        (3, "fx::gemm_wgrad_kernel(fx::WgradArgs)", 9999.0)]))
+    w = _write(tmp_path / "w.csv", PMC_HDR, _pmc_rows("WRITE_SIZE", [
+        (1, "void fx::gemm_wgrad_fast_kernel<3>(fx::WgradArgs)", 400.0),
+        (2, "fx::wgrad_reduce_kernel(float const*, int, long, int)", 40.0)]))
+    res = bench.pmc_summary(f, w, cf, cw, kernels=bench._WGRAD_TRAFFIC_KERNELS)
+    assert set(res["kernels"]) == {"gemm_wgrad_fast_kernel", "wgrad_reduce_kernel"}
+    assert res["traffic_bytes_per_launch"] == pytest.approx((1000.0 * 2 + 400.0 + 500.0 * 2 + 40.0) * 1024)
+
+
+def test_wgrad_roofline_weighs_the_four_shapes_equally(bench):
+    wg = {"a": {"shape_TMN": [10, 2, 3], "us": 1.0}, "b": {"shape_TMN": [10, 4, 5], "us": 3.0}}
+    flop, us = bench.wgrad_roofline(wg)
+    assert flop == pytest.approx((120.0 + 400.0) / 2) and us == pytest.approx(2.0)
 
 
 def test_counter_table_mfma_busy(bench, tmp_path):

@@ -158,6 +158,27 @@ def test_linear_ce(dev, N, D, V, gs):
     _assert_lin_grads(xq.grad, Wq.grad, rdx, rdW)
 
 
+@pytest.mark.parametrize("N,V", [(320, 4096), (1024, 1000)])   # V 1000: a 232-row last panel
+def test_linear_ce_native_head_weight_gradient(dev, monkeypatch, N, V):
+    # the head's weight gradient on fx_linear_wgrad (NATIVE_HEAD_WGRAD, off by default at the
+    # cfg5 head where hipBLASLt is faster): the same oracle bounds as the library product
+    import fxlm.cross_entropy as ce
+    monkeypatch.setattr(ce, "NATIVE_HEAD_WGRAD", True)
+    D = 256
+    torch.manual_seed(N + V)
+    x = torch.randn(N, D).bfloat16()
+    W = (torch.randn(V, D) * 0.02).bfloat16()
+    tg = torch.randint(0, V, (N,))
+    tg[::7] = -100
+    xq, Wq = x.to(dev).requires_grad_(), W.to(dev).requires_grad_()
+    loss = ce.linear_cross_entropy(xq, Wq, tg.to(dev), grad_scale=256.0)
+    loss.backward()
+    rl, _, _ = oce.linear_cross_entropy(x, W, tg)
+    assert abs(float(loss) - float(rl)) <= RTOL_LOSS * abs(float(rl))
+    rdx, rdW = _lin_ce_grads_bf16_points(x, W, tg)
+    _assert_lin_grads(xq.grad, Wq.grad, rdx, rdW)
+
+
 @pytest.mark.parametrize("gs", [1.0, 3.0, None])
 def test_lin_grad_scale_bf16_weight_gradient_is_exact(dev, gs):
     # a single chunk keeps its weight-gradient product in bf16: scaling it must give the
