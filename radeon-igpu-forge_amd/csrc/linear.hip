@@ -931,14 +931,28 @@ struct WgradArgs {
     int M, N, K, slices;
 };
 
+// Work item of workgroup b in a grid of `total` over (slice, tile) items numbered slice-major,
+// tiles row-panel-major.  Workgroups are dealt round-robin to the 8 XCDs (b % 8), each with
+// its own L2, so the items are dealt to XCDs in contiguous runs instead: XCD x takes items
+// x * (total / 8) + min(x, total % 8) onward, in order.  The tiles of one slice that share a
+// token slice of dY (one row panel, every column tile) or of X then run under one L2, and the
+// operand panels are fetched from memory about once (with b itself as the item, the column
+// tiles of a row panel ran on four different XCDs and every panel was fetched by each).  Only
+// which workgroup computes an item changes: the items, and so the results, are the same.
+__device__ __forceinline__ int wgrad_item(int b, int total) {
+    const int x = b & 7, q = total >> 3, r = total & 7;
+    return x * q + min(x, r) + (b >> 3);
+}
+
 __global__ void __launch_bounds__(kGThreads, 1) gemm_wgrad_kernel(WgradArgs a) {
     __shared__ __attribute__((aligned(16))) uint16_t sa[2][kWBK * kWLD];
     __shared__ __attribute__((aligned(16))) uint16_t sb[2][kWBK * kWLD];
 
     const int nn = (a.N + kGBN - 1) / kGBN;
-    // slice-major order: the workgroups dispatched together cover all tiles of a slice
+    // slice-major items, dealt to the XCDs in contiguous runs (wgrad_item)
     const int ntiles = ((a.M + kGBM - 1) / kGBM) * nn;
-    const int sl = blockIdx.x / ntiles, t = blockIdx.x - sl * ntiles;
+    const int item = wgrad_item(blockIdx.x, ntiles * a.slices);
+    const int sl = item / ntiles, t = item - sl * ntiles;
     const int m0 = (t / nn) * kGBM, n0 = (t - (t / nn) * nn) * kGBN;
     const int nk = (a.K + kWBK - 1) / kWBK;
     const int kb = (int)((int64_t)nk * sl / a.slices), ke = (int)((int64_t)nk * (sl + 1) / a.slices);
@@ -1053,7 +1067,8 @@ __global__ void __launch_bounds__(256, 1) gemm_wgrad_fast_kernel(WgradArgs a) {
     __shared__ __attribute__((aligned(16))) unsigned char lds[kAsmStages * G::kStage];
     const int nn = a.N / (64 * NJ);
     const int ntiles = ((a.M + 255) / 256) * nn;  // the last row panel may be partial (M % 256 != 0)
-    const int sl = blockIdx.x / ntiles, t = blockIdx.x - sl * ntiles;
+    const int item = wgrad_item(blockIdx.x, ntiles * a.slices);
+    const int sl = item / ntiles, t = item - sl * ntiles;
     const int m0 = (t / nn) * 256, n0 = (t - (t / nn) * nn) * 64 * NJ;
     const int nk64 = (a.K + 63) / 64;
     const int kb = (int)((int64_t)nk64 * sl / a.slices), ke = (int)((int64_t)nk64 * (sl + 1) / a.slices);
