@@ -78,10 +78,10 @@ def _finalize(row_loss, inv_n):
 FUSED_LINEAR_CE_LOSS = True
 FUSED_LINEAR_CE_TRAIN = False
 # True: the head's weight gradient lg^T x on this build's weight-gradient GEMM
-# (fx_linear_wgrad: 256 x 192 tiles, a partial last row panel at V = 50304, one K slice).
-# Off: at the cfg5 head its 788 tiles take four rounds of 256 CUs for 3.08 rounds of work,
-# 1376 against 1302 us for torch.mm (hipBLASLt), and the step 18.18 against 18.03 ms.
-NATIVE_HEAD_WGRAD = False
+# (fx_linear_wgrad: 256 x 192 tiles, a partial last row panel at V = 50304): at the cfg5
+# head 1196 against 1283 us for torch.mm (hipBLASLt), and the step 17.50 against 17.60 ms
+# (in-process A/B).  False: torch.mm.
+NATIVE_HEAD_WGRAD = True
 
 
 def _lce_fused_ok(x, weight):
