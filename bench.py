@@ -441,10 +441,12 @@ def bench_wgrad(torch):
     return out
 
 
-def bench_wgrad_step(torch, rounds=12):
+def bench_wgrad_step(torch, rounds=12, warm_ms=300.0):
     """For profiler runs: the cfg5 step's 48 layer weight gradients (12 rounds of the qkv,
-    proj, fc and fc2 products over 16384 tokens) after a warm-up round, so that per-dispatch
-    averages weigh the four shapes as the step does."""
+    proj, fc and fc2 products over 16384 tokens), after warm-up rounds that fill `warm_ms` of
+    GPU time (the clocks ramp up over the first ~100 ms), so that per-dispatch averages over
+    the last 48 dispatches weigh the four shapes as the step does and match bench.py's timing
+    (--trace-table ... --trace-last 48)."""
     from fxgpu.fused_linear import linear_wgrad
     T = 16384
     g = torch.Generator(device="cuda").manual_seed(8)
@@ -455,6 +457,11 @@ def bench_wgrad_step(torch, rounds=12):
     for dy, x in ops:
         linear_wgrad(dy, x)
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < warm_ms:
+        for dy, x in ops:
+            linear_wgrad(dy, x)
+        torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(rounds):
         for dy, x in ops:
