@@ -81,10 +81,13 @@ def whole_tiles(M, N, K):
 
 
 # Routing switches, set by measurements inside the cfg5 training step.  In isolation, with
-# the operands left in the caches by the previous call, the whole-tile kernels beat the
-# library GEMM at these shapes; inside the step, where the weights come from HBM, they
-# lose: 18.92 against 18.61 ms per step with the input gradients on fx_linear_dgrad, 18.93
-# against 18.82 ms with the qkv / proj forwards on fx_linear_fwd.  So both are off.
+# the operands left in the caches by the previous call, the whole-tile kernels match the
+# library GEMM at these shapes; inside the step, where the operands come from HBM, they
+# lose: a kernel trace of the step with every switch on had the qkv / proj / fc input
+# gradients at 57.4 against 52.6 us per product, fc2's with the GELU derivative at 140.7
+# against 86.9 + 45.2 us, and the qkv / proj forwards at 50.5 against 46.7 us, 0.42 ms
+# more kernel time per step; interleaved A/Bs of the whole step put the switches within
+# noise of the library routes.  So they are off.
 # NATIVE_INPUT_GRAD: input gradients on fx_linear_dgrad where input_grad() takes them;
 # NATIVE_PROJ_FWD: the whole_tiles() forwards on fx_linear_fwd.  False: the library GEMM.
 NATIVE_INPUT_GRAD = False
