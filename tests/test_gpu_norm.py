@@ -27,16 +27,19 @@ def test_golden(dev):
     assert torch.equal(dw.cpu(), dw32.cpu().bfloat16())
 
 
-# The backward runs 512 <= D <= 1536 on its LDS-ring kernel (1-3 vectors per lane, ring
-# depth 3, or 2 for dres rows past D = 1135); the register kernel folds dw partials through
-# one LDS row per wave up to D = 2048, wider rows wave by wave: (64, 2048) and (64, 2056)
-# sit either side of that switch; _LDS_SHAPES cover the LDS kernel's (vectors, depth)
-# combinations with ragged and tiny row counts
+# The backward runs D < 512 on the register kernel (one vector per lane), 512 <= D <= 1536
+# on its LDS-ring kernel (1-3 vectors per lane, ring depth 3, or 2 for dres rows past
+# D = 1135) and wider rows on the block-per-row kernel (one vector per thread up to
+# D = 4096, two up to 8192; more rows than its 512 blocks take the double-buffered row sum
+# and the next-row prefetch through several rows per block); _LDS_SHAPES cover the LDS
+# kernel's (vectors, depth) combinations with ragged and tiny row counts
 _LDS_SHAPES = [(1, 512), (7, 520), (2049, 1024), (33, 1128), (300, 1136), (11, 1536)]
+_WIDE_SHAPES = [(7, 1544), (64, 2048), (64, 2056), (1100, 2048), (5, 3000), (64, 4096), (9, 4104),
+                (1031, 8192)]
 
 
 @pytest.mark.parametrize("N,D", [(4, 8), (37, 64), (129, 768), (1000, 512), (300, 8192),
-                                 (5, 1032), (3, 96), (64, 2048), (64, 2056)] + _LDS_SHAPES)
+                                 (5, 1032), (3, 96)] + _LDS_SHAPES + _WIDE_SHAPES)
 def test_against_oracle(dev, N, D):
     # the reference selftest's cases (ml/fxlm/selftest.py:186-204) plus odd row shapes
     torch.manual_seed(N * 1000 + D)
@@ -89,7 +92,7 @@ def test_cfg4_full_size(dev):
 
 # ---- the residual block's fused gradient sum (fx_rms_norm_bwd_add / pre_norm) ----------
 
-@pytest.mark.parametrize("N,D", [(129, 768), (300, 8192), (64, 2056), (5, 96)] + _LDS_SHAPES)
+@pytest.mark.parametrize("N,D", [(129, 768), (300, 8192), (64, 2056), (5, 96), (1100, 2048)] + _LDS_SHAPES)
 def test_bwd_add_against_oracle(dev, N, D):
     # dx = dres + (the norm's dx) in one pass; dw is the norm's alone, bit for bit the
     # plain backward's
