@@ -1104,30 +1104,50 @@ __global__ void __launch_bounds__(256, 1) gemm_wgrad_fast_kernel(WgradArgs a) {
         asm volatile(FX_WGRAD_NJ3_KLOOP : FX_WGRAD_NJ3_OUTS : FX_WGRAD_NJ3_INS : FX_WGRAD_NJ3_CLOBBERS);
     (void)m0save;
 
-    // lane holds column n = n0 + wn + 32 j + lane%32 and rows m0 + wm + 32 i + 8 (e/4) + 4 g
-    // + e%4 (acc[4 j + i]); a half-wave stores 32 consecutive columns of a row.  Addresses:
-    // a wave-uniform row base plus a per-lane 32-bit offset (4 g rows + the column), one
-    // accumulator block at a time (the scheduler otherwise reads all 256 accumulators
-    // ahead of the stores and spills)
+    // Epilogue through LDS (the stages are free once every wave is past its loop): lane
+    // holds column n0 + wn + 32 j + lane%32 and rows m0 + wm + 32 i + 8 (e/4) + 4 g + e%4 of
+    // acc[4 j + i].  Per 32-row block i the wave writes these fp32 values into a 32 x (32 NJ)
+    // block of its own LDS region (row stride kWStg floats, so the half-waves' rows, 4 apart,
+    // fall in disjoint banks), then reads the block back along its rows and stores 16-byte
+    // chunks: 4 fp32 partials or 8 bf16 outputs per lane and store, rather than one element.
+    // One block at a time, so the accumulators are read block by block (read all at once
+    // they spill).  A wave's LDS operations complete in order, so a block's writes do not
+    // overtake the previous block's reads.
+    raw_barrier();
     const int g = lane >> 5;
+    constexpr int kWStg = 32 * NJ + 8;  // 4 kWStg = 32 (mod 64): rows r and r + 4 in disjoint banks
+    static_assert(4 * 32 * kWStg * 4 <= kAsmStages * G::kStage, "staging fits the stages");
+    float* stg = reinterpret_cast<float*>(lds) + wave * 32 * kWStg;
     auto store = [&](auto* out, int64_t ldo) {
+        constexpr bool kF32 = sizeof(*out) == 4;
+        constexpr int kCh = kF32 ? 8 * NJ : 4 * NJ;  // 16-byte chunks per output row of the block
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            const uint32_t voff = (uint32_t)(4 * g * ldo + wn + 32 * j + (lane & 31));
+        for (int i = 0; i < 4; ++i) {
+            const int64_t row0 = m0 + wm + 32 * i;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int64_t row0 = m0 + wm + 32 * i;
+            for (int j = 0; j < NJ; ++j) {
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    if (row0 + 8 * (e >> 2) + (e & 3) + 4 * g >= a.M) continue;  // past a ragged last panel
-                    auto* o = out + (row0 + 8 * (e >> 2) + (e & 3)) * ldo + n0;
-                    if constexpr (sizeof(*out) == 4)
-                        o[voff] = acc[4 * j + i][e];
-                    else
-                        o[voff] = f32_to_bf16(acc[4 * j + i][e]);
-                }
+                for (int e = 0; e < 16; ++e)
+                    stg[(8 * (e >> 2) + 4 * g + (e & 3)) * kWStg + 32 * j + (lane & 31)] = acc[4 * j + i][e];
                 __builtin_amdgcn_sched_barrier(0);
             }
+#pragma unroll
+            for (int k = 0; k < kCh / 2; ++k) {
+                const int idx = lane + 64 * k;
+                const int r = idx / kCh, c = idx - r * kCh;
+                if (row0 + r >= a.M) continue;  // past a ragged last panel
+                auto* o = out + (row0 + r) * ldo + n0 + wn;
+                const float* src = stg + r * kWStg;
+                if constexpr (kF32) {
+                    st16(o + 4 * c, *reinterpret_cast<const uint4*>(src + 4 * c));
+                } else {
+                    const float4 lo = *reinterpret_cast<const float4*>(src + 8 * c);
+                    const float4 hi = *reinterpret_cast<const float4*>(src + 8 * c + 4);
+                    st16(o + 8 * c, make_uint4(pack_bf16x2(lo.x, lo.y), pack_bf16x2(lo.z, lo.w),
+                                               pack_bf16x2(hi.x, hi.y), pack_bf16x2(hi.z, hi.w)));
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
     if (a.slices > 1)
