@@ -1511,12 +1511,21 @@ extern "C" int fx_linear_fwd_ex(const fxLinearArgs* args, void* stream) {
 // shapes); measured 67.9 / 43.1 / 80.4 / 78.5 µs against 80.3 / 47.6 / 92.9 / 81.9 for
 // 256 x 256 tiles (qkv / proj / fc / fc2 weight gradients, reduce included) and 18.05
 // against 18.47 ms per cfg5 step.  FX_WGRAD_TILE=256 keeps 256 x 256 tiles (comparisons).
+// How fx_linear_wgrad divides a product.  Outputs with fewer whole tiles than CUs split K
+// into `slices` (fp32 partials, then a reduce in slice order).  Outputs with more tiles
+// than CUs run one slice, except that a last, partly filled round of tiles (the tied head's
+// (50304, 768) gradient is 788 tiles: three rounds of 256 and 20 tiles in a fourth, which
+// would take as long as a full one) is split off: the rows from split_rows on (whole row
+// panels) run as a second product in tail_slices slices, one round.  The same plan drives the
+// general kernel (FX_GEMM_GENERAL), so the two agree bit for bit.
 struct WgradPlan {
     int nj, slices;
     bool fast;
+    int64_t split_rows;  // 0: one product
+    int tail_slices;
 };
 static WgradPlan wgrad_plan(int64_t M, int64_t N, int64_t K) {
-    WgradPlan p{0, 1, false};
+    WgradPlan p{0, 1, false, 0, 1};
     const char* tw = getenv("FX_WGRAD_TILE");
     const bool want4 = tw && tw[0] == '2' && tw[1] == '5' && tw[2] == '6';
     // M need not divide into whole 256-row panels: the last panel's loads are clamped and its
@@ -1528,18 +1537,32 @@ static WgradPlan wgrad_plan(int64_t M, int64_t N, int64_t K) {
     const int64_t tiles = p.nj ? ((M + 255) / 256) * (N / (64 * p.nj))
                                : ((M + kGBM - 1) / kGBM) * ((N + kGBN - 1) / kGBN);
     const int64_t nk = (K + kWBK - 1) / kWBK;
-    int64_t s = device_cus() / tiles;
-    if (s > nk / 4) s = nk / 4;
-    if (s > 32) s = 32;
-    p.slices = s < 1 ? 1 : (int)s;
+    const int64_t cus = device_cus();
+    auto slices_for = [&](int64_t t) {
+        int64_t sl = cus / t;
+        if (sl > nk / 4) sl = nk / 4;
+        if (sl > 32) sl = 32;
+        return sl < 1 ? 1 : (int)sl;
+    };
+    p.slices = slices_for(tiles);
     p.fast = p.nj != 0 && whole_tile_kernels_enabled('w');
+    if (p.nj && p.slices == 1 && tiles > cus) {
+        const int64_t nn = N / (64 * p.nj), panels = (M + 255) / 256;
+        const int64_t full = (tiles / cus) * cus / nn;  // row panels that fill whole rounds
+        const int tail = slices_for((panels - full) * nn);
+        if (full > 0 && full < panels && tail >= 2) {
+            p.split_rows = 256 * full;
+            p.tail_slices = tail;
+        }
+    }
     return p;
 }
 
 extern "C" int64_t fx_linear_wgrad_workspace(int64_t M, int64_t N, int64_t K) {
     if (M <= 0 || N <= 0 || K <= 0) return 0;
-    const int s = wgrad_plan(M, N, K).slices;
-    return s > 1 ? (int64_t)s * M * N * (int64_t)sizeof(float) : 0;
+    const WgradPlan p = wgrad_plan(M, N, K);
+    if (p.split_rows) return (int64_t)p.tail_slices * (M - p.split_rows) * N * (int64_t)sizeof(float);
+    return p.slices > 1 ? (int64_t)p.slices * M * N * (int64_t)sizeof(float) : 0;
 }
 
 extern "C" int fx_linear_wgrad(const uint16_t* dY, int64_t ldy, const uint16_t* X, int64_t ldx, uint16_t* dW,
@@ -1555,41 +1578,47 @@ extern "C" int fx_linear_wgrad(const uint16_t* dY, int64_t ldy, const uint16_t* 
                (long long)ldx, (long long)ldw);
     FX_REQUIRE(((((uintptr_t)dY) | ((uintptr_t)X) | ((uintptr_t)dW) | ((uintptr_t)work)) & 15) == 0,
                "fx_linear_wgrad: dY, X, dW and work must be 16-byte aligned");
-    const WgradPlan plan = K > 0 ? wgrad_plan(M, N, K) : WgradPlan{0, 1, false};
-    const int slices = plan.slices;
-    FX_REQUIRE(slices == 1 || work != nullptr, "fx_linear_wgrad: null workspace (%d slices)", slices);
-    WgradArgs a;
-    a.A = dY;
-    a.lda = ldy;
-    a.B = X;
-    a.ldb = ldx;
-    a.C = dW;
-    a.ldc = ldw;
-    a.part = work;
-    a.M = (int)M;
-    a.N = (int)N;
-    a.K = (int)K;
-    a.slices = slices;
+    const WgradPlan plan = K > 0 ? wgrad_plan(M, N, K) : WgradPlan{0, 1, false, 0, 1};
+    FX_REQUIRE((plan.slices == 1 && !plan.split_rows) || work != nullptr,
+               "fx_linear_wgrad: null workspace (%d slices)", plan.split_rows ? plan.tail_slices : plan.slices);
     hipStream_t s = (hipStream_t)stream;
-    // whole tiles and 32-token steps, every slice at least 4 steps: the generated loop (with
-    // several slices each spans at least 4 64-token steps, the last perhaps 32 tokens short)
-    if (plan.fast) {
-        const int64_t tiles = ((M + 255) / 256) * (N / (64 * plan.nj));
-        if (plan.nj == 4)
-            hipLaunchKernelGGL(gemm_wgrad_fast_kernel<4>, dim3((unsigned)(tiles * slices)), dim3(256), 0, s, a);
-        else
-            hipLaunchKernelGGL(gemm_wgrad_fast_kernel<3>, dim3((unsigned)(tiles * slices)), dim3(256), 0, s, a);
-    } else {
-        const int64_t tiles = ((M + kGBM - 1) / kGBM) * ((N + kGBN - 1) / kGBN);
-        hipLaunchKernelGGL(gemm_wgrad_kernel, dim3((unsigned)(tiles * slices)), dim3(kGThreads), 0, s, a);
-    }
-    if (int e = check_launch("gemm_wgrad")) return e;
-    if (slices == 1) return 0;
-    int64_t blocks = (M * N / 8 + 255) / 256;
-    if (blocks > 4096) blocks = 4096;
-    hipLaunchKernelGGL(wgrad_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, s, (const float*)work, slices,
-                       M * N, (int)N, dW, ldw);
-    return check_launch("wgrad_reduce");
+    // rows [r0, r0 + rows) of dW in `slices` slices
+    auto product = [&](int64_t r0, int64_t rows, int slices) -> int {
+        WgradArgs a;
+        a.A = dY + r0;
+        a.lda = ldy;
+        a.B = X;
+        a.ldb = ldx;
+        a.C = dW + r0 * ldw;
+        a.ldc = ldw;
+        a.part = work;
+        a.M = (int)rows;
+        a.N = (int)N;
+        a.K = (int)K;
+        a.slices = slices;
+        // whole tiles and 32-token steps, every slice at least 4 steps: the generated loop (with
+        // several slices each spans at least 4 64-token steps, the last perhaps 32 tokens short)
+        if (plan.fast) {
+            const int64_t tiles = ((rows + 255) / 256) * (N / (64 * plan.nj));
+            if (plan.nj == 4)
+                hipLaunchKernelGGL(gemm_wgrad_fast_kernel<4>, dim3((unsigned)(tiles * slices)), dim3(256), 0, s, a);
+            else
+                hipLaunchKernelGGL(gemm_wgrad_fast_kernel<3>, dim3((unsigned)(tiles * slices)), dim3(256), 0, s, a);
+        } else {
+            const int64_t tiles = ((rows + kGBM - 1) / kGBM) * ((N + kGBN - 1) / kGBN);
+            hipLaunchKernelGGL(gemm_wgrad_kernel, dim3((unsigned)(tiles * slices)), dim3(kGThreads), 0, s, a);
+        }
+        if (int e = check_launch("gemm_wgrad")) return e;
+        if (slices == 1) return 0;
+        int64_t blocks = (rows * N / 8 + 255) / 256;
+        if (blocks > 4096) blocks = 4096;
+        hipLaunchKernelGGL(wgrad_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, s, (const float*)work, slices,
+                           rows * N, (int)N, a.C, ldw);
+        return check_launch("wgrad_reduce");
+    };
+    if (!plan.split_rows) return product(0, M, plan.slices);
+    if (int e = product(0, plan.split_rows, 1)) return e;
+    return product(plan.split_rows, M - plan.split_rows, plan.tail_slices);
 }
 
 // the tile width (in 64-column units) of gemm_dgrad_fast_kernel for N columns: of the widths

@@ -78,9 +78,9 @@ def _finalize(row_loss, inv_n):
 FUSED_LINEAR_CE_LOSS = True
 FUSED_LINEAR_CE_TRAIN = False
 # True: the head's weight gradient lg^T x on this build's weight-gradient GEMM
-# (fx_linear_wgrad: 256 x 192 tiles, a partial last row panel at V = 50304): at the cfg5
-# head 1196 against 1283 us for torch.mm (hipBLASLt), and the step 17.50 against 17.60 ms
-# (in-process A/B).  False: torch.mm.
+# (fx_linear_wgrad: 256 x 192 tiles, a partial last row panel at V = 50304, the 20 tiles past
+# three full rounds split over the tokens): at the cfg5 head 1017 us against 1283 us for
+# torch.mm (hipBLASLt).  False: torch.mm.
 NATIVE_HEAD_WGRAD = True
 
 
