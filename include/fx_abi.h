@@ -25,7 +25,7 @@ extern "C" {
 #endif
 
 #define FX_EINVAL (-1)
-#define FX_ABI_VERSION 3
+#define FX_ABI_VERSION 4
 
 /* ---- library ------------------------------------------------------------ */
 
@@ -144,6 +144,15 @@ int fx_ce_lin_grad_scale(const float* dw, int64_t nw, const uint16_t* dx, int64_
 int fx_ce_lin_grad_scale_bf16w(const uint16_t* dw, int64_t nw, const uint16_t* dx, int64_t nx, const float* g,
                                const float* gs, float inv_value, uint16_t* dw_out, uint16_t* dx_out,
                                void* stream);
+
+/* fx_ce_lin_grad_scale_bf16w in place: dw = bf16(dw * s), dx = bf16(dx * bf16(s)), the same
+ * roundings (dw bf16 (nw,), dx bf16 (nx,), 16-byte aligned).  When s == 1 no value changes
+ * (the products are exact), and the kernel returns without a pass over either buffer: the
+ * usual training step, where the incoming gradient is the loss scale the head's gradients
+ * were formed with.  Replaces the first backward's gx = dx * (g * inv), gw = (dW * (g * inv))
+ * .to(dtype) of _LinearCE (ml/fxlm/cross_entropy.py:141-148), on the saved gradients. */
+int fx_ce_lin_grad_scale_inplace(uint16_t* dw, int64_t nw, uint16_t* dx, int64_t nx, const float* g,
+                                 const float* gs, float inv_value, void* stream);
 
 /* ---- FlatAdamW ---------------------------------------------------------- */
 

@@ -285,6 +285,38 @@ ce_lin_grad_scale_kernel(const WT* __restrict__ dw, int64_t nw, const uint16_t* 
     }
 }
 
+// ce_lin_grad_scale_kernel for a bf16 dw, in place: dw = bf16(dw * s), dx = bf16(dx * bf16(s)),
+// the same roundings.  s == 1 changes no value (x * 1 is exact), so then the whole grid
+// returns without touching memory.
+__global__ void __launch_bounds__(256)
+ce_lin_grad_scale_inplace_kernel(uint16_t* dw, int64_t nw, uint16_t* dx, int64_t nx, const float* __restrict__ g,
+                                 const float* __restrict__ gs, float inv_value) {
+    const float inv = gs != nullptr ? 1.f / *gs : inv_value;
+    const float sc = *g * inv;
+    if (sc == 1.f) return;
+    const float sx = bf16_to_f32(f32_to_bf16(sc));
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    const int64_t t0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    for (int64_t v = t0; v < nw / 8; v += stride) {
+        float f[8];
+        unpack8(ld16(dw + v * 8), f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) f[j] *= sc;
+        st16(dw + v * 8, pack8(f));
+    }
+    for (int64_t v = t0; v < nx / 8; v += stride) {
+        float f[8];
+        unpack8(ld16(dx + v * 8), f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) f[j] *= sx;
+        st16(dx + v * 8, pack8(f));
+    }
+    if (t0 == 0) {
+        for (int64_t i = nw / 8 * 8; i < nw; ++i) dw[i] = f32_to_bf16(bf16_to_f32(dw[i]) * sc);
+        for (int64_t i = nx / 8 * 8; i < nx; ++i) dx[i] = f32_to_bf16(bf16_to_f32(dx[i]) * sx);
+    }
+}
+
 }  // namespace fx
 
 using namespace fx;
@@ -420,4 +452,19 @@ extern "C" int fx_ce_lin_grad_scale_bf16w(const uint16_t* dw, int64_t nw, const 
                                           const float* g, const float* gs, float inv_value, uint16_t* dw_out,
                                           uint16_t* dx_out, void* stream) {
     return lin_grad_scale(dw, nw, dx, nx, g, gs, inv_value, dw_out, dx_out, stream, "fx_ce_lin_grad_scale_bf16w");
+}
+
+extern "C" int fx_ce_lin_grad_scale_inplace(uint16_t* dw, int64_t nw, uint16_t* dx, int64_t nx, const float* g,
+                                            const float* gs, float inv_value, void* stream) {
+    FX_REQUIRE(nw >= 0 && nx >= 0 && g != nullptr, "fx_ce_lin_grad_scale_inplace: bad arguments");
+    FX_REQUIRE((nw == 0 || dw) && (nx == 0 || dx), "fx_ce_lin_grad_scale_inplace: null pointer");
+    FX_REQUIRE(((((uintptr_t)dw) | ((uintptr_t)dx)) & 15) == 0,
+               "fx_ce_lin_grad_scale_inplace: buffers must be 16-byte aligned");
+    if (nw == 0 && nx == 0) return 0;
+    const int64_t groups = (nw > nx ? nw : nx) / 8 + 1;
+    int64_t blocks = (groups + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(ce_lin_grad_scale_inplace_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, dw,
+                       nw, dx, nx, g, gs, inv_value);
+    return check_launch("ce_lin_grad_scale_inplace");
 }

@@ -14,7 +14,7 @@ LIB_PATH = os.path.join(_PKG_ROOT, "libfxforge.so")
 HEADER_PATH = os.path.join(os.path.dirname(_PKG_ROOT), "include", "fx_abi.h")
 
 FX_EINVAL = -1
-FX_ABI_VERSION = 3
+FX_ABI_VERSION = 4
 MAX_TENSORS = 64
 ADAMW_NOALLOC_SCRATCH_BYTES = 1 << 20   # FX_ADAMW_NOALLOC_SCRATCH_BYTES
 
@@ -116,6 +116,7 @@ SIGNATURES = {
     "fx_ce_scale_grad": (c_int32, [_P, c_int64, _P, _P, c_int32, _P]),
     "fx_ce_lin_grad_scale": (c_int32, [_P, c_int64, _P, c_int64, _P, _P, c_float, _P, _P, _P]),
     "fx_ce_lin_grad_scale_bf16w": (c_int32, [_P, c_int64, _P, c_int64, _P, _P, c_float, _P, _P, _P]),
+    "fx_ce_lin_grad_scale_inplace": (c_int32, [_P, c_int64, _P, c_int64, _P, _P, c_float, _P]),
     "fx_adamw_workspace": (c_int64, [ctypes.POINTER(fxTensorList), c_int32]),
     "fx_adamw_step": (c_int32, [ctypes.POINTER(fxAdamWState), ctypes.POINTER(fxTensorList),
                                 c_int32, _P]),

@@ -230,21 +230,44 @@ class _LinearCE(torch.autograd.Function):
         ctx.save_for_backward(dx, dW)
         ctx.grad_scale = grad_scale
         ctx.wdtype = weight.dtype
+        ctx.calls = 0
         return _finalize(row_loss, inv_n)
 
     @staticmethod
     def backward(ctx, g):
         dx, dW = ctx.saved_tensors
         gs = ctx.grad_scale
+        ctx.calls += 1
         if _FUSED_LIN_GRAD_SCALE and ctx.wdtype == torch.bfloat16 and dx.dtype == torch.bfloat16:
             # one pass: the same fp32 reciprocal, products and bf16 rounding as below
-            g32 = g.detach().float().reshape(())
-            gs_t = gs.detach().float().reshape(()) if torch.is_tensor(gs) else None
+            g32 = g.detach().float().reshape(()).contiguous()
+            gs_t = gs.detach().float().reshape(()).contiguous() if torch.is_tensor(gs) else None
+            inv_value = 0.0 if gs_t is not None else 1.0 / gs
+            if dW.dtype == torch.bfloat16 and ctx.calls == 1:
+                # the usual single backward (one chunk, so dW is the bf16 product): scale the
+                # saved gradients in place and hand them over; in the training step the
+                # factor g / grad_scale is exactly 1 and the kernel makes no pass at all
+                call("fx_ce_lin_grad_scale_inplace", ptr(dW), dW.numel(), ptr(dx), dx.numel(), ptr(g32),
+                     ptr(gs_t), inv_value, stream_of(dx))
+                ctx.first = (g32, gs_t, inv_value)
+                return dx, dW, None, None, None, None
+            if dW.dtype == torch.bfloat16:
+                # a further backward through a retained graph: the saved gradients carry the
+                # first backward's factor s1; fresh tensors at s / s1
+                g1, gs1, inv1 = ctx.first
+                s1 = float(g1) * (1.0 / float(gs1) if gs1 is not None else inv1)
+                if s1 == 0.0:
+                    raise RuntimeError("linear_cross_entropy: the first backward of this graph had a "
+                                       "gradient factor of 0, which zeroed the saved gradients; run the "
+                                       "forward again")
+                s = float(g32) * (1.0 / float(gs_t) if gs_t is not None else inv_value)
+                g32 = torch.tensor(s / s1, device=dx.device, dtype=torch.float32)
+                gs_t, inv_value = None, 1.0
             gx = torch.empty_like(dx)
             gw = torch.empty(dW.shape, device=dW.device, dtype=torch.bfloat16)
             fn = "fx_ce_lin_grad_scale_bf16w" if dW.dtype == torch.bfloat16 else "fx_ce_lin_grad_scale"
-            call(fn, ptr(dW), dW.numel(), ptr(dx), dx.numel(), ptr(g32), ptr(gs_t),
-                 0.0 if gs_t is not None else 1.0 / gs, ptr(gw), ptr(gx), stream_of(dx))
+            call(fn, ptr(dW), dW.numel(), ptr(dx), dx.numel(), ptr(g32), ptr(gs_t), inv_value, ptr(gw), ptr(gx),
+                 stream_of(dx))
             return gx, gw, None, None, None, None
         inv = torch.reciprocal(gs.float()) if torch.is_tensor(gs) else 1.0 / gs
         gx = dx * (g * inv)

@@ -199,6 +199,64 @@ def test_lin_grad_scale_bf16_weight_gradient_is_exact(dev, gs):
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
 
 
+@pytest.mark.parametrize("g,gs", [(0.37, 2.0), (0.37, None), (1024.0, None), (3.0, 3.0)])
+def test_lin_grad_scale_inplace_matches_out_of_place(dev, g, gs):
+    # the first backward's in-place scaling gives the bits of the out-of-place kernel; with a
+    # factor of exactly 1 (the training step's g == grad_scale) it leaves both buffers as
+    # they were
+    from fxgpu.abi import call, ptr, stream_of
+    gen = torch.Generator(device=dev).manual_seed(5)
+    dw16 = (torch.randn(2003, device=dev, generator=gen) * 50).bfloat16()   # odd length: the tail too
+    dx = torch.randn(1029, device=dev, generator=gen).bfloat16()
+    gt = torch.tensor(g, device=dev)
+    gs_t = torch.tensor(1024.0, device=dev) if gs is None else None
+    inv = 0.0 if gs is None else 1.0 / gs
+    gw, gx = torch.empty_like(dw16), torch.empty_like(dx)
+    call("fx_ce_lin_grad_scale_bf16w", ptr(dw16), dw16.numel(), ptr(dx), dx.numel(), ptr(gt), ptr(gs_t), inv,
+         ptr(gw), ptr(gx), stream_of(dx))
+    w2, x2 = dw16.clone(), dx.clone()
+    call("fx_ce_lin_grad_scale_inplace", ptr(w2), w2.numel(), ptr(x2), x2.numel(), ptr(gt), ptr(gs_t), inv,
+         stream_of(dx))
+    torch.cuda.synchronize()
+    assert torch.equal(w2.view(torch.int16), gw.view(torch.int16))
+    assert torch.equal(x2.view(torch.int16), gx.view(torch.int16))
+    s = g * (1.0 / 1024.0 if gs is None else inv)
+    if s == 1.0:
+        assert torch.equal(w2.view(torch.int16), dw16.view(torch.int16))
+
+
+def test_linear_ce_backward_twice_with_retained_graph(dev):
+    # the first backward scales the saved gradients in place and returns them; a second
+    # backward through the retained graph returns fresh ones at its own factor, and the
+    # first call's results stay as they were
+    from fxlm.cross_entropy import linear_cross_entropy
+    torch.manual_seed(11)
+    N, D, V = 300, 256, 4096
+    x = torch.randn(N, D, device=dev).bfloat16().requires_grad_()
+    W = (torch.randn(V, D, device=dev) * 0.02).bfloat16().requires_grad_()
+    tg = torch.randint(0, V, (N,), device=dev)
+    loss = linear_cross_entropy(x, W, tg, grad_scale=4.0)
+    g1x, g1w = torch.autograd.grad(loss * 8.0, (x, W), retain_graph=True)
+    k1x, k1w = g1x.clone(), g1w.clone()
+    g2x, g2w = torch.autograd.grad(loss * 2.0, (x, W))
+    torch.cuda.synchronize()
+    assert torch.equal(g1x, k1x) and torch.equal(g1w, k1w)
+    for a, b in ((g2x, g1x), (g2w, g1w)):
+        assert torch.allclose(a.float() * 4.0, b.float(), rtol=2.0 ** -7, atol=1e-30)
+
+
+def test_linear_ce_retained_graph_after_zero_factor_raises(dev):
+    from fxlm.cross_entropy import linear_cross_entropy
+    torch.manual_seed(12)
+    x = torch.randn(64, 128, device=dev).bfloat16().requires_grad_()
+    W = (torch.randn(512, 128, device=dev) * 0.02).bfloat16().requires_grad_()
+    tg = torch.randint(0, 512, (64,), device=dev)
+    loss = linear_cross_entropy(x, W, tg)
+    torch.autograd.grad(loss * 0.0, (x, W), retain_graph=True)
+    with pytest.raises(RuntimeError, match="factor of 0"):
+        torch.autograd.grad(loss * 1.0, (x, W))
+
+
 @pytest.mark.parametrize("gs", [1.0, None])
 def test_linear_ce_single_chunk(dev, gs):
     # the default chunking holds these rows in one chunk (bf16 weight-gradient product)
