@@ -470,6 +470,42 @@ def bench_wgrad_step(torch, rounds=12, warm_ms=300.0):
     return {"launches": 4 * rounds, "wall_us_per_launch": round((time.perf_counter() - t0) / (4 * rounds) * 1e6, 2)}
 
 
+def bench_gemm_kernels(torch, reps=10, warm_ms=300.0):
+    """For counter runs: this build's three whole-tile GEMM kernels at the cfg5 layer shapes,
+    16384 tokens: the forward (fx_linear_fwd, gemm_fast_kernel) at the qkv / proj / fc2
+    shapes, the input gradient (fx_linear_dgrad, gemm_dgrad_fast_kernel) at the qkv / proj /
+    fc / fc2 shapes, the weight gradient (fx_linear_wgrad) at all four, `reps` times each
+    after warm-up rounds filling `warm_ms` of GPU time."""
+    from fxgpu.abi import call, ptr, stream_of
+    from fxgpu.fused_linear import _native_fwd, linear_wgrad
+    T = 16384
+    g = torch.Generator(device="cuda").manual_seed(9)
+    R = lambda *s: (torch.randn(*s, device="cuda", generator=g) * 0.5).bfloat16()  # noqa: E731
+    ops = []
+    for N, K in ((2304, 768), (768, 768), (768, 3072)):       # y (T, N) = x (T, K) W^T
+        x, w = R(T, K), R(N, K)
+        ops.append(lambda x=x, w=w: _native_fwd(x, w))
+    for N, K in ((768, 2304), (768, 768), (768, 3072), (3072, 768)):   # dx (T, N) = dy (T, K) W (K, N)
+        dy, w = R(T, K), R(K, N)
+        dx = torch.empty(T, N, device="cuda", dtype=torch.bfloat16)
+        ops.append(lambda dy=dy, w=w, dx=dx, N=N, K=K: call(
+            "fx_linear_dgrad", ptr(dy), K, ptr(w), N, None, ptr(dx), N, T, N, K, stream_of(dy)))
+    for M, N in ((2304, 768), (768, 768), (3072, 768), (768, 3072)):  # dW (M, N) = dy^T x
+        dy, x = R(T, M), R(T, N)
+        ops.append(lambda dy=dy, x=x: linear_wgrad(dy, x))
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < warm_ms:
+        for f in ops:
+            f()
+        torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        for f in ops:
+            f()
+    torch.cuda.synchronize()
+    return {"launches": reps * len(ops), "wall_us_per_launch": round((time.perf_counter() - t0) / (reps * len(ops)) * 1e6, 2)}
+
+
 def wgrad_roofline(wg):
     """fx_linear_wgrad over the step's four layer shapes (each 12 times per step): algorithmic
     FLOPs 2 T M N per product, over the measured launch times (kernel plus split-K reduce)."""
@@ -792,6 +828,18 @@ def counter_table(csv_paths, top=12):
         hdr.append("MFMA busy %")
     if bf:
         hdr.append("issued bf16 TFLOP/s")
+    # per-CU and per-SIMD ratios of the issue / LDS / memory-pipeline counters, when present:
+    # a count of CU cycles over GRBM_GUI_ACTIVE / 8 x 256 CUs, a count of wave quad-cycles
+    # (x 4) over GRBM_GUI_ACTIVE / 8 x 1024 SIMDs, and the mean L2 read latency in cycles
+    per_cu = [c for c in ("SQ_LDS_IDX_ACTIVE", "SQ_LDS_BANK_CONFLICT", "TA_TA_BUSY", "TD_TD_BUSY",
+                          "TCP_PENDING_STALL_CYCLES") if c in names]
+    per_simd = [c for c in ("SQ_WAIT_ANY", "SQ_WAIT_INST_ANY", "SQ_WAIT_INST_LDS") if c in names]
+    lat = "TCP_TCC_READ_REQ_LATENCY" in names and "TCP_TCC_READ_REQ" in names
+    grbm = "GRBM_GUI_ACTIVE" in names
+    if grbm:
+        hdr += [f"{c} % of CU cycles" for c in per_cu] + [f"{c} % of SIMD cycles" for c in per_simd]
+    if lat:
+        hdr.append("L2 read latency (cycles)")
     lines = ["| " + " | ".join(hdr) + " |", "|" + "---|" * len(hdr)]
     for k, n, a in rows[:top]:
         kn = k if len(k) < 70 else k[:67] + "..."
@@ -800,6 +848,12 @@ def counter_table(csv_paths, top=12):
             cells.append(f"{100 * a['SQ_VALU_MFMA_BUSY_CYCLES'] / max(1.0, a['GRBM_GUI_ACTIVE'] / 8 * 1024):.1f}")
         if bf:
             cells.append(f"{a['SQ_INSTS_VALU_MFMA_MOPS_BF16'] * 512 / max(1.0, a['_t']) / 1e3:.1f}")
+        if grbm:
+            cu_cycles = max(1.0, a["GRBM_GUI_ACTIVE"] / 8 * 256)
+            cells += [f"{100 * a[c] / cu_cycles:.1f}" for c in per_cu]
+            cells += [f"{100 * 4 * a[c] / (cu_cycles * 4):.1f}" for c in per_simd]
+        if lat:
+            cells.append(f"{a['TCP_TCC_READ_REQ_LATENCY'] / max(1.0, a['TCP_TCC_READ_REQ']):.0f}")
         lines.append("| " + " | ".join(cells) + " |")
     return "\n".join(lines)
 
@@ -912,7 +966,8 @@ def main():
     # so that no batch's first step (and no first allocation of a size) falls in the timed steps
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true", help="skip the host-CPU baseline")
-    ap.add_argument("--only", choices=["attention", "ce", "norm", "adamw", "linear", "wgrad", "wgrad-step", "head",
+    ap.add_argument("--only", choices=["attention", "ce", "norm", "adamw", "linear", "wgrad", "wgrad-step",
+                                       "gemm-kernels", "head",
                                        "library", "step", "copy",
                                        "decode", "embedding",
                                        "cpu", "fc-ours", "fc-library", "fc-ours-cold", "fc-library-cold"],
@@ -962,6 +1017,7 @@ def main():
     if args.only:
         fn = {"attention": bench_attention, "ce": bench_ce, "norm": bench_norm, "adamw": bench_adamw,
               "linear": bench_linear, "wgrad": bench_wgrad, "wgrad-step": bench_wgrad_step,
+              "gemm-kernels": bench_gemm_kernels,
               "head": bench_head, "copy": bench_copy,
               "library": bench_library,
               "decode": bench_decode, "embedding": bench_embedding,

@@ -133,3 +133,20 @@ def test_counter_table_mfma_busy(bench, tmp_path):
     assert cells[-2] == "50.0"
     # 1000 x 512 flops in 2000 ns = 256 GFLOP/s = 0.256 TFLOP/s
     assert cells[-1] == "0.3"
+
+
+def test_counter_table_pipeline_ratios(bench, tmp_path):
+    # GRBM_GUI_ACTIVE 8000 over 8 XCDs: 1000 cycles, so 256,000 CU cycles and 1,024,000 SIMD
+    # cycles; TA busy 128,000 CU cycles = 50 %; 64,000 wave quad-cycles waiting = 25 % of the
+    # SIMD cycles; 3000 cycles of latency over 10 L2 reads = 300
+    rows = [(1, "k", "GRBM_GUI_ACTIVE", 8000.0, 0, 2000), (1, "k", "TA_TA_BUSY", 128000.0, 0, 2000),
+            (1, "k", "SQ_WAIT_INST_ANY", 64000.0, 0, 2000), (1, "k", "TCP_TCC_READ_REQ_LATENCY", 3000.0, 0, 2000),
+            (1, "k", "TCP_TCC_READ_REQ", 10.0, 0, 2000)]
+    p = _write(tmp_path / "c.csv", PMC_HDR, rows)
+    out = bench.counter_table([p])
+    hdr = [c.strip() for c in out.splitlines()[0].strip("|").split("|")]
+    line = next(l for l in out.splitlines() if l.startswith("| `k`"))
+    cells = dict(zip(hdr, [c.strip() for c in line.strip("|").split("|")]))
+    assert cells["TA_TA_BUSY % of CU cycles"] == "50.0"
+    assert cells["SQ_WAIT_INST_ANY % of SIMD cycles"] == "25.0"
+    assert cells["L2 read latency (cycles)"] == "300"
