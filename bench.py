@@ -180,8 +180,9 @@ def _zipf_ids(torch, n, V, seed, a=1.1):
 
 
 def _byte_text_ids(torch, n):
-    """n byte-level tokens (V = 256) of this repository's own prose (DESIGN/README text; a
-    fixed English sentence when those are absent): the space byte holds ~15 % of them."""
+    """n byte-level tokens (V = 256) of this repository's own prose (its top-level markdown
+    documents; a fixed English sentence when those are absent): the space byte holds ~15 % of
+    them."""
     text = b""
     for name in ("DESIGN.md", "README.md", "INTEGRATION.md"):
         try:
