@@ -1549,10 +1549,12 @@ static WgradPlan wgrad_plan(int64_t M, int64_t N, int64_t K) {
     if (p.nj && p.slices == 1 && tiles > cus) {
         const int64_t nn = N / (64 * p.nj), panels = (M + 255) / 256;
         const int64_t full = (tiles / cus) * cus / nn;  // row panels that fill whole rounds
-        const int tail = slices_for((panels - full) * nn);
-        if (full > 0 && full < panels && tail >= 2) {
-            p.split_rows = 256 * full;
-            p.tail_slices = tail;
+        if (full > 0 && full < panels) {
+            const int tail = slices_for((panels - full) * nn);
+            if (tail >= 2) {
+                p.split_rows = 256 * full;
+                p.tail_slices = tail;
+            }
         }
     }
     return p;

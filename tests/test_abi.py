@@ -162,6 +162,23 @@ def test_lce_workspace_and_checks(abi):
     assert lib.fx_lce_fwd(fake, 128, fake, fake, -100, None, None, None, 0, 768, 128, None) == 0
 
 
+def test_wgrad_workspace_follows_the_plan(abi):
+    # off a GPU the library plans for 256 CUs.  Fewer whole 256 x 192 tiles than CUs: K split
+    # into CUs / tiles slices, one fp32 partial each (qkv: 36 tiles, 7 slices); whole rounds:
+    # one slice, no workspace; a partly filled last round: the panels past the full rounds in
+    # CUs / (their tiles) slices (the tied head: 788 tiles, the last 20 in 12 slices over its
+    # last 1152 rows; 264 tiles of 256 x 256 at N = 1024: the last 8 in 4 slices, capped at a
+    # quarter of the 16 64-token steps, over 392 rows); too few tail slices: one product
+    lib = abi.lib()
+    ws = lib.fx_linear_wgrad_workspace
+    assert ws(2304, 768, 16384) == 7 * 2304 * 768 * 4
+    assert ws(16384, 3072, 16384) == 0
+    assert ws(50304, 768, 16384) == 12 * (50304 - 49152) * 768 * 4
+    assert ws(16776, 768, 1024) == 4 * (16776 - 16384) * 768 * 4
+    assert ws(16740, 1024, 1024) == 4 * (16740 - 16384) * 1024 * 4
+    assert ws(256 * 114, 768, 16384) == 0      # 456 tiles: the 200 past one round get 1 slice each
+
+
 def test_adamw_workspace_counts_chunks(abi):
     tl = abi.fxTensorList()
     tl.count = 3

@@ -390,6 +390,8 @@ def test_whole_tile_kernel_matches_general_kernel(dev, M, K, N, act, bias, want_
     (1024, 520, 768, 0),     # an 8-row last panel, several slices
     (16384, 50304, 768, 0),  # the cfg5 tied head: 768 tiles in one slice, the last 20 (4.5 panels) in 12
     (1024, 16776, 768, 0),   # 264 tiles: 256 in one slice, the last 1.5 panels in 4 slices
+    (1024, 16740, 1024, 0),  # 256 x 256 tiles (N % 192 != 0): 264 tiles, the last 1.4 panels in 4 slices
+    (256, 16384, 3072, 0),   # 1024 tiles: four whole rounds, one slice, no tail
 ])
 @pytest.mark.parametrize("tile", ["256", "192"])   # FX_WGRAD_TILE=256: 256 x 256 tiles; else 256 x 192 where N allows
 def test_wgrad_whole_tile_kernel_matches_general(dev, monkeypatch, T, M, N, ld_pad, tile):
