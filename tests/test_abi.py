@@ -5,6 +5,7 @@ import ctypes
 import os
 import re
 import subprocess
+import sys
 import tempfile
 
 import pytest
@@ -204,3 +205,27 @@ def test_adamw_noalloc_rejects_lists_beyond_its_scratch(abi):
     assert b"scratch" in lib.fx_last_error()
     # the largest list that fits passes this check (and would go on to the device lookup)
     assert (4 + 262140) * 4 == 1 << 20
+
+
+def test_workspace_queries_survive_edge_shapes():
+    # every workspace query over zero, negative, tiny, odd and large sizes, in a child
+    # process so that a crash (an integer division by zero in a size plan) fails this test
+    code = r"""
+import itertools, sys
+sys.path.insert(0, sys.argv[1])
+from fxgpu import abi
+lib = abi.lib()
+vals = [-1, 0, 1, 7, 8, 127, 128, 192, 256, 257, 768, 1024, 3072, 16384, 16385, 50304, 65536]
+for M, N, K in itertools.product(vals, vals, vals):
+    lib.fx_linear_wgrad_workspace(M, N, K)
+    lib.fx_lce_workspace(M, N, K)
+    lib.fx_embedding_bwd_workspace(M, N, K)
+for a, b in itertools.product(vals, vals):
+    lib.fx_rms_norm_bwd_workspace(a, b)
+for a, b, c, d in itertools.product([-1, 0, 1, 16], [-1, 0, 12], [-1, 0, 1, 512, 4096], [-1, 0, 64, 128]):
+    lib.fx_attn_decode_workspace(a, b, c, d)
+print("swept")
+"""
+    r = subprocess.run([sys.executable, "-c", code, os.path.join(ROOT, "radeon-igpu-forge_amd")],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0 and "swept" in r.stdout, (r.returncode, r.stderr[-2000:])
