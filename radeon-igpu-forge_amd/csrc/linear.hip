@@ -440,11 +440,11 @@ __device__ __forceinline__ void asm_gemm_schedule(int nsteps, uint32_t& phase, u
 // block leaves through the wave's LDS share `stg` (free once every wave is done with the
 // stages): 8-byte writes from the MFMA layout, read back and stored as 16-byte row chunks,
 // 32 NJ columns contiguous.  value(i, j, q, a, v) turns the 4 accumulators a into the
-// 4 outputs v.
+// 4 outputs v.  nt: non-temporal stores, for an output that no kernel reads soon.
 constexpr int kStgExtra = 8;  // staging row padding (elements)
 template <int NJ, class Value>
 __device__ __forceinline__ void ct_store_block(uint16_t* stg, int lane, int i, uint16_t* out, int64_t ld, int64_t row0,
-                                               int col0, const f32x16 (&acc)[4 * NJ], Value&& value, int nrows = 32) {
+                                               int col0, const f32x16 (&acc)[4 * NJ], Value&& value, int nrows = 32, bool nt = false) {
     constexpr int LDE = 32 * NJ + kStgExtra;
     const int g = lane >> 5;
 #pragma unroll
@@ -462,7 +462,13 @@ __device__ __forceinline__ void ct_store_block(uint16_t* stg, int lane, int i, u
     for (int k = 0; k < 2 * NJ; ++k) {
         const int idx = lane + 64 * k;
         const int r = idx / (4 * NJ), c = idx - r * (4 * NJ);
-        if (r < nrows) st16(out + (row0 + r) * ld + col0 + 8 * c, *reinterpret_cast<const uint4*>(stg + r * LDE + 8 * c));
+        if (r < nrows) {
+            const uint4 v = *reinterpret_cast<const uint4*>(stg + r * LDE + 8 * c);
+            if (nt)
+                st16_nt(out + (row0 + r) * ld + col0 + 8 * c, v);
+            else
+                st16(out + (row0 + r) * ld + col0 + 8 * c, v);
+        }
     }
 }
 
@@ -533,7 +539,10 @@ __global__ void __launch_bounds__(256, 1) gemm_fast_kernel(GemmArgs a) {
     fast_tile_product<NJ>(a.A, a.lda, a.B, a.ldb, a.K, m0, n0, 1 << 30, lds, wave, lane, acc);
 
     // epilogue: h = acc + bias (H, when wanted), then C = act(h), rounded as
-    // gemm_bias_act_kernel rounds them
+    // gemm_bias_act_kernel rounds them.  H (the pre-activation, which only the backward's GELU
+    // derivative reads) leaves with non-temporal stores: in the cfg5 training step that kept
+    // the caches for the data the next kernels read, 0.10-0.14 ms per step in in-process
+    // A/Bs on three boxes (C, which fc2 reads next, measured slower that way)
     uint16_t* stg = reinterpret_cast<uint16_t*>(lds + wave * G::kWaveLds);
     float bias[NJ][4][4];
 #pragma unroll
@@ -551,7 +560,7 @@ __global__ void __launch_bounds__(256, 1) gemm_fast_kernel(GemmArgs a) {
                                [&](int j, int q, const float (&v)[4], float (&o)[4]) {
 #pragma unroll
                                    for (int e = 0; e < 4; ++e) o[e] = kBias ? v[e] + bias[j][q][e] : v[e];
-                               });
+                               }, 32, true);
         ct_store_block<NJ>(stg, lane, i, a.C, a.ldc, row0, n0 + wn, acc,
                            [&](int j, int q, const float (&v)[4], float (&o)[4]) {
 #pragma unroll
