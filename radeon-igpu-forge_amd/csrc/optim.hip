@@ -274,9 +274,9 @@ using namespace fx;
 
 extern "C" int64_t fx_adamw_workspace(const fxTensorList* lists, int32_t nlists) {
     int64_t parts = 0;
-    for (int i = 0; i < nlists; ++i)
+    for (int i = 0; lists != nullptr && i < nlists; ++i)
         for (int t = 0; t < lists[i].count && t < FX_ADAMW_MAX_TENSORS; ++t)
-            parts += (lists[i].n[t] + kChunk - 1) / kChunk;
+            if (lists[i].n[t] > 0) parts += (lists[i].n[t] + kChunk - 1) / kChunk;
     return (kWorkHead + parts) * (int64_t)sizeof(float);
 }
 
@@ -301,6 +301,7 @@ static int adamw_step(const fxAdamWState* st, const fxTensorList* lists, int32_t
     for (int i = 0; i < nlists; ++i) {
         if (int e = build_chunks(lists[i], (int32_t)total, cl[i], nch[i])) return e;
         total += nch[i];
+        FX_REQUIRE(total * kOptVec < 0x7fffffff, "%s: too many chunks over the lists", who);
     }
     if (work == nullptr) {
         const int64_t need = (kWorkHead + total) * (int64_t)sizeof(float);

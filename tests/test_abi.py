@@ -187,6 +187,11 @@ def test_adamw_workspace_counts_chunks(abi):
         tl.n[i] = n
     # 1 + 2 + 1 chunks of 8192 elements, plus the 4-float header
     assert abi.lib().fx_adamw_workspace(ctypes.byref(tl), 1) == (4 + 4) * 4
+    # no lists (null pointer) and empty or negative sizes add no chunks
+    assert abi.lib().fx_adamw_workspace(None, 3) == 4 * 4
+    tl.n[1] = 0
+    tl.n[2] = -5
+    assert abi.lib().fx_adamw_workspace(ctypes.byref(tl), 1) == (4 + 1) * 4
 
 
 def test_adamw_noalloc_rejects_lists_beyond_its_scratch(abi):
