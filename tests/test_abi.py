@@ -101,6 +101,59 @@ def test_argument_checks_reject_before_launch(abi):
     assert lib.fx_rms_norm_bwd_workspace(0, 768) == 0
 
 
+# One invalid call per compute entry point: each returns FX_EINVAL with a message naming the
+# entry point before it touches the device (the pointers are fake and never dereferenced).
+_F = 4096          # a 16-byte-aligned fake device address
+_M = 4098          # a misaligned one
+
+
+def _bad_calls(abi):
+    P = ctypes.c_void_p
+    f, m = P(_F), P(_M)
+    st = abi.fxAdamWState()          # every state pointer null
+    tl = abi.fxTensorList()
+    dec = abi.fxAttnDecodeArgs()
+    dec.D, dec.B, dec.H, dec.Tmax = 96, 1, 1, 1
+    bwd = abi.fxAttnArgs()
+    bwd.D, bwd.B, bwd.T, bwd.H, bwd.scale = 64, 1, 64, 1, 0.125
+    bwd.q = bwd.k = bwd.v = _F       # o, dout, lse, delta, dq, dk, dv null
+    return [
+        ("fx_fill_f32", (f, -1, 0.0, None)),
+        ("fx_rms_norm_fwd_add", (f, f, f, m, f, f, 4, 8, 1e-6, None)),
+        ("fx_rms_norm_bwd", (f, f, f, f, f, None, None, f, 4, 768, None)),
+        ("fx_rms_norm_bwd_add", (f, f, None, f, f, f, f, None, f, 4, 768, None)),
+        ("fx_ce_inv_nvalid", (f, 4, -100, None, 1.0, None, f, None)),
+        ("fx_ce_loss_finalize", (f, 4, None, f, None)),
+        ("fx_ce_scale_grad", (f, 8, f, f, 2, None)),
+        ("fx_ce_lin_grad_scale", (f, -1, f, 8, f, None, 1.0, f, f, None)),
+        ("fx_ce_lin_grad_scale_bf16w", (f, 8, m, 8, f, None, 1.0, f, f, None)),
+        ("fx_ce_lin_grad_scale_inplace", (m, 8, f, 8, f, None, 1.0, None)),
+        ("fx_adamw_step_noalloc", (ctypes.byref(st), ctypes.byref(tl), 1, None)),
+        ("fx_attn_bwd", (ctypes.byref(bwd), None)),
+        ("fx_attn_decode", (ctypes.byref(dec), None)),
+        ("fx_linear_fwd", (f, 8, None, 0, 0, f, None, f, None, None, 4, 8, 7, 0, None)),
+        ("fx_linear_fwd_ex", (None, None)),
+        ("fx_gelu_bwd", (f, m, f, 8, None)),
+        ("fx_linear_dgrad", (f, 768, f, 768, None, f, 768, 100, 768, 768, None)),
+        ("fx_linear_wgrad", (f, 12, f, 8, f, 8, None, 12, 8, 16, None)),
+        ("fx_lce_fwd", (f, 768, f, f, -100, f, f, f, 256, 1000, 768, None)),
+        ("fx_lce_grad", (f, 768, None, f, -100, f, f, f, 768, 256, 768, 768, None)),
+    ]
+
+
+def test_every_entry_point_rejects_bad_arguments_before_launch(abi):
+    lib = abi.lib()
+    calls = _bad_calls(abi)
+    compute = {n for n in abi.SIGNATURES if not n.endswith("_workspace")} - {"fx_abi_version", "fx_last_error"}
+    covered = {n for n, _ in calls} | {"fx_rms_norm_fwd", "fx_ce_fwd_grad", "fx_attn_fwd", "fx_adamw_step",
+                                       "fx_embedding_bwd"}   # covered by the tests around this one
+    assert compute <= covered, sorted(compute - covered)
+    for name, args in calls:
+        rc = getattr(lib, name)(*args)
+        assert rc == abi.FX_EINVAL, (name, rc)
+        assert lib.fx_last_error().decode().startswith(name), (name, lib.fx_last_error())
+
+
 def test_embedding_bwd_checks_and_workspace(abi):
     lib = abi.lib()
     fake = ctypes.c_void_p(4096)     # never dereferenced: the checks fail first
