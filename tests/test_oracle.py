@@ -125,7 +125,7 @@ def test_ce_matches_torch(N, V):
     lr = lg.clone().requires_grad_()
     ref = F.cross_entropy(lr, tg, ignore_index=-100)
     ref.backward()
-    assert abs(float(loss) - float(ref)) < 1e-12
+    assert abs(loss.item() - ref.item()) < 1e-12
     assert torch.allclose(grad, lr.grad, atol=1e-14)
 
 
@@ -156,7 +156,7 @@ def test_linear_ce_matches_autograd():
     xr, Wr = x.clone().requires_grad_(), W.clone().requires_grad_()
     ref = F.cross_entropy(xr @ Wr.t(), tg, ignore_index=-100)
     ref.backward()
-    assert abs(float(loss) - float(ref)) < 1e-12
+    assert abs(loss.item() - ref.item()) < 1e-12
     assert torch.allclose(dx, xr.grad, atol=1e-13) and torch.allclose(dW, Wr.grad, atol=1e-13)
 
 
@@ -324,8 +324,8 @@ def test_cpu_gpt_init_scales():
         else:
             assert torch.equal(p, torch.ones_like(p)), name
             continue
-        assert abs(float(p.std()) / want - 1) < 0.03, name
-        assert abs(float(p.mean())) < 0.1 * want, name
+        assert abs(p.detach().std().item() / want - 1) < 0.03, name
+        assert abs(p.detach().mean().item()) < 0.1 * want, name
 
 
 def test_cpu_gpt_block_from_definitions():
