@@ -421,7 +421,7 @@ def test_cpu_gpt_matches_fxlm_torch_path():
     l_fx, l_o = fx(idx, tgt), m(idx, tgt)
     l_fx.backward()
     l_o.backward()
-    assert abs(float(l_fx) - float(l_o)) <= 1e-6 * abs(float(l_o))
+    assert abs(l_fx.item() - l_o.item()) <= 1e-6 * abs(l_o.item())
     op = dict(m.named_parameters())
     for name, p in fx.named_parameters():
         r = op[name].grad
