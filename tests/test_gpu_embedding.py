@@ -24,6 +24,7 @@ def _case(n, V, D, lo=0, seed=0, ld=None, same=None):
     (2500, 7, 16, 0, 3, None),           # every position the same id: one sum of 2500 rows
     (1030, 8, 24, -3, None, None),       # ids outside [0, V) add nothing
     (1, 5, 8, 0, None, None),
+    (0, 10, 16, 0, None, None),          # no positions: every row zero
     (1024, 1, 8, 0, None, None),         # one chunk exactly, one id
     (700, 300, 40, 0, None, 48),         # rows of dy strided (ld 48 > D 40)
     (16384, 50304, 768, 0, None, None),  # the cfg5 step's lookup
