@@ -38,6 +38,13 @@ constexpr float kLazyRescale = 8.f;
 
 __device__ __forceinline__ bf16x8 as_bf16x8(const uint4& v) { return __builtin_bit_cast(bf16x8, v); }
 
+// v with every bit cleared unless keep is all ones (a per-lane zeroing by bitwise and: a
+// select between two vectors can become a select between their addresses, which puts
+// the vectors in scratch memory)
+__device__ __forceinline__ uint4 mask16(const uint4& v, uint32_t keep) {
+    return make_uint4(v.x & keep, v.y & keep, v.z & keep, v.w & keep);
+}
+
 // 8 fp32 accumulator values (elements 8h..8h+7) -> bf16x8 operand
 __device__ __forceinline__ bf16x8 pack_op(const f32x16& c, int h) {
     const f32x8 v = h == 0 ? __builtin_shufflevector(c, c, 0, 1, 2, 3, 4, 5, 6, 7)
@@ -202,6 +209,7 @@ struct TileDma2 {
     static constexpr int NI = R * SPR / 64;  // wave instructions per tile
     static_assert(R * SPR % 64 == 0, "tile must be a whole number of wave loads");
     static constexpr int PW = (2 * NI + kAttWaves - 1) / kAttWaves;  // per wave, at most
+    static_assert(4 * kAttWaves <= 2 * NI, "every wave issues at least four loads per tile pair");
     uint32_t off[PW];  // byte offset of this lane's chunk from the tile's first row
     int wave;
     // tile row and in-row chunk of this lane's slot in wave instruction i
@@ -221,10 +229,39 @@ struct TileDma2 {
             off[k] = (uint32_t)(r * (i < NI ? rs0 : rs1) + c * 8) * 2u;
         }
     }
+    // the source base and LDS destination of this wave's load k (wave-uniform)
+    __device__ __forceinline__ void target(int k, const uint16_t* first0, const uint16_t* first1,
+                                           const uint16_t* lds0, const uint16_t* lds1, const uint16_t*& base,
+                                           uint32_t& dst) const {
+        const int i = wave + k * kAttWaves;
+        const bool second = i >= NI;
+        base = second ? first1 : first0;
+        dst = lds_addr((second ? lds1 : lds0) + (i - (second ? NI : 0)) * 64 * 8);
+    }
     // first0/first1: the tiles' first rows in global memory; rows >= valid read zeros
     __device__ __forceinline__ void issue(const uint16_t* first0, const uint16_t* first1, int valid,
                                           const uint16_t* lds0, const uint16_t* lds1) const {
         const bool full = valid >= R;  // wave-uniform: every row of the tile exists
+        if (full) {
+            // straight-line: the first four loads of every wave exist (4 kAttWaves <= 2 NI)
+            const uint16_t *b0, *b1, *b2, *b3;
+            uint32_t d0, d1, d2, d3;
+            target(0, first0, first1, lds0, lds1, b0, d0);
+            target(1, first0, first1, lds0, lds1, b1, d1);
+            target(2, first0, first1, lds0, lds1, b2, d2);
+            target(3, first0, first1, lds0, lds1, b3, d3);
+            dma16_so_x4(b0, off[0], d0, b1, off[1], d1, b2, off[2], d2, b3, off[3], d3);
+#pragma unroll
+            for (int k = 4; k < PW; ++k) {
+                if (wave + k * kAttWaves < 2 * NI) {
+                    const uint16_t* b;
+                    uint32_t d;
+                    target(k, first0, first1, lds0, lds1, b, d);
+                    dma16_so(b, off[k], d);
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int k = 0; k < PW; ++k) {
             const int i = wave + k * kAttWaves;
@@ -295,6 +332,10 @@ __global__ void __launch_bounds__(kAttThreads) attn_fwd_kernel(fxAttnArgs a) {
     TileDma2<D, kBN, SW> dma;
     dma.init(a.kst, a.vst);
     dma.issue(kbase, vbase, T, sk0, sv0);
+    // the next tile's first K and V rows, advanced by one tile per step
+    const int64_t kstep = (int64_t)kBN * a.kst, vstep = (int64_t)kBN * a.vst;
+    const uint16_t* kn = kbase;
+    const uint16_t* vn = vbase;
 
     bf16x8 qop[DC];
     {
@@ -317,9 +358,9 @@ __global__ void __launch_bounds__(kAttThreads) attn_fwd_kernel(fxAttnArgs a) {
     auto step = [&](int j, const uint16_t* K, const uint16_t* V, uint16_t* nK, uint16_t* nV) {
         const int kb = j * kBN;
         tile_arrive();
-        if (j + 1 < nblk)
-            dma.issue(kbase + (int64_t)(kb + kBN) * a.kst, vbase + (int64_t)(kb + kBN) * a.vst,
-                      T - kb - kBN, nK, nV);
+        kn += kstep;
+        vn += vstep;
+        if (j + 1 < nblk) dma.issue(kn, vn, T - kb - kBN, nK, nV);
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             const int kh = kb + 32 * hh;  // first key of this half
@@ -429,35 +470,46 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dq_kern
     TileDma2<D, kBN, SW> dma;
     dma.init(a.kst, a.vst);
     dma.issue(kbase, vbase, T, sk0, sv0);
+    // the next tile's first K and V rows, advanced by one tile per step
+    const int64_t kstep = (int64_t)kBN * a.kst, vstep = (int64_t)kBN * a.vst;
+    const uint16_t* kn = kbase;
+    const uint16_t* vn = vbase;
 
-    // this lane's lse, read before the Delta store below (a load after a store to
-    // another fp32 array may not be moved above it: one more memory round trip)
-    const float lse2 = qok ? a.lse[(int64_t)bh * T + qi] * kLog2e : 0.f;
-    // Q^T and dO^T operands, Delta = rowsum(dO * O) for this lane's query
+    // This lane's lse (read before the Delta store below: a load after a store to another
+    // fp32 array may not be moved above it), Q^T and dO^T operands and O row: every load is
+    // issued before any is used, and the lse is scaled only after Delta, so the wave makes
+    // one memory round trip here.  Rows past T read row 0 and are zeroed after.
+    const float lse_raw = qok ? a.lse[(int64_t)bh * T + qi] : 0.f;
     bf16x8 qop[DC], dop[DC];
     float delta = 0.f;
     {
         const uint16_t* qrow = a.q + b * a.qsb + h * a.qsh + (int64_t)(qok ? qi : 0) * a.qst;
         const int64_t orow = (((int64_t)b * T + (qok ? qi : 0)) * a.H + h) * D;
+        uint4 qv[DC], dv[DC], ov[DC];
 #pragma unroll
         for (int c = 0; c < DC; ++c) {
-            uint4 qv = make_uint4(0u, 0u, 0u, 0u), dv = qv, ov = qv;
-            if (qok) {
-                qv = ld16(qrow + 16 * c + 8 * g);
-                dv = ld16(a.dout + orow + 16 * c + 8 * g);
-                ov = ld16(a.o + orow + 16 * c + 8 * g);
-            }
-            qop[c] = as_bf16x8(qv);
-            dop[c] = as_bf16x8(dv);
+            qv[c] = ld16(qrow + 16 * c + 8 * g);
+            dv[c] = ld16(a.dout + orow + 16 * c + 8 * g);
+            ov[c] = ld16(a.o + orow + 16 * c + 8 * g);
+        }
+        const uint32_t keep = qok ? ~0u : 0u;
+#pragma unroll
+        for (int c = 0; c < DC; ++c) {
+            const uint4 d = mask16(dv[c], keep), o = mask16(ov[c], keep);
+            qop[c] = as_bf16x8(mask16(qv[c], keep));
+            dop[c] = as_bf16x8(d);
             float fd[8], fo[8];
-            unpack8(dv, fd);
-            unpack8(ov, fo);
+            unpack8(d, fd);
+            unpack8(o, fo);
 #pragma unroll
             for (int j = 0; j < 8; ++j) delta += fd[j] * fo[j];
         }
         delta = pair_sum(delta);
         if (qok && g == 0) a.delta[(int64_t)bh * T + qi] = delta;
     }
+    float lse_l = lse_raw;
+    __asm__ volatile("" : "+v"(lse_l));  // scaled here, after Delta, not where it is loaded
+    const float lse2 = lse_l * kLog2e;
     const float sl2 = a.scale * kLog2e;
 
     f32x16 acc[DT];
@@ -467,9 +519,9 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dq_kern
     auto step = [&](int j, const uint16_t* K, const uint16_t* V, uint16_t* nK, uint16_t* nV) {
         const int kb = j * kBN;
         tile_arrive();
-        if (j + 1 < nblk)
-            dma.issue(kbase + (int64_t)(kb + kBN) * a.kst, vbase + (int64_t)(kb + kBN) * a.vst,
-                      T - kb - kBN, nK, nV);
+        kn += kstep;
+        vn += vstep;
+        if (j + 1 < nblk) dma.issue(kn, vn, T - kb - kBN, nK, nV);
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             const int kh = kb + 32 * hh;
@@ -548,33 +600,46 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dkv_ker
     const int nblk = (T - qstart + kBQ - 1) / kBQ;
 
     // Q / dO tiles by DMA; the tile's lse and Delta through one register each
-    // (threads 0..63), stored to LDS once they have arrived
+    // (threads 0..63), stored to LDS once they have arrived.  The lse is kept raw until
+    // then: scaling it where it is loaded makes the wave wait for that load, and with it
+    // for the tile loads issued just before (memory loads complete in order), at every
+    // tile.
     TileDma2<D, kBQ, SW> dma;
     dma.init(a.qst, dors);
     float rl = 0.f, rdl = 0.f;
+    // the next tile's first Q and dO rows, advanced by one tile per issue
+    const int64_t qstep = (int64_t)kBQ * a.qst, dostep = (int64_t)kBQ * dors;
+    const uint16_t* qn = qbase + (int64_t)qstart * a.qst;
+    const uint16_t* don = dobase + (int64_t)qstart * dors;
     auto issue = [&](int qb, const uint16_t* nQ, const uint16_t* nDO) {
-        dma.issue(qbase + (int64_t)qb * a.qst, dobase + (int64_t)qb * dors, T - qb, nQ, nDO);
+        dma.issue(qn, don, T - qb, nQ, nDO);
+        qn += qstep;
+        don += dostep;
         if (threadIdx.x < kBQ) {
             const int q = qb + threadIdx.x;
-            rl = q < T ? lse_bh[q] * kLog2e : 0.f;
+            rl = q < T ? lse_bh[q] : 0.f;
             rdl = q < T ? del_bh[q] : 0.f;
         }
     };
     if (nblk > 0) issue(qstart, sq0, sdo0);
 
+    // K and V rows of this lane's key: every load issued before any is used (rows past T
+    // read row 0 and are zeroed after)
     bf16x8 kop[DC], vop[DC];
     {
         const uint16_t* krow = a.k + b * a.ksb + h * a.ksh + (int64_t)(kok ? ki : 0) * a.kst;
         const uint16_t* vrow = a.v + b * a.vsb + h * a.vsh + (int64_t)(kok ? ki : 0) * a.vst;
+        uint4 kv[DC], vv[DC];
 #pragma unroll
         for (int c = 0; c < DC; ++c) {
-            uint4 kv = make_uint4(0u, 0u, 0u, 0u), vv = kv;
-            if (kok) {
-                kv = ld16(krow + 16 * c + 8 * g);
-                vv = ld16(vrow + 16 * c + 8 * g);
-            }
-            kop[c] = as_bf16x8(kv);
-            vop[c] = as_bf16x8(vv);
+            kv[c] = ld16(krow + 16 * c + 8 * g);
+            vv[c] = ld16(vrow + 16 * c + 8 * g);
+        }
+        const uint32_t keep = kok ? ~0u : 0u;
+#pragma unroll
+        for (int c = 0; c < DC; ++c) {
+            kop[c] = as_bf16x8(mask16(kv[c], keep));
+            vop[c] = as_bf16x8(mask16(vv[c], keep));
         }
     }
     const float sl2 = a.scale * kLog2e;
@@ -591,7 +656,7 @@ __global__ void __launch_bounds__(kAttThreads, D == 64 ? 2 : 1) attn_bwd_dkv_ker
         const int st = j & 1;
         __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's tile loads and rl / rdl
         if (threadIdx.x < kBQ) {
-            slse[st][threadIdx.x] = rl;
+            slse[st][threadIdx.x] = rl * kLog2e;
             sdelta[st][threadIdx.x] = rdl;
         }
         __syncthreads();

@@ -184,6 +184,36 @@ __device__ __forceinline__ void dma16_so(const void* sbase, uint32_t voff, uint3
         : "v"(voff), "s"(sbase), "s"(lds)
         : "memory");
 }
+// Four dma16_so loads in one statement, M0 saved and restored once (one statement per load
+// spends two more M0 moves per load on saving and restoring it).
+__device__ __forceinline__ void dma16_so_x4(const void* b0, uint32_t o0, uint32_t l0, const void* b1, uint32_t o1,
+                                            uint32_t l1, const void* b2, uint32_t o2, uint32_t l2, const void* b3,
+                                            uint32_t o3, uint32_t l3) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %3\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %2\n\t"
+        "s_nop 0\n\t"
+        "s_mov_b32 m0, %6\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %4, %5\n\t"
+        "s_nop 0\n\t"
+        "s_mov_b32 m0, %9\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %7, %8\n\t"
+        "s_nop 0\n\t"
+        "s_mov_b32 m0, %12\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %10, %11\n\t"
+        "s_nop 0\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(o0), "s"(b0), "s"(l0), "v"(o1), "s"(b1), "s"(l1), "v"(o2), "s"(b2), "s"(l2), "v"(o3), "s"(b3),
+          "s"(l3)
+        : "memory");
+}
 // global_load_lds_dword: 4 bytes per active lane to lds + 4 * lane (same protocol as dma16)
 __device__ __forceinline__ void dma4(const void* src, uint32_t lds) {
     uint32_t saved;
