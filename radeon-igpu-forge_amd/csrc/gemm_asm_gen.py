@@ -29,7 +29,7 @@ cannot name.
 Per step: the first half runs 4 NJ MFMAs on chunk 0 while the reads of chunk 1 follow the
 first MFMAs; `s_waitcnt vmcnt` for the next stage's loads, `lgkmcnt(0)` and `s_barrier`
 (every wave is then done reading this stage); the second half runs chunk 1's MFMAs with the
-reads of the next step's chunk 0 and, after its last 8 MFMAs, this stage's loads of step
+reads of the next step's chunk 0 and, spread evenly over its MFMAs, this stage's loads of step
 j + 4 (`global_load_lds_dwordx4`, L per wave; instruction q = wave + 4 t of a stage covers 64
 16-byte slots, the M-side's, then the N-side's, then a never-read pad that rounds the count
 to a multiple of 4), each pointer then advanced by its stride (one SGPR pair per t: the
@@ -134,13 +134,15 @@ def generate(kd):
         return [block_reads(kd, b, x, stage, ch) for x in range(kd.set_size)]
 
     def loads(stage):
-        groups = [[] for _ in range(8)]
-        slot = [0, 0, 1, 1, 2, 3, 4, 5, 6, 7][:kd.loads] if kd.loads == 10 else [0, 0, 1, 2, 3, 4, 5, 6, 7]
+        # spread evenly over the half step's MFMAs: issued in bursts (the last 8 MFMAs) the
+        # loads of the four waves queued up in the address unit and delayed MFMA issue
+        groups = [[] for _ in range(n_mfma)]
         for t in range(kd.loads):
-            groups[slot[t]] += [f"s_add_u32 m0, %{kd.sbase}, {stage * kd.stage + 4096 * t}", "s_nop 0",
-                                f"global_load_lds_dwordx4 %{kd.ptr0 + t}, off", "s_nop 0"]
+            groups[(t * n_mfma) // kd.loads] += [
+                f"s_add_u32 m0, %{kd.sbase}, {stage * kd.stage + 4096 * t}", "s_nop 0",
+                f"global_load_lds_dwordx4 %{kd.ptr0 + t}, off", "s_nop 0"]
         for t in range(kd.loads):
-            groups[7].append(f"v_lshl_add_u64 %{kd.ptr0 + t}, %{kd.ptr0 + t}, 0, %{kd.stride0 + t}")
+            groups[n_mfma - 1].append(f"v_lshl_add_u64 %{kd.ptr0 + t}, %{kd.ptr0 + t}, 0, %{kd.stride0 + t}")
         return groups
 
     def mfma(k, cur):
@@ -151,14 +153,13 @@ def generate(kd):
 
     def half(cur, rd, extra):
         e("s_waitcnt lgkmcnt(0)")
-        dma_from = n_mfma - 8
         for k in range(n_mfma):
             mfma(k, cur)
             if rd and k < len(rd):
                 for x in rd[k]:
                     e(x)
-            if extra and k >= dma_from:
-                for x in extra[k - dma_from]:
+            if extra:
+                for x in extra[k]:
                     e(x)
 
     def step(u, vm, do_load, next_reads):
