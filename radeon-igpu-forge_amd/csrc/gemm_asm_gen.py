@@ -12,12 +12,16 @@ accumulators stay in AGPRs for the whole K loop (one inline-asm statement):
   wgrad  C = dY^T X     dY (K x M), X (K x N): both col operands (K = tokens)
 
 K advances in steps of 32 held in 4 LDS stages.  A stage holds the M-side operand's tile,
-then the N-side's:
-  row operand: one LDS row per tile row, 80 bytes (32 bf16 + 16 of padding: the 32 rows
-    of a read fall in distinct banks); an operand block is one `ds_read_b128`, lane l taking
-    row l%32 and K 8 (l/32) + 0..7;
-  col operand: one LDS row per K (32 rows), the tile's columns + 32 bf16 of padding (the 4
-    rows of a transposed read fall in disjoint banks); an operand block is two
+then the N-side's.  The loops with a row operand (fwd, dgrad) keep the stages in two
+buffers of two steps and load a buffer every other step: a row's segments of both steps are
+then one 128-byte run (a whole cache line: loaded one 64-byte step at a time, every line was
+requested twice, and from HBM those requests, not the bytes, set the pace: 1-8 % faster
+when the operands come from HBM).  The weight gradient keeps four one-step buffers.
+  row operand: one LDS row per tile row, 144 bytes in a two-step buffer (2 x 32 bf16 and
+    16 of padding), 80 in a one-step one (the 32 rows of a read fall in distinct banks); an
+    operand block is one `ds_read_b128`, lane l taking row l%32 and K 8 (l/32) + 0..7;
+  col operand: one LDS row per K (32 rows per step), the tile's columns + 32 bf16 of
+    padding (the 4 rows of a transposed read fall in disjoint banks); an operand block is two
     `ds_read_b64_tr_b16` (4 K each).  With a row operand on the other side (dgrad) the two
     reads take K 8 g + 0..3 and 8 g + 4..7 (g = l/32), the row operand's order; in wgrad both
     sides take 4 g + 0..3 and 8 + 4 g + 0..3 (fx_mfma.h's lds_op_t, the general kernel's
@@ -29,20 +33,25 @@ cannot name.
 Per step: the first half runs 4 NJ MFMAs on chunk 0 while the reads of chunk 1 follow the
 first MFMAs; `s_waitcnt vmcnt` for the next stage's loads, `lgkmcnt(0)` and `s_barrier`
 (every wave is then done reading this stage); the second half runs chunk 1's MFMAs with the
-reads of the next step's chunk 0 and, spread evenly over its MFMAs, this stage's loads of step
-j + 4 (`global_load_lds_dwordx4`, L per wave; instruction q = wave + 4 t of a stage covers 64
-16-byte slots, the M-side's, then the N-side's, then a never-read pad that rounds the count
-to a multiple of 4), each pointer then advanced by its stride (one SGPR pair per t: the
-region of instruction q may differ between waves).  Loads run three steps ahead (the data
-of a step is requested about three steps of MFMA time before it is read, enough for loads
-that miss the caches): at the barrier of step j only the loads of steps j + 2 and j + 3 may
-be outstanding (`vmcnt(2 L)`), fewer in the last three steps.  The operands rotate through
-4 register sets (one per half step, refilled three halves after the MFMAs that read it).
+reads of the next step's chunk 0 and, spread evenly over its MFMAs, the loads of the buffer
+every wave has just finished reading (`global_load_lds_dwordx4`, L per wave; instruction
+q = wave + 4 t of a buffer covers 64 16-byte slots, the M-side's, then the N-side's, then a
+never-read pad that rounds the count to a multiple of 4), each pointer then advanced by its
+stride (one SGPR pair per t: the region of instruction q may differ between waves).
+One-step buffers: each step loads step j + 4, three steps ahead; at the barrier of step j
+only the loads of steps j + 2 and j + 3 may be outstanding (`vmcnt(2 L)`), fewer in the last
+three steps.  Two-step buffers: odd steps load steps j + 3 and j + 4 into the buffer of j - 1
+and j; the barrier before a buffer's first step is read waits for it (`vmcnt(0)`, nothing was
+issued after it), the other barriers need no wait (the second step came with the first).
+The operands rotate through 4 register sets (one per half step, refilled three halves after
+the MFMAs that read it).
 
 Any number of steps >= 4: the loop body is 4 steps (stages rotate with period 4, operand sets
 with period 2) and the last 4 steps are a tail without loads, so a product of n steps enters
 the body at step p = (4 - n % 4) % 4 (`phase`), its prologue having loaded steps 0..3 into
-stages p, p + 1, p + 2, p + 3 (mod 4).
+stages p, p + 1, p + 2, p + 3 (mod 4).  Two-step buffers take an even n: an odd K / 32 gets a
+leading step of zeros (loop_steps), which the prologue loads from the zero line and which adds
+exact zeros to the accumulators.
 
 Operands of each loop (FX_<KIND>_OUTS / _INS / _CLOBBERS): acc[4 j + i] ("+a"; i: M-side
 block, j: N-side block), the L load pointers P[t] ("+v", 64-bit), the loop iterations
@@ -67,20 +76,29 @@ class Kind:
         self.set_size = 4 + nj                        # operand blocks per set
         self.fb = 256 - 4 * SETS * self.set_size      # first VGPR of the operand sets
         self.n_acc = 4 * nj
-        self.region = []                              # (mode, bytes, wave-instructions) per side
+        # Two-step buffers when an operand has K along its rows: a row operand's 64-byte
+        # segment of one step is half of a 128-byte line, and loading each row's segments of
+        # two steps together (one 128-byte run per row) halves the cache-line requests; so
+        # the four stages are two buffers of two steps, loaded every other step.
+        self.pair = "row" in (m_mode, n_mode)
+        self.ksteps = 2 if self.pair else 1           # K steps of 32 per buffer
+        self.bufs = STAGES // self.ksteps             # LDS buffers
+        self.row_stride = 144 if self.pair else 80    # LDS bytes per row of a row operand
+        self.region = []                              # (mode, bytes, wave-instructions) per buffer side
         for mode, rows in ((m_mode, 256), (n_mode, 64 * nj)):
             if mode == "row":
-                self.region.append(("row", rows * 80, rows * 5 // 64))
+                self.region.append(("row", rows * self.row_stride, rows * self.row_stride // 1024))
             else:
                 row_bytes = (rows + 32) * 2
-                self.region.append(("col", 32 * row_bytes, 32 * row_bytes // 1024))
-        self.col_row = {side: (self.region[side][1] // 32 if self.region[side][0] == "col" else None)
+                nb = 32 * self.ksteps * row_bytes
+                self.region.append(("col", nb, nb // 1024))
+        self.col_row = {side: ((64 * (nj if side else 4) + 32) * 2 if self.region[side][0] == "col" else None)
                         for side in (0, 1)}
         n_ins = self.region[0][2] + self.region[1][2]
         self.loads = -(-n_ins // 4)                   # L
         self.pad_ins = 4 * self.loads - n_ins
-        self.stage = 1024 * 4 * self.loads
-        self.n_off = self.region[0][1]                # N-side region offset in a stage
+        self.stage = 1024 * 4 * self.loads            # bytes of one buffer
+        self.n_off = self.region[0][1]                # N-side region offset in a buffer
         # operand numbers
         self.acc0 = 0
         self.ptr0 = self.n_acc
@@ -119,7 +137,7 @@ def block_reads(kd, b, x, stage, ch):
     base = (kd.vm0 if side == 0 else kd.vn0) + stage
     r = kd.freg(b, x)
     if kd.region[side][0] == "row":
-        return [f"ds_read_b128 v[{r}:{r + 3}], %{base} offset:{32 * ch + 2560 * blk}"]
+        return [f"ds_read_b128 v[{r}:{r + 3}], %{base} offset:{32 * ch + 32 * kd.row_stride * blk}"]
     lo = ch * 16 * kd.col_row[side] + 64 * blk
     return [f"ds_read_b64_tr_b16 v[{r}:{r + 1}], %{base} offset:{lo}",
             f"ds_read_b64_tr_b16 v[{r + 2}:{r + 3}], %{base} offset:{lo + kd.hi_off(side)}"]
@@ -145,6 +163,17 @@ def generate(kd):
             groups[n_mfma - 1].append(f"v_lshl_add_u64 %{kd.ptr0 + t}, %{kd.ptr0 + t}, 0, %{kd.stride0 + t}")
         return groups
 
+    def loads_buf(buf):
+        # a two-step buffer's loads, spread evenly over the half step's MFMAs
+        groups = [[] for _ in range(n_mfma)]
+        for t in range(kd.loads):
+            groups[(t * n_mfma) // kd.loads] += [
+                f"s_add_u32 m0, %{kd.sbase}, {buf * kd.stage + 4096 * t}", "s_nop 0",
+                f"global_load_lds_dwordx4 %{kd.ptr0 + t}, off", "s_nop 0"]
+        for t in range(kd.loads):
+            groups[n_mfma - 1].append(f"v_lshl_add_u64 %{kd.ptr0 + t}, %{kd.ptr0 + t}, 0, %{kd.stride0 + t}")
+        return groups
+
     def mfma(k, cur):
         j, i = k // 4, k % 4
         m_reg, n_reg = kd.freg(cur, i), kd.freg(cur, 4 + j)
@@ -165,18 +194,37 @@ def generate(kd):
     def step(u, vm, do_load, next_reads):
         c0, c1, c2 = (2 * u) % SETS, (2 * u + 1) % SETS, (2 * u + 2) % SETS
         half(c0, reads(c1, u % STAGES, 1), None)
-        e(f"s_waitcnt vmcnt({vm})")
+        if vm is not None:
+            e(f"s_waitcnt vmcnt({vm})")
         e("s_waitcnt lgkmcnt(0)")
         e("s_barrier")
-        half(c1, reads(c2, (u + 1) % STAGES, 0) if next_reads else None, loads(u % STAGES) if do_load else None)
+        if not do_load:
+            ld = None
+        elif kd.pair:   # both steps of buffer u // 2 are read by now (odd u)
+            ld = loads_buf(u // 2) if u % 2 else None
+        else:
+            ld = loads(u % STAGES)
+        half(c1, reads(c2, (u + 1) % STAGES, 0) if next_reads else None, ld)
 
+    L = kd.loads
+    if kd.pair:
+        # at the barrier of step k the loads of step k + 1 must have landed: at an even stage
+        # k + 1 shares step k's buffer (landed already), at an odd one its buffer is the last
+        # issued (vmcnt(0)); the prologue loaded two buffers, the first of which the entry
+        # step reads
+        body_vm, tail_vm, entry_vm = [None, 0, None, 0], [None, 0, None, None], L
+    else:
+        body_vm = [(STAGES - 2) * L] * STAGES
+        tail_vm = [max(0, STAGES - 2 - u) * L for u in range(STAGES)]
+        entry_vm = (STAGES - 1) * L
     e(f"s_mov_b32 %{kd.m0s}, m0")
-    e(f"s_waitcnt vmcnt({(STAGES - 1) * kd.loads})")
+    e(f"s_waitcnt vmcnt({entry_vm})")
     e("s_barrier")
-    for p in range(1, STAGES):
+    entries = range(0, STAGES, kd.ksteps)   # two-step buffers: even step counts, even phases
+    for p in entries[1:]:
         e(f"s_cmp_eq_u32 %{kd.phase}, {p}")
         e(f"s_cbranch_scc1 .Lp{p}%=")
-    for p in range(STAGES):
+    for p in entries:
         if p:
             e(f".Lp{p}%=:")
         for blk in reads((2 * p) % SETS, p, 0):
@@ -188,22 +236,27 @@ def generate(kd):
         e(f"s_branch .Lu{p}%=")
     for u in range(STAGES):
         e(f".Lu{u}%=:")
-        step(u, (STAGES - 2) * kd.loads, True, True)
+        step(u, body_vm[u], True, True)
     e(f"s_sub_u32 %{kd.iters}, %{kd.iters}, 1")
     e(f"s_cmp_lg_u32 %{kd.iters}, 0")
     e("s_cbranch_scc1 .Lu0%=")
     e(".Ltail%=:")
     for u in range(STAGES):   # the last STAGES steps: no loads; the next step's were issued
-        left = max(0, STAGES - 2 - u)
-        step(u, left * kd.loads, False, u < STAGES - 1)
+        step(u, tail_vm[u], False, u < STAGES - 1)
     for _ in range(8):  # the last MFMAs' results before the compiler reads the AGPRs
         e("s_nop 7")
     e(f"s_mov_b32 m0, %{kd.m0s}")
     return out
 
 
+def loop_steps(kd, nsteps):
+    """K steps the loop runs for a product of nsteps: two-step buffers take an even count, a
+    leading step of zeros (loaded from the zero line by the prologue) making up an odd one"""
+    return nsteps + (nsteps % 2 if kd.pair else 0)
+
+
 def schedule(nsteps):
-    """(phase, iterations) for a product of nsteps K steps"""
+    """(phase, iterations) for a loop of nsteps K steps"""
     p = (STAGES - nsteps % STAGES) % STAGES
     return p, (nsteps - STAGES + p) // STAGES
 
@@ -215,7 +268,7 @@ def decode_read(kd, ins):
         assert int(m[2]) == reg + 3
         side = 0 if kd.vm0 <= op < kd.vm0 + STAGES else 1
         assert kd.region[side][0] == "row", ("b128 read of a col operand", ins)
-        blk, r = divmod(off, 2560)
+        blk, r = divmod(off, 32 * kd.row_stride)
         ch, r = divmod(r, 32)
         assert r == 0 and ch in (0, 1) and blk < 4
         return reg, None, side, op - (kd.vm0 if side == 0 else kd.vn0), ch, blk
@@ -251,7 +304,9 @@ def check(kd, nsteps):
     sreg = {kd.iters: iters, kd.phase: phase}
     stage_of = lambda j: (j + phase) % STAGES  # noqa: E731
     L = kd.loads
-    vmq = [(stage_of(j), j) for j in range(STAGES) for _ in range(L)]
+    kst = kd.ksteps
+    # each load instruction fills its slots of one buffer: kst consecutive steps, one stage each
+    vmq = [[(stage_of(j0 + i), j0 + i) for i in range(kst)] for j0 in range(0, STAGES, kst) for _ in range(L)]
     stage_data = {stage_of(j): [j, L, None] for j in range(STAGES)}
     ptr_step = {kd.ptr0 + t: STAGES for t in range(L)}
     loaded = {}
@@ -285,12 +340,12 @@ def check(kd, nsteps):
             sreg[int(m[1])] -= 1
         elif m := re.match(r"s_waitcnt vmcnt\((\d+)\)$", ins):
             while len(vmq) > int(m[1]):
-                st, j = vmq.pop(0)
-                d = stage_data[st]
-                assert d[0] == j
-                d[1] -= 1
-                if d[1] == 0:
-                    d[2] = pos
+                for st, j in vmq.pop(0):
+                    d = stage_data[st]
+                    assert d[0] == j
+                    d[1] -= 1
+                    if d[1] == 0:
+                        d[2] = pos
         elif ins == "s_waitcnt lgkmcnt(0)":
             for reg, val, st in pending:
                 reg_holds[reg] = val
@@ -336,25 +391,29 @@ def check(kd, nsteps):
             m0 = int(m[2])
         elif m := re.match(r"global_load_lds_dwordx4 %(\d+), off$", ins):
             p = int(m[1])
-            j = ptr_step[p]
-            st, rel = divmod(m0, kd.stage)
+            j0 = ptr_step[p]
+            buf, rel = divmod(m0, kd.stage)
             t = p - kd.ptr0
-            assert j < nsteps and st == stage_of(j), ("load of the wrong step or stage", ins, j, st)
             assert rel == 4096 * t, ("load to another pointer's slots", ins)
-            assert last_read[st] < last_wait[st] < last_barrier, ("reload before the reads ended", ins)
-            d = stage_data[st]
-            if d[0] != j:
-                assert d[1] == 0 and d[0] == j - STAGES
-                stage_data[st] = d = [j, 0, None]
-            d[1] += 1
-            loaded.setdefault(j, []).append(t)
-            vmq.append((st, j))
+            item = []
+            for i in range(kst):
+                j, st = j0 + i, buf * kst + i
+                assert j < nsteps and st == stage_of(j), ("load of the wrong step or stage", ins, j, st)
+                assert last_read[st] < last_wait[st] < last_barrier, ("reload before the reads ended", ins)
+                d = stage_data[st]
+                if d[0] != j:
+                    assert d[1] == 0 and d[0] == j - STAGES
+                    stage_data[st] = d = [j, 0, None]
+                d[1] += 1
+                loaded.setdefault(j, []).append(t)
+                item.append((st, j))
+            vmq.append(item)
             m0 = None
         elif m := re.match(r"v_lshl_add_u64 %(\d+), %(\d+), 0, %(\d+)$", ins):
             p = int(m[1])
             assert int(m[2]) == p and int(m[3]) == kd.stride0 + (p - kd.ptr0), ("wrong stride", ins)
             assert loaded.get(ptr_step[p], []).count(p - kd.ptr0) == 1, ("advance before the load", ins)
-            ptr_step[p] += 1
+            ptr_step[p] += kst
         elif ins.startswith("s_nop") or ins.startswith("s_mov_b32"):
             pass
         else:
@@ -386,6 +445,9 @@ def header_text():
                   f"{len(out)} instructions",
                   f"#define FX_{n}_STAGE {kd.stage}",
                   f"#define FX_{n}_STAGES {STAGES}",
+                  f"#define FX_{n}_BUFS {kd.bufs}",
+                  f"#define FX_{n}_KSTEPS {kd.ksteps}",
+                  f"#define FX_{n}_ROW {kd.row_stride}",
                   f"#define FX_{n}_LOADS {kd.loads}",
                   f"#define FX_{n}_N_OFF {kd.n_off}",
                   f"#define FX_{n}_M_INS {kd.region[0][2]}",
@@ -403,7 +465,7 @@ STEP_COUNTS = (4, 5, 6, 7, 8, 9, 24, 72, 73, 74, 75, 96)
 def main(argv):
     for kd in KINDS:
         for n in STEP_COUNTS:
-            check(kd, n)
+            check(kd, loop_steps(kd, n))
     text = header_text()
     if "--check" in argv:
         with open(OUT) as f:

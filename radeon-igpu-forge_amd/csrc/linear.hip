@@ -358,14 +358,17 @@ __global__ void __launch_bounds__(kFThreads, 1) gemm_bias_act_kernel(GemmArgs a)
 // M = 16384, one per CU, where 256 x 256 tiles would leave a quarter of the CUs idle).
 __device__ __forceinline__ void raw_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-constexpr int kAsmStages = FX_FWD_NJ4_STAGES;  // LDS stages of every generated loop
+constexpr int kAsmStages = FX_FWD_NJ4_STAGES;  // K-step stages of every generated loop
 static_assert(kAsmStages == FX_WGRAD_STAGES && kAsmStages == FX_DGRAD_NJ4_STAGES, "one stage count");
 
-// One operand tile of a whole-tile kernel as its loads see it.  base: the tile's element
-// (0, 0) at K step 0.  Row operand (K along the rows, `rows` tile rows): LDS rows of 5 16-byte
-// slots, the 5th (padding) loading the row's 4th chunk again.  Col operand (K down the rows,
-// `cols` tile columns): LDS rows of cols / 8 + 4 slots, the last 4 (padding) loading the row's
-// first chunks again.  step: bytes from one K step of 32 to the next.
+// One operand tile of a whole-tile kernel as its loads see it.  The stages live in LDS
+// buffers of ks K steps of 32 (ks = 2 for the loops with a row operand, 1 for the weight
+// gradient's).  base: the tile's element (0, 0) at the buffer's first K step.  Row operand
+// (K along the rows, `rows` tile rows): LDS rows of 4 ks + 1 16-byte slots, the ks steps'
+// 64-byte segments side by side (with ks = 2 one 128-byte run of the row, a whole cache
+// line) and a padding slot loading the last chunk again.  Col operand (K down the rows,
+// `cols` tile columns): 32 ks LDS rows of cols / 8 + 4 slots, the last 4 (padding) loading
+// the row's first chunks again.  step: bytes from one buffer's K steps to the next's.
 struct TileSrc {
     const uint16_t* base;
     int64_t ld;
@@ -374,12 +377,14 @@ struct TileSrc {
     uint64_t step;
     int rmax = 1 << 30;  // row operand: tile rows past this one load this row (a ragged last tile)
     int cmax = 1 << 30;  // col operand: 8-column chunks past this one load this chunk (a ragged last tile)
+    int ks = 1;          // K steps per buffer
 };
 
 __device__ __forceinline__ const uint16_t* slot_addr(const TileSrc& t, int s) {
     if (!t.col) {
-        const int r = s / 5;
-        return t.base + (int64_t)min(r, t.rmax) * t.ld + 8 * min(s - 5 * r, 3);
+        const int spr = 4 * t.ks + 1;
+        const int r = s / spr;
+        return t.base + (int64_t)min(r, t.rmax) * t.ld + 8 * min(s - spr * r, 4 * t.ks - 1);
     }
     const int spr = t.cols / 8 + 4;
     const int r = s / spr;
@@ -388,41 +393,77 @@ __device__ __forceinline__ const uint16_t* slot_addr(const TileSrc& t, int s) {
     return t.base + (int64_t)r * t.ld + 8 * min(c, t.cmax);
 }
 
-// Load pointers, their strides and the prologue: wave-instruction q = wave + 4 t of a stage
+// whether slot s of a buffer holds the buffer's first K step (a row's first 4 chunks, or the
+// first 32 K rows of a col operand)
+__device__ __forceinline__ bool slot_first_step(const TileSrc& t, int s) {
+    if (!t.col) {
+        const int spr = 4 * t.ks + 1;
+        return s - spr * (s / spr) < 4;
+    }
+    return s / (t.cols / 8 + 4) < 32;
+}
+
+// K steps a loop of KS-step buffers runs for K: an odd count of steps of two-step buffers
+// gets a leading step of zeros (the "lead", which adds exact zeros to the accumulators).
+template <int KS>
+__device__ __forceinline__ int asm_gemm_steps(int K, bool& lead) {
+    const int n = K / 32;
+    lead = KS == 2 && (n & 1);
+    return n + (lead ? 1 : 0);
+}
+
+// Load pointers, their strides and the prologue: wave-instruction q = wave + 4 t of a buffer
 // covers 64 slots of the M-side tile (q < MI), the N-side tile (q < MI + NI) or a pad after
 // them that is never read (loading the N tile's first slot); its LDS slots start at q KiB.
-// Steps 0..3 go to stages phase + 0..3 (mod 4); the pointers are left at step 4.
-template <int L, int MI, int NI>
+// Steps 0..3 go to stages phase + 0..3 (mod 4), the buffers of KS steps each; the pointers
+// are left at step 4.  With the lead, the pointers start one step before K = 0 and the first
+// buffer's lead-step slots load the zero line.
+template <int L, int MI, int NI, int KS>
 __device__ __forceinline__ void asm_gemm_prologue(const TileSrc& ms, const TileSrc& ns, int wave, int lane, int phase,
-                                                  uint32_t base, int stage_bytes, uint64_t (&P)[L],
+                                                  bool lead, uint32_t base, int buf_bytes, uint64_t (&P)[L],
                                                   uint64_t (&S)[L]) {
     static_assert(MI + NI <= 4 * L && MI + NI > 4 * (L - 1), "load count");
+    constexpr int kBufs = kAsmStages / KS;
+    bool zero[L];
 #pragma unroll
     for (int t = 0; t < L; ++t) {
         const int q = wave + 4 * t;
         const TileSrc& src = q < MI ? ms : ns;
         const int s = q < MI ? q * 64 + lane : q < MI + NI ? (q - MI) * 64 + lane : 0;
-        P[t] = (uint64_t)(uintptr_t)slot_addr(src, s);
+        // one K step back: 32 elements along a row, 32 rows down a column
+        const int64_t back = lead ? (src.col ? 32 * src.ld : 32) : 0;
+        P[t] = (uint64_t)(uintptr_t)slot_addr(src, s) - (uint64_t)(back * 2);
         S[t] = src.step;
+        zero[t] = lead && slot_first_step(src, s);
     }
 #pragma unroll
-    for (int j = 0; j < kAsmStages; ++j) {
-        const int st = (j + phase) % kAsmStages;
+    for (int g = 0; g < kBufs; ++g) {
+        const int buf = ((g * KS + phase) % kAsmStages) / KS;
 #pragma unroll
-        for (int t = 0; t < L; ++t)
-            dma16((const void*)(uintptr_t)(P[t] + j * S[t]), base + st * stage_bytes + (wave + 4 * t) * 1024);
+        for (int t = 0; t < L; ++t) {
+            const void* src = g == 0 && zero[t] ? (const void*)g_zero_line : (const void*)(uintptr_t)(P[t] + g * S[t]);
+            dma16(src, base + buf * buf_bytes + (wave + 4 * t) * 1024);
+        }
     }
 #pragma unroll
-    for (int t = 0; t < L; ++t) P[t] += kAsmStages * S[t];
+    for (int t = 0; t < L; ++t) P[t] += kBufs * S[t];
 }
 
-// Per-lane LDS read address of a wave's operand blocks in stage 0 (the stages follow at
-// stage_bytes).  Row side: row w0 + l%32, 16 bytes per l/32.  Col side (row_bytes per K row):
+// LDS address of stage s (K step s mod 4 of the loop) in buffers of KS steps: the buffer, then
+// `sub` bytes per step inside it (a row operand's 64-byte segment, a col operand's 32 rows)
+template <int KS>
+__device__ __forceinline__ uint32_t stage_addr(uint32_t base, int s, int buf_bytes, int sub) {
+    return base + (s / KS) * buf_bytes + (s % KS) * sub;
+}
+
+// Per-lane LDS read address of a wave's operand blocks relative to a stage's base
+// (stage_addr).  Row side (row_bytes per LDS row): row w0 + l%32, 16 bytes per l/32.  Col
+// side (row_bytes per K row):
 // the transposed reads' lane pattern, K rows 8 (g'/2) + l%16 / 4 (natural order: the second
 // read 4 rows on) or 4 (g'/2) + l%16 / 4 (lds_op_t's order: 8 rows on), columns
 // w0 + 16 (g' % 2) + 4 (l % 4), g' = l / 16.
 __device__ __forceinline__ uint32_t read_addr(bool col, bool natural, int row_bytes, int w0, int lane) {
-    if (!col) return (w0 + (lane & 31)) * 80 + 16 * (lane >> 5);
+    if (!col) return (w0 + (lane & 31)) * row_bytes + 16 * (lane >> 5);
     const int grp = lane >> 4, s16 = lane & 15;
     const int k = (natural ? 8 : 4) * (grp >> 1) + (s16 >> 2);
     return k * row_bytes + (w0 + 16 * (grp & 1) + 4 * (s16 & 3)) * 2;
@@ -474,10 +515,14 @@ __device__ __forceinline__ void ct_store_block(uint16_t* stg, int lane, int i, u
 
 template <int NJ>
 struct FastGemm {
-    static constexpr int kStage = NJ == 4 ? FX_FWD_NJ4_STAGE : FX_FWD_NJ3_STAGE;
+    static constexpr int kStage = NJ == 4 ? FX_FWD_NJ4_STAGE : FX_FWD_NJ3_STAGE;  // bytes of one LDS buffer
+    static constexpr int kBufs = NJ == 4 ? FX_FWD_NJ4_BUFS : FX_FWD_NJ3_BUFS;
+    static constexpr int kKs = NJ == 4 ? FX_FWD_NJ4_KSTEPS : FX_FWD_NJ3_KSTEPS;
+    static constexpr int kRowB = NJ == 4 ? FX_FWD_NJ4_ROW : FX_FWD_NJ3_ROW;      // LDS bytes per operand row
+    static constexpr int kLds = kBufs * kStage;
     static constexpr int kLoads = NJ == 4 ? FX_FWD_NJ4_LOADS : FX_FWD_NJ3_LOADS;
     static constexpr int kTN = 64 * NJ;
-    static constexpr int kWaveLds = kAsmStages * kStage / 4;
+    static constexpr int kWaveLds = kLds / 4;
     static_assert(32 * (32 * NJ + kStgExtra) * 2 <= kWaveLds && kWaveLds % 16 == 0, "staging fits a wave's share");
 };
 
@@ -493,21 +538,26 @@ __device__ __forceinline__ void fast_tile_product(const uint16_t* A, int64_t lda
     const int wm = (wave >> 1) * 128, wn = (wave & 1) * 32 * NJ;
     const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(lds));
     uint32_t phase, iters;
-    asm_gemm_schedule(K / 32, phase, iters);
-    TileSrc ms{A + (int64_t)m0 * lda, lda, false, 0, 64};
+    bool lead;
+    asm_gemm_schedule(asm_gemm_steps<G::kKs>(K, lead), phase, iters);
+    TileSrc ms{A + (int64_t)m0 * lda, lda, false, 0, 64 * G::kKs};
     ms.rmax = rmax;
-    const TileSrc ns{B + (int64_t)n0 * ldb, ldb, false, 0, 64};
+    ms.ks = G::kKs;
+    TileSrc ns{B + (int64_t)n0 * ldb, ldb, false, 0, 64 * G::kKs};
+    ns.ks = G::kKs;
     uint64_t P[L], S[L];
     if constexpr (NJ == 4)
-        asm_gemm_prologue<L, FX_FWD_NJ4_M_INS, FX_FWD_NJ4_N_INS>(ms, ns, wave, lane, phase, base, G::kStage, P, S);
+        asm_gemm_prologue<L, FX_FWD_NJ4_M_INS, FX_FWD_NJ4_N_INS, G::kKs>(ms, ns, wave, lane, phase, lead, base,
+                                                                        G::kStage, P, S);
     else
-        asm_gemm_prologue<L, FX_FWD_NJ3_M_INS, FX_FWD_NJ3_N_INS>(ms, ns, wave, lane, phase, base, G::kStage, P, S);
+        asm_gemm_prologue<L, FX_FWD_NJ3_M_INS, FX_FWD_NJ3_N_INS, G::kKs>(ms, ns, wave, lane, phase, lead, base,
+                                                                        G::kStage, P, S);
     constexpr int kNOff = NJ == 4 ? FX_FWD_NJ4_N_OFF : FX_FWD_NJ3_N_OFF;
     uint32_t vM[kAsmStages], vN[kAsmStages];
 #pragma unroll
     for (int s = 0; s < kAsmStages; ++s) {
-        vM[s] = base + s * G::kStage + read_addr(false, true, 0, wm, lane);
-        vN[s] = base + s * G::kStage + kNOff + read_addr(false, true, 0, wn, lane);
+        vM[s] = stage_addr<G::kKs>(base, s, G::kStage, 64) + read_addr(false, true, G::kRowB, wm, lane);
+        vN[s] = stage_addr<G::kKs>(base, s, G::kStage, 64) + kNOff + read_addr(false, true, G::kRowB, wn, lane);
     }
     const uint32_t sbase = base + wave * 1024;
     uint32_t m0save;
@@ -527,7 +577,7 @@ template <int NJ, int EPI>
 __global__ void __launch_bounds__(256, 1) gemm_fast_kernel(GemmArgs a) {
     using G = FastGemm<NJ>;
     constexpr bool kGelu = EPI & 1, kH = EPI & 2, kBias = EPI & 4;
-    __shared__ __attribute__((aligned(16))) unsigned char lds[kAsmStages * G::kStage];
+    __shared__ __attribute__((aligned(16))) unsigned char lds[G::kLds];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 5;
@@ -643,7 +693,7 @@ __device__ __forceinline__ int lce_target_slot(int64_t t, int64_t c0, int g) {
 template <int NJ>
 __global__ void __launch_bounds__(256, 1) lce_stats_kernel(LceArgs a) {
     using G = FastGemm<NJ>;
-    __shared__ __attribute__((aligned(16))) unsigned char lds[kAsmStages * G::kStage];
+    __shared__ __attribute__((aligned(16))) unsigned char lds[G::kLds];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 5, ln = lane & 31;
@@ -739,7 +789,7 @@ __global__ void __launch_bounds__(256) lce_combine_kernel(LceArgs a, int ntiles,
 template <int NJ>
 __global__ void __launch_bounds__(256, 1) lce_grad_kernel(LceArgs a) {
     using G = FastGemm<NJ>;
-    __shared__ __attribute__((aligned(16))) unsigned char lds[kAsmStages * G::kStage];
+    __shared__ __attribute__((aligned(16))) unsigned char lds[G::kLds];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 5, ln = lane & 31;
@@ -795,12 +845,16 @@ struct DgradArgs {
 
 template <int NJ>
 struct DgradGemm {
-    static constexpr int kStage = NJ == 4 ? FX_DGRAD_NJ4_STAGE : FX_DGRAD_NJ3_STAGE;
+    static constexpr int kStage = NJ == 4 ? FX_DGRAD_NJ4_STAGE : FX_DGRAD_NJ3_STAGE;  // bytes of one LDS buffer
+    static constexpr int kBufs = NJ == 4 ? FX_DGRAD_NJ4_BUFS : FX_DGRAD_NJ3_BUFS;
+    static constexpr int kKs = NJ == 4 ? FX_DGRAD_NJ4_KSTEPS : FX_DGRAD_NJ3_KSTEPS;
+    static constexpr int kRowB = NJ == 4 ? FX_DGRAD_NJ4_ROW : FX_DGRAD_NJ3_ROW;  // LDS bytes per dY row
+    static constexpr int kLds = kBufs * kStage;
     static constexpr int kLoads = NJ == 4 ? FX_DGRAD_NJ4_LOADS : FX_DGRAD_NJ3_LOADS;
     static constexpr int kNOff = NJ == 4 ? FX_DGRAD_NJ4_N_OFF : FX_DGRAD_NJ3_N_OFF;
     static constexpr int kRow = (64 * NJ + 32) * 2;  // LDS bytes per K row of the W tile
     static constexpr int kTN = 64 * NJ;
-    static constexpr int kWaveLds = kAsmStages * kStage / 4;
+    static constexpr int kWaveLds = kLds / 4;
     static_assert(32 * (32 * NJ + kStgExtra) * 2 <= kWaveLds && kWaveLds % 16 == 0, "staging fits a wave's share");
 };
 
@@ -808,7 +862,7 @@ template <int NJ, int EPI>
 __global__ void __launch_bounds__(256, 1) gemm_dgrad_fast_kernel(DgradArgs a) {
     using G = DgradGemm<NJ>;
     constexpr int L = G::kLoads;
-    __shared__ __attribute__((aligned(16))) unsigned char lds[kAsmStages * G::kStage];
+    __shared__ __attribute__((aligned(16))) unsigned char lds[G::kLds];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 5;
@@ -818,19 +872,25 @@ __global__ void __launch_bounds__(256, 1) gemm_dgrad_fast_kernel(DgradArgs a) {
     n0 = nt * G::kTN;
     const uint32_t base = __builtin_amdgcn_readfirstlane(lds_addr(lds));
     uint32_t phase, iters;
-    asm_gemm_schedule(a.K / 32, phase, iters);
-    const TileSrc ms{a.dY + (int64_t)m0 * a.ldy, a.ldy, false, 0, 64};
-    const TileSrc ns{a.W + n0, a.ldw, true, G::kTN, (uint64_t)a.ldw * 64};
+    bool lead;
+    asm_gemm_schedule(asm_gemm_steps<G::kKs>(a.K, lead), phase, iters);
+    TileSrc ms{a.dY + (int64_t)m0 * a.ldy, a.ldy, false, 0, 64 * G::kKs};
+    ms.ks = G::kKs;
+    TileSrc ns{a.W + n0, a.ldw, true, G::kTN, (uint64_t)a.ldw * 64 * G::kKs};
+    ns.ks = G::kKs;
     uint64_t P[L], S[L];
     if constexpr (NJ == 4)
-        asm_gemm_prologue<L, FX_DGRAD_NJ4_M_INS, FX_DGRAD_NJ4_N_INS>(ms, ns, wave, lane, phase, base, G::kStage, P, S);
+        asm_gemm_prologue<L, FX_DGRAD_NJ4_M_INS, FX_DGRAD_NJ4_N_INS, G::kKs>(ms, ns, wave, lane, phase, lead, base,
+                                                                            G::kStage, P, S);
     else
-        asm_gemm_prologue<L, FX_DGRAD_NJ3_M_INS, FX_DGRAD_NJ3_N_INS>(ms, ns, wave, lane, phase, base, G::kStage, P, S);
+        asm_gemm_prologue<L, FX_DGRAD_NJ3_M_INS, FX_DGRAD_NJ3_N_INS, G::kKs>(ms, ns, wave, lane, phase, lead, base,
+                                                                            G::kStage, P, S);
     uint32_t vM[kAsmStages], vN[kAsmStages];
 #pragma unroll
     for (int s = 0; s < kAsmStages; ++s) {
-        vM[s] = base + s * G::kStage + read_addr(false, true, 0, wm, lane);
-        vN[s] = base + s * G::kStage + G::kNOff + read_addr(true, true, G::kRow, wn, lane);
+        vM[s] = stage_addr<G::kKs>(base, s, G::kStage, 64) + read_addr(false, true, G::kRowB, wm, lane);
+        vN[s] = stage_addr<G::kKs>(base, s, G::kStage, 32 * G::kRow) + G::kNOff +
+                read_addr(true, true, G::kRow, wn, lane);
     }
     const uint32_t sbase = base + wave * 1024;
     uint32_t m0save;
@@ -1067,13 +1127,15 @@ struct WgradGemm {
     static constexpr int kNOff = NJ == 4 ? FX_WGRAD_N_OFF : FX_WGRAD_NJ3_N_OFF;
     static constexpr int kRowM = (256 + 32) * 2, kRowN = (64 * NJ + 32) * 2;  // LDS bytes per token row
     static_assert(kNOff == 32 * kRowM, "stage layout");
+    static_assert((NJ == 4 ? FX_WGRAD_KSTEPS : FX_WGRAD_NJ3_KSTEPS) == 1, "one K step per buffer");
+    static constexpr int kLds = kAsmStages * kStage;
 };
 
 template <int NJ>
 __global__ void __launch_bounds__(256, 1) gemm_wgrad_fast_kernel(WgradArgs a) {
     using G = WgradGemm<NJ>;
     constexpr int L = G::kLoads;
-    __shared__ __attribute__((aligned(16))) unsigned char lds[kAsmStages * G::kStage];
+    __shared__ __attribute__((aligned(16))) unsigned char lds[G::kLds];
     const int nn = a.N / (64 * NJ);
     const int ntiles = ((a.M + 255) / 256) * nn;  // the last row panel may be partial (M % 256 != 0)
     const int item = wgrad_item(blockIdx.x, ntiles * a.slices);
@@ -1093,9 +1155,10 @@ __global__ void __launch_bounds__(256, 1) gemm_wgrad_fast_kernel(WgradArgs a) {
     const TileSrc ns{a.B + (int64_t)t0 * a.ldb + n0, a.ldb, true, 64 * NJ, (uint64_t)a.ldb * 64};
     uint64_t P[L], S[L];
     if constexpr (NJ == 4)
-        asm_gemm_prologue<L, FX_WGRAD_M_INS, FX_WGRAD_N_INS>(ms, ns, wave, lane, phase, base, G::kStage, P, S);
+        asm_gemm_prologue<L, FX_WGRAD_M_INS, FX_WGRAD_N_INS, 1>(ms, ns, wave, lane, phase, false, base, G::kStage, P, S);
     else
-        asm_gemm_prologue<L, FX_WGRAD_NJ3_M_INS, FX_WGRAD_NJ3_N_INS>(ms, ns, wave, lane, phase, base, G::kStage, P, S);
+        asm_gemm_prologue<L, FX_WGRAD_NJ3_M_INS, FX_WGRAD_NJ3_N_INS, 1>(ms, ns, wave, lane, phase, false, base,
+                                                                       G::kStage, P, S);
     uint32_t vM[kAsmStages], vN[kAsmStages];
 #pragma unroll
     for (int s = 0; s < kAsmStages; ++s) {

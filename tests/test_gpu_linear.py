@@ -348,9 +348,9 @@ def _linear_fwd(x, W, b, act, want_h):
     (768, 768, 2304, 0, True, False, 0),   # qkv widths
     (256, 3072, 768, 1, False, True, 0),   # fc2 depth
     (16384, 768, 3072, 1, False, True, 0), # the cfg5 MLP fc (256-wide tiles): GELU and the pre-activation
-    (512, 160, 256, 1, True, True, 0),     # 5 K steps: enters the loop body at its fourth step
-    (512, 192, 192, 0, False, False, 8),   # 6 K steps: enters at the third
-    (512, 224, 256, 0, True, False, 0),    # 7 K steps: enters at the second
+    (512, 160, 256, 1, True, True, 0),     # 5 K steps: a leading zero step makes 6 (entry at the body's third)
+    (512, 192, 192, 0, False, False, 8),   # 6 K steps: enters the loop body at its third step
+    (512, 224, 256, 0, True, False, 0),    # 7 K steps: 8 with the zero step (the body from its first)
 ])
 def test_whole_tile_kernel_matches_general_kernel(dev, M, K, N, act, bias, want_h, pad_k):
     g = torch.Generator(device=dev).manual_seed(M + K + N)
@@ -429,8 +429,8 @@ def _dgrad(dy, W, h=None):
 
 @pytest.mark.parametrize("M,N,K,pad", [
     (256, 256, 128, 0),      # 256-wide tiles, the loop's tail only
-    (512, 192, 160, 0),      # 192-wide tiles, 5 K steps (entry at the body's fourth step)
-    (256, 768, 224, 8),      # 7 K steps; rows of dY strided
+    (512, 192, 160, 0),      # 192-wide tiles, 5 K steps (with the leading zero step, 6)
+    (256, 768, 224, 8),      # 7 K steps (8 with the zero step); rows of dY strided
     (1024, 3072, 768, 0),    # fc2's input gradient shape (192-wide tiles at this M)
     (16384, 3072, 768, 0),   # cfg5 fc2 (256-wide tiles, 768 tiles)
     (16384, 768, 2304, 0),   # cfg5 qkv
