@@ -73,25 +73,26 @@ FEW_ROWS = 64
 
 def whole_tiles(M, N, K):
     """Shapes that fx_linear_fwd runs on its whole-tile kernel (M % 256 == 0, N % 192 or
-    % 256 == 0, K % 32 == 0, K >= 128) and where that kernel measured faster than the library
-    GEMM in isolation: K up to 1024 (the cfg5 qkv and proj, 64 and 22.6 us against 66 and
-    25.3 us).  With K = 3072 and N = 768 (fc2: one tile per CU) the library GEMM is faster
-    (61.7 against 69.8 us).  Taken only with NATIVE_PROJ_FWD."""
+    % 256 == 0, K % 32 == 0, K >= 128) and where that kernel measured at least as fast as the
+    library GEMM: K up to 1024 (the cfg5 qkv and proj, 62.9 and 22.8 us against 66.8 and
+    24.2 us with the operands in the caches, 76.7 and 31.2 against 75.2 and 29.7 us from
+    HBM).  With K = 3072 and N = 768 (fc2: one tile per CU) the library GEMM is faster from
+    HBM (81.0 against 95.7 us).  Taken only with NATIVE_PROJ_FWD."""
     return M % 256 == 0 and K % 32 == 0 and 128 <= K <= 1024 and (N % 256 == 0 or N % 192 == 0)
 
 
-# Routing switches, set by measurements inside the cfg5 training step.  In isolation, with
-# the operands left in the caches by the previous call, the whole-tile kernels match the
-# library GEMM at these shapes; inside the step, where the operands come from HBM, they
-# lose: a kernel trace of the step with every switch on had the qkv / proj / fc input
-# gradients at 57.4 against 52.6 us per product, fc2's with the GELU derivative at 140.7
-# against 86.9 + 45.2 us, and the qkv / proj forwards at 50.5 against 46.7 us, 0.42 ms
-# more kernel time per step; interleaved A/Bs of the whole step put the switches within
-# noise of the library routes.  So they are off.
+# Routing switches, set by interleaved A/Bs of the whole cfg5 training step (24 rounds of 5
+# steps, medians, one process).  With the two-step LDS buffers of the whole-tile kernels
+# (whole 128-byte lines from HBM), the qkv and proj forwards (whole_tiles()) on fx_linear_fwd
+# measured +0.011 ms per step against the library GEMM, within the rounds' spread: they run
+# on this build's kernel.  The input gradients do not: the qkv one at parity (-0.003 to
+# +0.005 ms), the proj and fc ones and fc2's with the GELU derivative folded in 0.04-0.08 ms
+# slower each (cold operands from HBM, and tile epilogues that one workgroup per CU cannot
+# overlap with its MFMA work).
 # NATIVE_INPUT_GRAD: input gradients on fx_linear_dgrad where input_grad() takes them;
 # NATIVE_PROJ_FWD: the whole_tiles() forwards on fx_linear_fwd.  False: the library GEMM.
 NATIVE_INPUT_GRAD = False
-NATIVE_PROJ_FWD = False
+NATIVE_PROJ_FWD = True
 # NATIVE_GELU_INPUT_GRAD: only the input gradient with the GELU derivative folded in (the
 # GPT MLP's fc2, where fx_linear_dgrad also saves fx_gelu_bwd's pass over three tensors)
 NATIVE_GELU_INPUT_GRAD = False
@@ -105,11 +106,12 @@ def dgrad_tiles(M, N, K):
 def input_grad(dy2, weight, h=None):
     """dx = dy2 @ weight (bf16), and with h (the pre-activation of a GELU(tanh) layer feeding
     this one) dx * gelu'(h).  With NATIVE_INPUT_GRAD, on fx_linear_dgrad for dgrad_tiles()
-    shapes where it measured at least as fast as the library GEMM in isolation (input widths
-    up to 1024 columns: the cfg5 qkv, proj and fc input gradients, 52.9 / 22.6 / 68.1 us
-    against 53.7 / 25.9 / 68.7 us), and always with h (the GELU backward folded into the
-    epilogue: 116 us against 78 + 45.7 us for the cfg5 fc2 product and fx_gelu_bwd); else
-    torch.mm, then fx_gelu_bwd for h."""
+    shapes where it measured at least as fast as the library GEMM with the operands in the
+    caches (input widths up to 1024 columns: the cfg5 qkv, proj and fc input gradients,
+    52.1 / 22.9 / 66.0 us against 60.5 / 25.4 / 67.2 us; from HBM 72.3 / 31.6 / 93.7 against
+    64.5 / 30.3 / 82.4 us), and always with h (the GELU backward folded into the epilogue:
+    122.8 us against 76.4 + 46 us for the cfg5 fc2 product and fx_gelu_bwd); else torch.mm,
+    then fx_gelu_bwd for h."""
     M, K = dy2.shape
     N = weight.shape[1]
     wanted = (NATIVE_INPUT_GRAD and (h is not None or N <= 1024)) or (NATIVE_GELU_INPUT_GRAD and h is not None)
