@@ -11,8 +11,10 @@ from tolerances import RTOL_LOSS
 pytestmark = pytest.mark.gpu
 
 # (M, D, V): ragged row counts (the last 256-row tile partly past M), V on 192- and
-# 256-column tiles, D from the smallest K the kernels take up to the GPT's
-SHAPES = [(1, 128, 768), (300, 128, 768), (512, 256, 1536), (777, 128, 1024), (256, 768, 2304), (1000, 384, 4608)]
+# 256-column tiles, D from the smallest K the kernels take up to the GPT's; D = 160 and 224
+# are odd counts of 32-wide K steps (the loop's leading step of zeros)
+SHAPES = [(1, 128, 768), (300, 128, 768), (512, 256, 1536), (777, 128, 1024), (256, 768, 2304), (1000, 384, 4608),
+          (300, 160, 768), (512, 224, 1536)]
 
 
 def _inputs(M, D, V, dev, seed):
