@@ -33,7 +33,6 @@ constexpr int kGSPR = kGBK / 8 + 1;         // 16-byte LDS slots per row (the la
 constexpr int kGNI = kGBM * kGSPR / 64;     // wave loads per 256-row tile
 constexpr int kGThreads = 1024;
 constexpr int kGWaves = kGThreads / 64;
-constexpr int kGPW = (2 * kGNI + kGWaves - 1) / kGWaves;  // wave loads per wave per stage (A and W)
 constexpr int kGWM = 64, kGWN = 64;         // wave tile: 16 waves in 4 (M) x 4 (N)
 constexpr int kGTI = kGWM / 32, kGTJ = kGWN / 32;  // 32 x 32 MFMA tiles per wave
 static_assert(kGBM == kGBN && kGBM * kGSPR % 64 == 0, "tile shape");
