@@ -52,7 +52,7 @@ def test_all_ignored_gives_zero(dev):
     lg = torch.randn(6, 64, device=dev).bfloat16().requires_grad_()
     loss = fused_cross_entropy(lg, torch.full((6,), -100, device=dev))
     loss.backward()
-    assert float(loss) == 0.0 and float(lg.grad.abs().max()) == 0.0
+    assert loss.item() == 0.0 and lg.grad.abs().max().item() == 0.0
 
 
 def test_backward_scales_by_incoming_grad(dev):
