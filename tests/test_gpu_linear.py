@@ -351,6 +351,7 @@ def _linear_fwd(x, W, b, act, want_h):
     (512, 160, 256, 1, True, True, 0),     # 5 K steps: a leading zero step makes 6 (entry at the body's third)
     (512, 192, 192, 0, False, False, 8),   # 6 K steps: enters the loop body at its third step
     (512, 224, 256, 0, True, False, 0),    # 7 K steps: 8 with the zero step (the body from its first)
+    (256, 288, 192, 1, False, True, 0),    # 9 K steps: 10 with the zero step
 ])
 def test_whole_tile_kernel_matches_general_kernel(dev, M, K, N, act, bias, want_h, pad_k):
     g = torch.Generator(device=dev).manual_seed(M + K + N)
@@ -431,6 +432,9 @@ def _dgrad(dy, W, h=None):
     (256, 256, 128, 0),      # 256-wide tiles, the loop's tail only
     (512, 192, 160, 0),      # 192-wide tiles, 5 K steps (with the leading zero step, 6)
     (256, 768, 224, 8),      # 7 K steps (8 with the zero step); rows of dY strided
+    (256, 256, 192, 0),      # 6 K steps: enters the loop body at its third step
+    (512, 192, 256, 8),      # 8 K steps: the body from its first
+    (256, 768, 288, 0),      # 9 K steps (10 with the zero step)
     (1024, 3072, 768, 0),    # fc2's input gradient shape (192-wide tiles at this M)
     (16384, 3072, 768, 0),   # cfg5 fc2 (256-wide tiles, 768 tiles)
     (16384, 768, 2304, 0),   # cfg5 qkv
