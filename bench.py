@@ -393,8 +393,15 @@ def bench_linear(torch):
     with torch.no_grad():
         t = time_us(torch, lambda: fused_linear(x, W, None, "gelu_tanh"))
         t_ref = time_us(torch, lambda: torch.nn.functional.gelu(x @ W.t(), approximate="tanh"))
+    # the training step's form: the GELU output and, in place of the pre-activation, its
+    # derivative (fx_linear_fwd act 2, fused_mlp's fc)
+    from fxgpu.abi import call, ptr, stream_of
+    y = torch.empty(M, N, device="cuda", dtype=torch.bfloat16)
+    gd = torch.empty_like(y)
+    t_d = time_us(torch, lambda: call("fx_linear_fwd", ptr(x), K, None, 0, 0, ptr(W), None, ptr(y), ptr(gd), None,
+                                      M, N, K, 2, stream_of(x)))
     f = 2.0 * M * K * N
-    del W
+    del W, y, gd
     # the block's projections (y = x W^T): this build's routing (linear) against torch.mm
     from fxgpu.fused_linear import linear
     proj = {}
@@ -409,7 +416,7 @@ def bench_linear(torch):
         del xp, wp
     return {"shape": [M, K, N], "fwd_us": round(t, 2), "tflops": round(f / t / 1e6, 1),
             "frac_of_bf16_peak": round(f / t / 1e6 / BF16_PEAK_TFLOPS, 4),
-            "hipblaslt_mm_plus_gelu_us": round(t_ref, 2), "projections": proj}
+            "hipblaslt_mm_plus_gelu_us": round(t_ref, 2), "with_derivative_us": round(t_d, 2), "projections": proj}
 
 
 def bench_wgrad(torch):

@@ -25,7 +25,7 @@ extern "C" {
 #endif
 
 #define FX_EINVAL (-1)
-#define FX_ABI_VERSION 4
+#define FX_ABI_VERSION 5
 
 /* ---- library ------------------------------------------------------------ */
 
@@ -303,8 +303,11 @@ int fx_attn_decode(const fxAttnDecodeArgs* args, void* stream);
 /* Y = act(A W^T + bias), A (M, K): dense rows (A row m = X + m*ldx) when idx is NULL,
  * otherwise gathered windows A[m, w*F + f] = X[idx[m] + w, f] of X (R, F) (K = W*F,
  * F % 8 == 0; a window outside X reads as zeros).  W (N, K) bf16 contiguous, bias (N,)
- * or NULL, Y (M, N).  act: 0 identity, 1 GELU (tanh approximation).  H (M, N), when
- * not NULL, receives the pre-activation; Xg (M, K), when not NULL, the gathered A.
+ * or NULL, Y (M, N).  act: 0 identity, 1 GELU (tanh approximation), 2 GELU with H
+ * receiving its derivative.  H (M, N), when not NULL, receives the pre-activation h
+ * (act 0 and 1) or gelu_tanh'(h) (act 2: computed from the same exponential as the GELU,
+ * for the backward's fx_linear_dgrad_gate / fx_gelu_bwd_gate); Xg (M, K), when not NULL,
+ * the gathered A.
  * bf16 MFMA, fp32 accumulation.  K % 8 == 0.
  * Replaces FusedGatherLinear.forward + gather_gemm (ml/fxgpu/fused_linear.py:35-88,
  * ml/fxgpu/gather_gemm.hip:16-180) and the fc -> gelu_tanh of the GPT MLP
@@ -345,6 +348,12 @@ int fx_linear_fwd_ex(const fxLinearArgs* args, void* stream);
  * The activation half of the fused linear's backward (the reference's torch autograd
  * of F.gelu(approximate="tanh"), ml/fxlm/model.py:71). */
 int fx_gelu_bwd(const uint16_t* dy, const uint16_t* h, uint16_t* dh, int64_t n, void* stream);
+
+/* dh = dy * g, elementwise over n bf16 values (16-byte aligned buffers), g = gelu_tanh'(h)
+ * as fx_linear_fwd with act 2 stores it.  The same backward as fx_gelu_bwd (the reference's
+ * autograd of F.gelu(approximate="tanh"), ml/fxlm/model.py:71) with the derivative taken
+ * in the forward, from the fp32 pre-activation, and saved in place of it. */
+int fx_gelu_bwd_gate(const uint16_t* dy, const uint16_t* g, uint16_t* dh, int64_t n, void* stream);
 
 /* Bytes of workspace fx_embedding_bwd needs for n positions, a V-row table and rows of D
  * values (0 when n, V or D is not positive). */
@@ -389,6 +398,15 @@ int fx_linear_wgrad(const uint16_t* dY, int64_t ldy, const uint16_t* X, int64_t 
  * (ml/fxlm/model.py:71). */
 int fx_linear_dgrad(const uint16_t* dY, int64_t ldy, const uint16_t* W, int64_t ldw, const uint16_t* H,
                     uint16_t* dX, int64_t ldx, int64_t M, int64_t N, int64_t K, void* stream);
+
+/* fx_linear_dgrad with G (M, N) the GELU derivative at this product's output columns, as
+ * fx_linear_fwd with act 2 stores it: dX = bf16(bf16(dY W) G), bit for bit fx_linear_dgrad
+ * without H followed by fx_gelu_bwd_gate; the epilogue multiplies instead of evaluating the
+ * derivative.  Same shapes, strides and alignment as fx_linear_dgrad; G row stride ldx.
+ * Replaces the GPT MLP's fc2 input gradient and the F.gelu backward after it
+ * (ml/fxlm/model.py:71, torch autograd of nn.Linear and F.gelu(approximate="tanh")). */
+int fx_linear_dgrad_gate(const uint16_t* dY, int64_t ldy, const uint16_t* W, int64_t ldw, const uint16_t* G,
+                         uint16_t* dX, int64_t ldx, int64_t M, int64_t N, int64_t K, void* stream);
 
 /* ---- fused linear cross-entropy ------------------------------------------- */
 

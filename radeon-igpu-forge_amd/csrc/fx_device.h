@@ -127,6 +127,21 @@ __device__ __forceinline__ float gelu_tanh(float h) {
     return h * __builtin_amdgcn_rcpf(e + 1.f);
 }
 
+// GELU and its derivative from the one v_exp_f32 and v_rcp_f32 of gelu_tanh: with
+// s = 1 / (1 + e) = sigmoid(2u), GELU = h s (c here is gelu_tanh(h) bit for bit) and
+// d/dh (h s) = s + h s (1 - s) 2 u'(h) = s (1 + h (1 - s) (2c0 + 6 c0 0.044715 h^2)),
+// c0 = sqrt(2/pi), which equals gelu_tanh_grad's 0.5 (1 + t) + 0.5 h (1 - t^2) u' since
+// 1 + t = 2 s and 1 - t^2 = 4 s (1 - s).  Four more VALU operations than the GELU alone.
+__device__ __forceinline__ void gelu_tanh_and_grad(float h, float& c, float& d) {
+    constexpr float k0 = -2.f * 1.4426950408889634f * 0.7978845608028654f;
+    constexpr float k1 = k0 * 0.044715f;
+    constexpr float c2 = 2.f * 0.7978845608028654f, c6 = 6.f * 0.7978845608028654f * 0.044715f;
+    const float h2 = h * h;
+    const float s = __builtin_amdgcn_rcpf(exp2_fast(h * fmaf(h2, k1, k0)) + 1.f);
+    c = h * s;
+    d = s * fmaf(fmaf(-h, s, h), fmaf(h2, c6, c2), 1.f);  // explicit fmas: the same bits in every kernel
+}
+
 // d/dh of the above: 0.5 (1 + t) + 0.5 h (1 - t^2) u'(h), t = tanh(u) = 1 - 2 / (e + 1)
 __device__ __forceinline__ float gelu_tanh_grad(float h) {
     const float u = 0.7978845608028654f * fmaf(0.044715f * h, h * h, h);

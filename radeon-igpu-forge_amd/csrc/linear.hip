@@ -154,10 +154,12 @@ __device__ __forceinline__ void epi_flush(const uint16_t* tmp, uint16_t* out, in
 // stage pipeline runs on across tiles, so the next tile's first K stage loads during
 // the current tile's last MFMAs and epilogue.
 // EPI selects the epilogue at compile time (fewer live registers than runtime switches):
-// bit 0 GELU, bit 1 pre-activation H out, bit 2 bias, bit 3 residual
+// bit 0 GELU, bit 1 pre-activation H out, bit 2 bias, bit 3 residual, bit 4 (with bits 0
+// and 1) H receives the GELU derivative at the pre-activation instead
 template <int EPI>
 __global__ void __launch_bounds__(kFThreads, 1) gemm_bias_act_kernel(GemmArgs a) {
-    constexpr bool kGelu = EPI & 1, kH = EPI & 2, kBias = EPI & 4, kRes = EPI & 8;
+    constexpr bool kGelu = EPI & 1, kH = EPI & 2, kBias = EPI & 4, kRes = EPI & 8, kDeriv = EPI & 16;
+    static_assert(!kDeriv || (kGelu && kH), "the derivative goes to H, of a GELU layer");
     __shared__ __attribute__((aligned(16))) uint16_t sa[2][kGBM * kGLD];
     __shared__ __attribute__((aligned(16))) uint16_t sb[2][kGBN * kGLD];
     // the bias of the current tile's columns (0 past N), read by the epilogue at
@@ -325,6 +327,9 @@ __global__ void __launch_bounds__(kFThreads, 1) gemm_bias_act_kernel(GemmArgs a)
                             if (pass == 1) {
                                 if (kGelu) h = gelu_tanh(h);
                                 if (kRes) h += rv[e];
+                            } else if (kDeriv) {
+                                float c;
+                                gelu_tanh_and_grad(h, c, h);
                             }
                             v[e] = h;
                         }
@@ -512,6 +517,36 @@ __device__ __forceinline__ void ct_store_block(uint16_t* stg, int lane, int i, u
     }
 }
 
+// Two outputs of block i from one evaluation: value(j, q, acc4, o, o2) gives the 4 values of
+// `out` (ordinary stores) and of `out2` (non-temporal stores) at the positions ct_store_block
+// describes, staged in stg and stg2 (two disjoint 32-row staging blocks of the wave).
+template <int NJ, typename Value>
+__device__ __forceinline__ void ct_store_block2(uint16_t* stg, uint16_t* stg2, int lane, int i, uint16_t* out,
+                                                int64_t ld, uint16_t* out2, int64_t ld2, int64_t row0, int col0,
+                                                const f32x16 (&acc)[4 * NJ], Value&& value) {
+    constexpr int LDE = 32 * NJ + kStgExtra;
+    const int g = lane >> 5;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float a[4] = {acc[4 * j + i][4 * q], acc[4 * j + i][4 * q + 1], acc[4 * j + i][4 * q + 2],
+                                acc[4 * j + i][4 * q + 3]};
+            float v[4], w[4];
+            value(j, q, a, v, w);
+            const int off = (lane & 31) * LDE + 32 * j + 8 * q + 4 * g;
+            *reinterpret_cast<uint2*>(stg + off) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+            *reinterpret_cast<uint2*>(stg2 + off) = make_uint2(pack_bf16x2(w[0], w[1]), pack_bf16x2(w[2], w[3]));
+        }
+#pragma unroll
+    for (int k = 0; k < 2 * NJ; ++k) {
+        const int idx = lane + 64 * k;
+        const int r = idx / (4 * NJ), c = idx - r * (4 * NJ);
+        st16(out + (row0 + r) * ld + col0 + 8 * c, *reinterpret_cast<const uint4*>(stg + r * LDE + 8 * c));
+        st16_nt(out2 + (row0 + r) * ld2 + col0 + 8 * c, *reinterpret_cast<const uint4*>(stg2 + r * LDE + 8 * c));
+    }
+}
+
 template <int NJ>
 struct FastGemm {
     static constexpr int kStage = NJ == 4 ? FX_FWD_NJ4_STAGE : FX_FWD_NJ3_STAGE;  // bytes of one LDS buffer
@@ -522,7 +557,8 @@ struct FastGemm {
     static constexpr int kLoads = NJ == 4 ? FX_FWD_NJ4_LOADS : FX_FWD_NJ3_LOADS;
     static constexpr int kTN = 64 * NJ;
     static constexpr int kWaveLds = kLds / 4;
-    static_assert(32 * (32 * NJ + kStgExtra) * 2 <= kWaveLds && kWaveLds % 16 == 0, "staging fits a wave's share");
+    static_assert(2 * 32 * (32 * NJ + kStgExtra) * 2 <= kWaveLds && kWaveLds % 16 == 0,
+                  "two staging blocks fit a wave's share");
 };
 
 // The product of one 256 x (64 NJ) tile: acc = A[m0.., :] B[n0.., :]^T over K (A rows past
@@ -571,11 +607,13 @@ __device__ __forceinline__ void fast_tile_product(const uint16_t* A, int64_t lda
 }
 
 // Forward: C = act(X W^T + bias), with the pre-activation H.  EPI: bit 0 GELU, bit 1 H out,
-// bit 2 bias (no residual, gather or Xg)
+// bit 2 bias, bit 3 (with bits 0 and 1) H receives the GELU derivative at the pre-activation
+// instead (no residual, gather or Xg)
 template <int NJ, int EPI>
 __global__ void __launch_bounds__(256, 1) gemm_fast_kernel(GemmArgs a) {
     using G = FastGemm<NJ>;
-    constexpr bool kGelu = EPI & 1, kH = EPI & 2, kBias = EPI & 4;
+    constexpr bool kGelu = EPI & 1, kH = EPI & 2, kBias = EPI & 4, kDeriv = EPI & 8;
+    static_assert(!kDeriv || (kGelu && kH), "the derivative goes to H, of a GELU layer");
     __shared__ __attribute__((aligned(16))) unsigned char lds[G::kLds];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -601,6 +639,20 @@ __global__ void __launch_bounds__(256, 1) gemm_fast_kernel(GemmArgs a) {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
                 bias[j][q][e] = kBias ? bf16_to_f32(a.bias[n0 + wn + 32 * j + 8 * q + 4 * g + e]) : 0.f;
+    if constexpr (kDeriv) {
+        // C and H = gelu'(h) from one exponential and reciprocal per value (the two-pass
+        // form below would evaluate them twice: 24 us more per cfg5 fc product)
+        uint16_t* stg2 = stg + 32 * (32 * NJ + kStgExtra);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            ct_store_block2<NJ>(stg, stg2, lane, i, a.C, a.ldc, a.H, a.ldh, m0 + wm + 32 * i, n0 + wn, acc,
+                                [&](int j, int q, const float (&v)[4], float (&o)[4], float (&d)[4]) {
+#pragma unroll
+                                    for (int e = 0; e < 4; ++e)
+                                        gelu_tanh_and_grad(kBias ? v[e] + bias[j][q][e] : v[e], o[e], d[e]);
+                                });
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int64_t row0 = m0 + wm + 32 * i;
@@ -896,9 +948,9 @@ __global__ void __launch_bounds__(256, 1) gemm_dgrad_fast_kernel(DgradArgs a) {
     f32x16 acc[4 * NJ];
 #pragma unroll
     for (int k = 0; k < 4 * NJ; ++k) acc[k] = f32x16{};
-    // EPI 1: the pre-activation of each 32-row block, 4 columns per (j, q), loaded one block
-    // ahead (the first before the K loop: older than the loop's loads, so its waits only
-    // get stricter)
+    // EPI 1: the pre-activation of each 32-row block (EPI 2: the GELU derivative there), 4
+    // columns per (j, q), loaded one block ahead (the first before the K loop: older than
+    // the loop's loads, so its waits only get stricter)
     uint2 hb[2][NJ][4];
     auto load_h = [&](int i, uint2 (&d)[NJ][4]) {
         const uint16_t* hrow = a.H + (int64_t)(m0 + wm + 32 * i + (lane & 31)) * a.ldx + n0 + wn + 4 * g;
@@ -907,7 +959,7 @@ __global__ void __launch_bounds__(256, 1) gemm_dgrad_fast_kernel(DgradArgs a) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) d[j][q] = *reinterpret_cast<const uint2*>(hrow + 32 * j + 8 * q);
     };
-    if constexpr (EPI == 1) load_h(0, hb[0]);
+    if constexpr (EPI != 0) load_h(0, hb[0]);
     if constexpr (NJ == 4)
         asm volatile(FX_DGRAD_NJ4_KLOOP : FX_DGRAD_NJ4_OUTS : FX_DGRAD_NJ4_INS : FX_DGRAD_NJ4_CLOBBERS);
     else
@@ -919,17 +971,17 @@ __global__ void __launch_bounds__(256, 1) gemm_dgrad_fast_kernel(DgradArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int64_t row0 = m0 + wm + 32 * i;
-        if constexpr (EPI == 1)
+        if constexpr (EPI != 0)
             if (i + 1 < 4) load_h(i + 1, hb[(i + 1) & 1]);
         ct_store_block<NJ>(stg, lane, i, a.dX, a.ldx, row0, n0 + wn, acc,
                            [&](int j, int q, const float (&v)[4], float (&o)[4]) {
-                               if constexpr (EPI == 1) {
+                               if constexpr (EPI != 0) {
                                    const uint2 hh = hb[i & 1][j][q];
                                    const float h[4] = {bf16_to_f32((uint16_t)hh.x), bf16_to_f32((uint16_t)(hh.x >> 16)),
                                                        bf16_to_f32((uint16_t)hh.y), bf16_to_f32((uint16_t)(hh.y >> 16))};
 #pragma unroll
                                    for (int e = 0; e < 4; ++e)
-                                       o[e] = bf16_to_f32(f32_to_bf16(v[e])) * gelu_tanh_grad(h[e]);
+                                       o[e] = bf16_to_f32(f32_to_bf16(v[e])) * (EPI == 1 ? gelu_tanh_grad(h[e]) : h[e]);
                                } else {
 #pragma unroll
                                    for (int e = 0; e < 4; ++e) o[e] = v[e];
@@ -1399,8 +1451,15 @@ __global__ void __launch_bounds__(1024) gemm_skinny_kernel(GemmArgs a, int sw) {
         const int n = n0 + 16 * (tile / MT) + nl, m = 16 * (tile % MT) + ml;
         if (n < a.N && m < a.M) {
             const float h = sum + (a.bias ? bf16_to_f32(a.bias[n]) : 0.f);
-            if (a.H) a.H[(int64_t)m * a.ldh + n] = f32_to_bf16(h);
-            float y = a.act == 1 ? gelu_tanh(h) : h;
+            float y = h;
+            if (a.act == 2) {
+                float d;
+                gelu_tanh_and_grad(h, y, d);
+                if (a.H) a.H[(int64_t)m * a.ldh + n] = f32_to_bf16(d);
+            } else {
+                if (a.H) a.H[(int64_t)m * a.ldh + n] = f32_to_bf16(h);
+                if (a.act == 1) y = gelu_tanh(h);
+            }
             if (a.res) y += bf16_to_f32(a.res[(int64_t)m * a.ldres + n]);
             a.C[(int64_t)m * a.ldc + n] = f32_to_bf16(y);
         }
@@ -1449,6 +1508,24 @@ gelu_bwd_kernel(const uint16_t* __restrict__ dy, const uint16_t* __restrict__ h,
         dh[i] = f32_to_bf16(bf16_to_f32(dy[i]) * gelu_tanh_grad(bf16_to_f32(h[i])));
 }
 
+// dh = dy * g elementwise (g the GELU derivative the forward stored), rounded to bf16
+__global__ void __launch_bounds__(256)
+gate_mul_kernel(const uint16_t* __restrict__ dy, const uint16_t* __restrict__ g, uint16_t* __restrict__ dh,
+                int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    const int64_t n8 = n >> 3;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n8; i += stride) {
+        float fd[8], fg[8], o[8];
+        unpack8(ld16_nt(dy + i * 8), fd);
+        unpack8(ld16_nt(g + i * 8), fg);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = fd[j] * fg[j];
+        st16_nt(dh + i * 8, pack8(o));
+    }
+    for (int64_t i = n8 * 8 + (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride)
+        dh[i] = f32_to_bf16(bf16_to_f32(dy[i]) * bf16_to_f32(g[i]));
+}
+
 // the few-row kernel for M <= kSKMaxM, else the persistent tiled kernel
 static int linear_fwd(GemmArgs a, hipStream_t stream) {
     if (a.M <= kSKMaxM) return linear_skinny(a, stream);
@@ -1459,15 +1536,19 @@ static int linear_fwd(GemmArgs a, hipStream_t stream) {
     FX_REQUIRE(tiles < 0x7fffffffLL, "fx_linear_fwd: too many tiles");
     if (const int nj = fast_gemm_nj(a)) {
         const int64_t ft = (int64_t)(a.M / 256) * (a.N / (64 * nj));
-        const int fe = (a.act == 1 ? 1 : 0) | (a.H ? 2 : 0) | (a.bias ? 4 : 0);
+        const int fe = (a.act != 0 ? 1 : 0) | (a.H ? 2 : 0) | (a.bias ? 4 : 0) | (a.act == 2 && a.H ? 8 : 0);
 #define FX_FAST_EPI(J, E) \
     case E: hipLaunchKernelGGL((gemm_fast_kernel<J, E>), dim3((unsigned)ft), dim3(256), 0, stream, a); break;
         if (nj == 4) {
             switch (fe) { FX_FAST_EPI(4, 0) FX_FAST_EPI(4, 1) FX_FAST_EPI(4, 2) FX_FAST_EPI(4, 3)
-                          FX_FAST_EPI(4, 4) FX_FAST_EPI(4, 5) FX_FAST_EPI(4, 6) FX_FAST_EPI(4, 7) }
+                          FX_FAST_EPI(4, 4) FX_FAST_EPI(4, 5) FX_FAST_EPI(4, 6) FX_FAST_EPI(4, 7)
+                          FX_FAST_EPI(4, 11) FX_FAST_EPI(4, 15)
+                          default: return set_error(FX_EINVAL, "fx_linear_fwd: epilogue %d", fe); }
         } else {
             switch (fe) { FX_FAST_EPI(3, 0) FX_FAST_EPI(3, 1) FX_FAST_EPI(3, 2) FX_FAST_EPI(3, 3)
-                          FX_FAST_EPI(3, 4) FX_FAST_EPI(3, 5) FX_FAST_EPI(3, 6) FX_FAST_EPI(3, 7) }
+                          FX_FAST_EPI(3, 4) FX_FAST_EPI(3, 5) FX_FAST_EPI(3, 6) FX_FAST_EPI(3, 7)
+                          FX_FAST_EPI(3, 11) FX_FAST_EPI(3, 15)
+                          default: return set_error(FX_EINVAL, "fx_linear_fwd: epilogue %d", fe); }
         }
 #undef FX_FAST_EPI
         return check_launch("gemm_fast");
@@ -1475,13 +1556,15 @@ static int linear_fwd(GemmArgs a, hipStream_t stream) {
     // persistent grid: one workgroup per CU (the LDS of one is 147 KB)
     const int64_t cus = device_cus();
     const int64_t grid = tiles < cus ? tiles : cus;
-    const int epi = (a.act == 1 ? 1 : 0) | (a.H ? 2 : 0) | (a.bias ? 4 : 0) | (a.res ? 8 : 0);
+    const int epi = (a.act != 0 ? 1 : 0) | (a.H ? 2 : 0) | (a.bias ? 4 : 0) | (a.res ? 8 : 0) |
+                    (a.act == 2 && a.H ? 16 : 0);
 #define FX_GEMM_EPI(E) \
     case E: hipLaunchKernelGGL(gemm_bias_act_kernel<E>, dim3((unsigned)grid), dim3(kFThreads), 0, stream, a); break;
     switch (epi) {
         FX_GEMM_EPI(0) FX_GEMM_EPI(1) FX_GEMM_EPI(2) FX_GEMM_EPI(3) FX_GEMM_EPI(4) FX_GEMM_EPI(5) FX_GEMM_EPI(6)
         FX_GEMM_EPI(7) FX_GEMM_EPI(8) FX_GEMM_EPI(9) FX_GEMM_EPI(10) FX_GEMM_EPI(11) FX_GEMM_EPI(12)
-        FX_GEMM_EPI(13) FX_GEMM_EPI(14) FX_GEMM_EPI(15)
+        FX_GEMM_EPI(13) FX_GEMM_EPI(14) FX_GEMM_EPI(15) FX_GEMM_EPI(19) FX_GEMM_EPI(23)
+        default: return set_error(FX_EINVAL, "fx_linear_fwd: epilogue %d", epi);
     }
 #undef FX_GEMM_EPI
     return check_launch("gemm_bias_act");
@@ -1499,7 +1582,8 @@ extern "C" int fx_linear_fwd(const uint16_t* X, int64_t ldx, const int32_t* idx,
                (long long)N, (long long)K);
     FX_REQUIRE(K % 8 == 0, "fx_linear_fwd: K=%lld must be a multiple of 8", (long long)K);
     FX_REQUIRE(M < 0x7fffffffLL && N < 0x7fffffffLL && K < 0x7fffffffLL, "fx_linear_fwd: size too large");
-    FX_REQUIRE(act == 0 || act == 1, "fx_linear_fwd: act=%d (0 identity, 1 gelu_tanh)", act);
+    FX_REQUIRE(act >= 0 && act <= 2, "fx_linear_fwd: act=%d (0 identity, 1 gelu_tanh, 2 gelu_tanh with its derivative in H)",
+               act);
     if (idx) {
         FX_REQUIRE(F >= 8 && F % 8 == 0 && K % F == 0, "fx_linear_fwd: gather needs F%%8==0 and K%%F==0 (F=%lld)",
                    (long long)F);
@@ -1707,33 +1791,51 @@ static int dgrad_nj(int64_t M, int64_t N) {
     return (int)nj;
 }
 
-extern "C" int fx_linear_dgrad(const uint16_t* dY, int64_t ldy, const uint16_t* W, int64_t ldw, const uint16_t* H,
-                               uint16_t* dX, int64_t ldx, int64_t M, int64_t N, int64_t K, void* stream) {
-    FX_REQUIRE(dY && W && dX, "fx_linear_dgrad: null pointer");
-    FX_REQUIRE(M >= 0 && N >= 1 && K >= 1, "fx_linear_dgrad: bad shape M=%lld N=%lld K=%lld", (long long)M,
-               (long long)N, (long long)K);
-    FX_REQUIRE(M < 0x7fffffffLL && N < 0x7fffffffLL && K < 0x7fffffffLL, "fx_linear_dgrad: size too large");
+// EPI 0: dX = dY W; 1: H the pre-activation of a GELU layer, dX = bf16(dY W) gelu'(H);
+// 2: H the GELU derivative itself, dX = bf16(dY W) H
+static int dgrad_run(const char* fn, const uint16_t* dY, int64_t ldy, const uint16_t* W, int64_t ldw,
+                     const uint16_t* H, int epi, uint16_t* dX, int64_t ldx, int64_t M, int64_t N, int64_t K,
+                     void* stream) {
+    FX_REQUIRE(dY && W && dX && (epi == 0 || H), "%s: null pointer", fn);
+    FX_REQUIRE(M >= 0 && N >= 1 && K >= 1, "%s: bad shape M=%lld N=%lld K=%lld", fn, (long long)M, (long long)N,
+               (long long)K);
+    FX_REQUIRE(M < 0x7fffffffLL && N < 0x7fffffffLL && K < 0x7fffffffLL, "%s: size too large", fn);
     const int nj = dgrad_nj(M, N);
     FX_REQUIRE(M % 256 == 0 && nj != 0 && K % 32 == 0 && K >= 32 * kAsmStages,
-               "fx_linear_dgrad: whole tiles only (M %% 256, N %% 256 or %% 192, K %% 32 == 0, K >= 128): "
-               "M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
+               "%s: whole tiles only (M %% 256, N %% 256 or %% 192, K %% 32 == 0, K >= 128): "
+               "M=%lld N=%lld K=%lld", fn, (long long)M, (long long)N, (long long)K);
     FX_REQUIRE(ldy >= K && ldw >= N && ldx >= N && ldy % 8 == 0 && ldw % 8 == 0 && ldx % 8 == 0,
-               "fx_linear_dgrad: bad leading dimension (ldy=%lld ldw=%lld ldx=%lld)", (long long)ldy, (long long)ldw,
+               "%s: bad leading dimension (ldy=%lld ldw=%lld ldx=%lld)", fn, (long long)ldy, (long long)ldw,
                (long long)ldx);
     FX_REQUIRE(((((uintptr_t)dY) | ((uintptr_t)W) | ((uintptr_t)H) | ((uintptr_t)dX)) & 15) == 0,
-               "fx_linear_dgrad: dY, W, H and dX must be 16-byte aligned");
+               "%s: dY, W, H and dX must be 16-byte aligned", fn);
     if (M == 0) return 0;
     DgradArgs a{dY, ldy, W, ldw, H, dX, ldx, (int)M, (int)N, (int)K};
     const unsigned tiles = (unsigned)((M / 256) * (N / (64 * nj)));
     hipStream_t s = (hipStream_t)stream;
+#define FX_DGRAD(J, E) hipLaunchKernelGGL((gemm_dgrad_fast_kernel<J, E>), dim3(tiles), dim3(256), 0, s, a)
     if (nj == 4) {
-        if (H) hipLaunchKernelGGL((gemm_dgrad_fast_kernel<4, 1>), dim3(tiles), dim3(256), 0, s, a);
-        else hipLaunchKernelGGL((gemm_dgrad_fast_kernel<4, 0>), dim3(tiles), dim3(256), 0, s, a);
+        if (epi == 2) FX_DGRAD(4, 2);
+        else if (epi == 1) FX_DGRAD(4, 1);
+        else FX_DGRAD(4, 0);
     } else {
-        if (H) hipLaunchKernelGGL((gemm_dgrad_fast_kernel<3, 1>), dim3(tiles), dim3(256), 0, s, a);
-        else hipLaunchKernelGGL((gemm_dgrad_fast_kernel<3, 0>), dim3(tiles), dim3(256), 0, s, a);
+        if (epi == 2) FX_DGRAD(3, 2);
+        else if (epi == 1) FX_DGRAD(3, 1);
+        else FX_DGRAD(3, 0);
     }
+#undef FX_DGRAD
     return check_launch("gemm_dgrad");
+}
+
+extern "C" int fx_linear_dgrad(const uint16_t* dY, int64_t ldy, const uint16_t* W, int64_t ldw, const uint16_t* H,
+                               uint16_t* dX, int64_t ldx, int64_t M, int64_t N, int64_t K, void* stream) {
+    return dgrad_run("fx_linear_dgrad", dY, ldy, W, ldw, H, H ? 1 : 0, dX, ldx, M, N, K, stream);
+}
+
+extern "C" int fx_linear_dgrad_gate(const uint16_t* dY, int64_t ldy, const uint16_t* W, int64_t ldw,
+                                    const uint16_t* G, uint16_t* dX, int64_t ldx, int64_t M, int64_t N, int64_t K,
+                                    void* stream) {
+    return dgrad_run("fx_linear_dgrad_gate", dY, ldy, W, ldw, G, 2, dX, ldx, M, N, K, stream);
 }
 
 extern "C" int fx_gelu_bwd(const uint16_t* dy, const uint16_t* h, uint16_t* dh, int64_t n, void* stream) {
@@ -1746,6 +1848,18 @@ extern "C" int fx_gelu_bwd(const uint16_t* dy, const uint16_t* h, uint16_t* dh, 
     if (blocks < 1) blocks = 1;
     hipLaunchKernelGGL(gelu_bwd_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, dy, h, dh, n);
     return check_launch("gelu_bwd");
+}
+
+extern "C" int fx_gelu_bwd_gate(const uint16_t* dy, const uint16_t* g, uint16_t* dh, int64_t n, void* stream) {
+    FX_REQUIRE(n >= 0 && (n == 0 || (dy && g && dh)), "fx_gelu_bwd_gate: null pointer");
+    FX_REQUIRE(((((uintptr_t)dy) | ((uintptr_t)g) | ((uintptr_t)dh)) & 15) == 0,
+               "fx_gelu_bwd_gate: buffers must be 16-byte aligned");
+    if (n == 0) return 0;
+    int64_t blocks = (n / 8 + 255) / 256;
+    if (blocks > 16384) blocks = 16384;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(gate_mul_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, dy, g, dh, n);
+    return check_launch("gate_mul");
 }
 
 // ---------------------------------------------------------------------------

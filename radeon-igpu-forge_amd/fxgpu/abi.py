@@ -14,7 +14,7 @@ LIB_PATH = os.path.join(_PKG_ROOT, "libfxforge.so")
 HEADER_PATH = os.path.join(os.path.dirname(_PKG_ROOT), "include", "fx_abi.h")
 
 FX_EINVAL = -1
-FX_ABI_VERSION = 4
+FX_ABI_VERSION = 5
 MAX_TENSORS = 64
 ADAMW_NOALLOC_SCRATCH_BYTES = 1 << 20   # FX_ADAMW_NOALLOC_SCRATCH_BYTES
 
@@ -130,9 +130,12 @@ SIGNATURES = {
                                 c_int64, c_int64, c_int64, c_int32, _P]),
     "fx_linear_fwd_ex": (c_int32, [_P, _P]),
     "fx_gelu_bwd": (c_int32, [_P, _P, _P, c_int64, _P]),
+    "fx_gelu_bwd_gate": (c_int32, [_P, _P, _P, c_int64, _P]),
     "fx_embedding_bwd_workspace": (c_int64, [c_int64, c_int64, c_int64]),
     "fx_embedding_bwd": (c_int32, [_P, c_int64, _P, c_int64, _P, c_int64, c_int64, _P, _P]),
     "fx_linear_dgrad": (c_int32, [_P, c_int64, _P, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int64, _P]),
+    "fx_linear_dgrad_gate": (c_int32, [_P, c_int64, _P, c_int64, _P, _P, c_int64, c_int64, c_int64, c_int64,
+                                       _P]),
     "fx_linear_wgrad_workspace": (c_int64, [c_int64, c_int64, c_int64]),
     "fx_linear_wgrad": (c_int32, [_P, c_int64, _P, c_int64, _P, c_int64, _P, c_int64, c_int64, c_int64,
                                   _P]),

@@ -14,10 +14,11 @@
   GPT's qkv, proj and fc2 projections.  Forwards of at most FEW_ROWS rows (decode
   steps) run on the few-row kernel behind fx_linear_fwd, the whole_tiles() shapes on
   its whole-tile kernel, the others on the library GEMM.
-* ``fused_mlp(x, w1, w2)`` -- gelu_tanh(x w1^T) w2^T as one autograd node: the GELU in
-  the fc epilogue, its derivative in the fc2 input gradient's epilogue (fx_linear_dgrad).
-* ``input_grad(dy, W, h=None)`` -- dx = dy W (and * gelu'(h)) on fx_linear_dgrad for whole
-  tiles, else the library GEMM.
+* ``fused_mlp(x, w1, w2)`` -- gelu_tanh(x w1^T) w2^T as one autograd node: the GELU and
+  its derivative g = gelu'(h) in the fc epilogue (g saved in place of the pre-activation),
+  the product with g in the fc2 input gradient's epilogue (fx_linear_dgrad_gate).
+* ``input_grad(dy, W, g=None)`` -- dx = dy W (and * g) on fx_linear_dgrad(_gate) for whole
+  tiles, else the library GEMM (and fx_gelu_bwd_gate).
 * ``linear_wgrad(dy, x)`` -- dW = dy^T x for dy (T, N) and x (T, K): the weight
   gradient that ml/fxgpu/fused_linear.py:90-101 computes with rocBLAS.
 * ``linear_ex(x, W, bias, residual, norm_weight, eps, activation)`` -- inference
@@ -85,17 +86,21 @@ def whole_tiles(M, N, K):
 # steps, medians, one process).  With the two-step LDS buffers of the whole-tile kernels
 # (whole 128-byte lines from HBM), the qkv and proj forwards (whole_tiles()) on fx_linear_fwd
 # measured +0.011 ms per step against the library GEMM, within the rounds' spread: they run
-# on this build's kernel.  The input gradients do not: the qkv one at parity (-0.003 to
-# +0.005 ms), the proj and fc ones and fc2's with the GELU derivative folded in 0.04-0.08 ms
-# slower each (cold operands from HBM, and tile epilogues that one workgroup per CU cannot
-# overlap with its MFMA work).
+# on this build's kernel.  The plain input gradients do not: the qkv one at parity (-0.003
+# to +0.005 ms), the proj and fc ones 0.04-0.08 ms slower each (cold operands from HBM, and
+# tile epilogues that one workgroup per CU cannot overlap with its MFMA work).  fc2's, with
+# the saved GELU derivative multiplied in its epilogue, runs on this build's kernel.
 # NATIVE_INPUT_GRAD: input gradients on fx_linear_dgrad where input_grad() takes them;
 # NATIVE_PROJ_FWD: the whole_tiles() forwards on fx_linear_fwd.  False: the library GEMM.
 NATIVE_INPUT_GRAD = False
 NATIVE_PROJ_FWD = True
 # NATIVE_GELU_INPUT_GRAD: only the input gradient with the GELU derivative folded in (the
-# GPT MLP's fc2, where fx_linear_dgrad also saves fx_gelu_bwd's pass over three tensors)
-NATIVE_GELU_INPUT_GRAD = False
+# GPT MLP's fc2, where fx_linear_dgrad_gate also saves fx_gelu_bwd_gate's pass over three
+# tensors).  With the derivative stored by the fc forward (fused_mlp) the epilogue only
+# multiplies, and the step measured 0.13 ms faster (16 interleaved rounds, every round
+# faster); evaluating the derivative from the pre-activation in that epilogue had measured
+# 0.04 ms slower than the library GEMM and fx_gelu_bwd.
+NATIVE_GELU_INPUT_GRAD = True
 
 
 def dgrad_tiles(M, N, K):
@@ -103,32 +108,37 @@ def dgrad_tiles(M, N, K):
     return M % 256 == 0 and (N % 256 == 0 or N % 192 == 0) and K % 32 == 0 and K >= 128
 
 
-def input_grad(dy2, weight, h=None):
-    """dx = dy2 @ weight (bf16), and with h (the pre-activation of a GELU(tanh) layer feeding
-    this one) dx * gelu'(h).  With NATIVE_INPUT_GRAD, on fx_linear_dgrad for dgrad_tiles()
-    shapes where it measured at least as fast as the library GEMM with the operands in the
-    caches (input widths up to 1024 columns: the cfg5 qkv, proj and fc input gradients,
-    52.1 / 22.9 / 66.0 us against 60.5 / 25.4 / 67.2 us; from HBM 72.3 / 31.6 / 93.7 against
-    64.5 / 30.3 / 82.4 us), and always with h (the GELU backward folded into the epilogue:
-    122.8 us against 76.4 + 46 us for the cfg5 fc2 product and fx_gelu_bwd); else torch.mm,
-    then fx_gelu_bwd for h."""
+def input_grad(dy2, weight, g=None):
+    """dx = dy2 @ weight (bf16), and with g (the GELU(tanh) derivative at the output of the
+    layer feeding this one, as fx_linear_fwd with act 2 stores it) bf16(dx) * g.  With
+    NATIVE_INPUT_GRAD, on fx_linear_dgrad for dgrad_tiles() shapes where it measured at
+    least as fast as the library GEMM with the operands in the caches (input widths up to
+    1024 columns: the cfg5 qkv, proj and fc input gradients, 52.1 / 22.9 / 66.0 us against
+    60.5 / 25.4 / 67.2 us; from HBM 72.3 / 31.6 / 93.7 against 64.5 / 30.3 / 82.4 us); with
+    g and NATIVE_GELU_INPUT_GRAD on fx_linear_dgrad_gate (the product with g in the
+    epilogue: 98.8 us against 126.3 for the cfg5 fc2 product on the library GEMM and
+    fx_gelu_bwd, 125.5 against 133.6 from HBM); else torch.mm, then fx_gelu_bwd_gate for g."""
     M, K = dy2.shape
     N = weight.shape[1]
-    wanted = (NATIVE_INPUT_GRAD and (h is not None or N <= 1024)) or (NATIVE_GELU_INPUT_GRAD and h is not None)
+    wanted = (NATIVE_INPUT_GRAD and (g is not None or N <= 1024)) or (NATIVE_GELU_INPUT_GRAD and g is not None)
     native = (wanted and dy2.is_cuda and dgrad_tiles(M, N, K)
               and weight.is_contiguous() and weight.data_ptr() % 16 == 0
               and dy2.stride(1) == 1 and dy2.stride(0) % 8 == 0 and dy2.data_ptr() % 16 == 0
-              and (h is None or (h.is_contiguous() and h.data_ptr() % 16 == 0)))
+              and (g is None or (g.is_contiguous() and g.data_ptr() % 16 == 0)))
     if native:
         dx = torch.empty(M, N, device=dy2.device, dtype=torch.bfloat16)
-        call("fx_linear_dgrad", ptr(dy2), dy2.stride(0), ptr(weight), N, ptr(h), ptr(dx), N, M, N, K,
-             stream_of(dy2))
+        if g is None:
+            call("fx_linear_dgrad", ptr(dy2), dy2.stride(0), ptr(weight), N, None, ptr(dx), N, M, N, K,
+                 stream_of(dy2))
+        else:
+            call("fx_linear_dgrad_gate", ptr(dy2), dy2.stride(0), ptr(weight), N, ptr(g), ptr(dx), N, M, N,
+                 K, stream_of(dy2))
         return dx
     dx = torch.mm(dy2, weight)
-    if h is None:
+    if g is None:
         return dx
     dh = torch.empty_like(dx)
-    call("fx_gelu_bwd", ptr(dx), ptr(h), ptr(dh), dh.numel(), stream_of(dx))
+    call("fx_gelu_bwd_gate", ptr(dx), ptr(g), ptr(dh), dh.numel(), stream_of(dx))
     return dh
 
 
@@ -293,10 +303,11 @@ def fused_linear(x, weight, bias=None, activation="gelu_tanh"):
 
 class FusedMLP(torch.autograd.Function):
     """y = gelu_tanh(x W1^T) W2^T (no biases): the GPT MLP (ml/fxlm/model.py:64-66,71,
-    nn.Linear fc -> F.gelu(approximate="tanh") -> nn.Linear fc2) as one autograd node, so
-    that the backward can fold the GELU derivative into the fc2 input-gradient product
-    (fx_linear_dgrad with the pre-activation).  Same kernels and roundings as fused_linear
-    followed by linear in the forward."""
+    nn.Linear fc -> F.gelu(approximate="tanh") -> nn.Linear fc2) as one autograd node.  The
+    fc forward (fx_linear_fwd, act 2) stores, in place of the pre-activation h, the GELU
+    derivative g = gelu'(h) from the fp32 h and the exponential the GELU itself takes; the
+    backward's fc2 input gradient multiplies by it in its epilogue (fx_linear_dgrad_gate).
+    The forward's outputs are those of fused_linear followed by linear, bit for bit."""
 
     @staticmethod
     def forward(ctx, x, w1, w2):
@@ -314,23 +325,23 @@ class FusedMLP(torch.autograd.Function):
         x2 = _rows(x)
         M, Fh = x2.shape[0], w1.shape[0]
         u = torch.empty(M, Fh, device=x.device, dtype=torch.bfloat16)
-        h = torch.empty_like(u) if any(ctx.needs_input_grad) else None
-        call("fx_linear_fwd", ptr(x2), x2.stride(0), None, 0, 0, ptr(w1), None, ptr(u), ptr(h), None,
-             M, Fh, K, 1, stream_of(x))
+        gd = torch.empty_like(u) if any(ctx.needs_input_grad) else None
+        call("fx_linear_fwd", ptr(x2), x2.stride(0), None, 0, 0, ptr(w1), None, ptr(u), ptr(gd), None,
+             M, Fh, K, 2, stream_of(x))
         N = w2.shape[0]
         if 0 < M <= FEW_ROWS or (NATIVE_PROJ_FWD and whole_tiles(M, N, Fh)):
             y = _native_fwd(u, w2)
         else:
             y = torch.mm(u, w2.t())
-        ctx.save_for_backward(x2, w1, w2, u, h)
+        ctx.save_for_backward(x2, w1, w2, u, gd)
         ctx.xshape = x.shape
         return y.view(*x.shape[:-1], N)
 
     @staticmethod
     def backward(ctx, dy):
-        x2, w1, w2, u, h = ctx.saved_tensors
+        x2, w1, w2, u, gd = ctx.saved_tensors
         dy2 = _rows(dy.to(torch.bfloat16) if dy.dtype != torch.bfloat16 else dy)
-        dh = input_grad(dy2, w2, h)              # (dy W2) gelu'(h)
+        dh = input_grad(dy2, w2, gd)             # (dy W2) gelu'(h)
         dw2 = linear_wgrad(dy2, u) if ctx.needs_input_grad[2] else None
         dx = input_grad(dh, w1).view(ctx.xshape) if ctx.needs_input_grad[0] else None
         dw1 = linear_wgrad(dh, x2) if ctx.needs_input_grad[1] else None
@@ -338,8 +349,8 @@ class FusedMLP(torch.autograd.Function):
 
 
 def fused_mlp(x, w1, w2):
-    """gelu_tanh(x @ w1.T) @ w2.T with the GELU in the fc epilogue and its derivative in the
-    fc2 input gradient's epilogue."""
+    """gelu_tanh(x @ w1.T) @ w2.T with the GELU and its derivative in the fc epilogue and the
+    product with the derivative in the fc2 input gradient's epilogue."""
     return FusedMLP.apply(x, w1, w2)
 
 

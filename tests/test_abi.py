@@ -134,7 +134,9 @@ def _bad_calls(abi):
         ("fx_linear_fwd", (f, 8, None, 0, 0, f, None, f, None, None, 4, 8, 7, 0, None)),
         ("fx_linear_fwd_ex", (None, None)),
         ("fx_gelu_bwd", (f, m, f, 8, None)),
+        ("fx_gelu_bwd_gate", (f, m, f, 8, None)),
         ("fx_linear_dgrad", (f, 768, f, 768, None, f, 768, 100, 768, 768, None)),
+        ("fx_linear_dgrad_gate", (f, 768, f, 768, None, f, 768, 256, 768, 768, None)),   # no G
         ("fx_linear_wgrad", (f, 12, f, 8, f, 8, None, 12, 8, 16, None)),
         ("fx_lce_fwd", (f, 768, f, f, -100, f, f, f, 256, 1000, 768, None)),
         ("fx_lce_grad", (f, 768, None, f, -100, f, f, f, 768, 256, 768, 768, None)),
@@ -152,6 +154,15 @@ def test_every_entry_point_rejects_bad_arguments_before_launch(abi):
         rc = getattr(lib, name)(*args)
         assert rc == abi.FX_EINVAL, (name, rc)
         assert lib.fx_last_error().decode().startswith(name), (name, lib.fx_last_error())
+
+
+def test_linear_fwd_activation_codes(abi):
+    # 0 identity, 1 GELU, 2 GELU with its derivative in H; anything else is refused first
+    lib = abi.lib()
+    f = ctypes.c_void_p(_F)
+    for act in (-1, 3):
+        assert lib.fx_linear_fwd(f, 8, None, 0, 0, f, None, f, f, None, 4, 8, 8, act, None) == abi.FX_EINVAL
+        assert "act=" in lib.fx_last_error().decode()
 
 
 def test_embedding_bwd_checks_and_workspace(abi):

@@ -1,4 +1,5 @@
-"""Fused (gather) linear layers on the GPU (fx_linear_fwd / fx_gelu_bwd) against the oracle.
+"""Fused (gather) linear layers on the GPU (fx_linear_fwd / fx_gelu_bwd / fx_linear_dgrad(_gate) /
+fx_gelu_bwd_gate / fx_linear_wgrad) against the oracle.
 
 Tolerance (tolerances.oracle_close): |ours - oracle| <= 2^-8 |oracle| + f max|oracle| with
 f = 1e-3 for outputs (one rounding of an fp32 product) and f = 4e-3 for gradients (the
@@ -10,7 +11,7 @@ import torch.nn.functional as F
 
 from golden_util import bf16, f32, load
 from oracle import linear as olin
-from tolerances import FRAC_OUT, oracle_close
+from tolerances import FRAC_GRAD, FRAC_OUT, oracle_close
 
 pytestmark = pytest.mark.gpu
 
@@ -53,7 +54,7 @@ def test_reference_selftest_gather(dev):
     out_r = F.linear(xb.float(), w_r.float(), b_r.float())
     w_f, b_f = weight.clone().requires_grad_(), bias.clone().requires_grad_()
     out_f = fused_gather_linear(X, idx, w_f, b_f)
-    assert float((out_f.double() - out_r.double()).abs().max()) < 0.05
+    assert (out_f.detach().double() - out_r.detach().double()).abs().max().item() < 0.05
     g = torch.randn(B, HID, device=dev).bfloat16()
     out_f.backward(g)
     # the reference's backward on the unfolded rows, in fp64: the bf16 dW is its rounding
@@ -467,17 +468,88 @@ def test_dgrad_rejects_partial_tiles(dev):
         call("fx_linear_dgrad", ptr(dy), 128, ptr(W), 256, None, ptr(dx), 256, 256, 256, 96, stream_of(dy))
 
 
-# ---- the GPT MLP as one node (fused_mlp): GELU in the fc epilogue, its derivative in the fc2
-# input gradient's epilogue ---------------------------------------------------------------------
+# ---- the GELU derivative stored by the forward (act 2) and multiplied in the backward --------
+
+@pytest.mark.parametrize("M,K,N,bias,path", [
+    (512, 256, 512, True, "whole"),     # 256-wide whole tiles, with bias
+    (512, 160, 192, False, "whole"),    # 192-wide whole tiles, 5 K steps (the leading zero step)
+    (16384, 768, 3072, False, "whole"), # the cfg5 MLP fc
+    (300, 96, 200, True, "general"),    # partial tiles: the general kernel
+    (40, 64, 72, True, "few"),          # few rows
+])
+def test_linear_fwd_gelu_derivative(dev, monkeypatch, M, K, N, bias, path):
+    g = torch.Generator(device=dev).manual_seed(M + K + N)
+    x = torch.randn(M, K, device=dev, generator=g).bfloat16()
+    W = (torch.randn(N, K, device=dev, generator=g) * K ** -0.5).bfloat16()
+    b = (torch.randn(N, device=dev, generator=g) * 0.3).bfloat16() if bias else None
+    print(f"gelu derivative fwd M={M} K={K} N={N} bias={bias} path={path}", flush=True)
+    y1, _ = _linear_fwd(x, W, b, 1, True)
+    y2, d2 = _linear_fwd(x, W, b, 2, True)
+    y3, _ = _linear_fwd(x, W, b, 2, False)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2) and torch.equal(y1, y3)       # the same GELU output, bit for bit
+    h = x.double() @ W.double().t() + (b.double() if bias else 0)
+    assert oracle_close(d2, olin.gelu_tanh_grad(h.cpu()), FRAC_OUT)
+    if path == "whole":   # the general kernel evaluates the same expression
+        monkeypatch.setenv("FX_GEMM_GENERAL", "f")
+        y4, d4 = _linear_fwd(x, W, b, 2, True)
+        torch.cuda.synchronize()
+        assert torch.equal(y4, y2) and torch.equal(d4, d2)
+
+
+def _dgrad_gate(dy, W, gd):
+    from fxgpu.abi import call, ptr, stream_of
+    M, K = dy.shape
+    N = W.shape[1]
+    dx = torch.empty(M, N, device=dy.device, dtype=torch.bfloat16)
+    call("fx_linear_dgrad_gate", ptr(dy), dy.stride(0), ptr(W), W.stride(0), ptr(gd), ptr(dx), N, M, N, K,
+         stream_of(dy))
+    return dx
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 128), (512, 192, 160), (256, 768, 224), (16384, 3072, 768)])
+def test_dgrad_gate_matches_the_pair(dev, M, N, K):
+    from fxgpu.abi import call, ptr, stream_of
+    g = torch.Generator(device=dev).manual_seed(M + N + K)
+    dy = torch.randn(M, K, device=dev, generator=g).bfloat16()
+    W = (torch.randn(K, N, device=dev, generator=g) * K ** -0.5).bfloat16()
+    gd = (torch.rand(M, N, device=dev, generator=g) * 1.3 - 0.15).bfloat16()   # the range of gelu'
+    print(f"dgrad gate M={M} N={N} K={K}", flush=True)
+    got = _dgrad_gate(dy, W, gd)
+    dx = _dgrad(dy, W)
+    pair = torch.empty_like(dx)
+    call("fx_gelu_bwd_gate", ptr(dx), ptr(gd), ptr(pair), dx.numel(), stream_of(dx))
+    torch.cuda.synchronize()
+    assert torch.equal(got, pair)
+    ref = (dy.double() @ W.double()) * gd.double()
+    assert oracle_close(got, ref, FRAC_GRAD)   # two roundings: the bf16 product, then dh
+
+
+@pytest.mark.parametrize("n", [0, 5, 8 * 997 + 3, 16384 * 3072])
+def test_gelu_bwd_gate_is_the_rounded_product(dev, n):
+    from fxgpu.abi import call, ptr, stream_of
+    g = torch.Generator(device=dev).manual_seed(n)
+    a = torch.randn(max(n, 1), device=dev, generator=g).bfloat16()[:n]
+    b = torch.randn(max(n, 1), device=dev, generator=g).bfloat16()[:n]
+    out = torch.empty_like(a)
+    call("fx_gelu_bwd_gate", ptr(a), ptr(b), ptr(out), n, stream_of(a))
+    torch.cuda.synchronize()
+    # a product of two bf16 values is exact in fp32, so one rounding to nearest even decides
+    assert torch.equal(out.cpu(), (a.float().cpu() * b.float().cpu()).bfloat16())
+
+
+# ---- the GPT MLP as one node (fused_mlp): GELU and its derivative in the fc epilogue, the
+# product with the derivative in the fc2 input gradient's epilogue --------------------------------
 
 @pytest.mark.parametrize("native", [True, False])  # the whole-tile kernels where shapes allow, or the library
-@pytest.mark.parametrize("M,K,Fh,N", [(512, 256, 1024, 256),     # whole tiles: fx_linear_dgrad with H
-                                      (300, 64, 256, 64),        # partial tiles: library GEMM + fx_gelu_bwd
+@pytest.mark.parametrize("M,K,Fh,N", [(512, 256, 1024, 256),     # whole tiles: fx_linear_dgrad_gate
+                                      (300, 64, 256, 64),        # partial tiles: library GEMM + fx_gelu_bwd_gate
                                       (16384, 768, 3072, 768)])  # cfg5
 def test_fused_mlp_against_composition_and_fp32(dev, monkeypatch, native, M, K, Fh, N):
     import fxgpu.fused_linear as FL
     monkeypatch.setattr(FL, "NATIVE_INPUT_GRAD", native)
     monkeypatch.setattr(FL, "NATIVE_PROJ_FWD", native)
+    monkeypatch.setattr(FL, "NATIVE_GELU_INPUT_GRAD", native)
     g = torch.Generator(device=dev).manual_seed(M + Fh)
     x = torch.randn(M, K, device=dev, generator=g).bfloat16()
     w1 = (torch.randn(Fh, K, device=dev, generator=g) * K ** -0.5).bfloat16()

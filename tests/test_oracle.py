@@ -278,6 +278,25 @@ def test_linear_gelu_matches_autograd():
     assert torch.allclose(dW, Wr.grad, atol=1e-12) and torch.allclose(db, br.grad, atol=1e-12)
 
 
+
+def test_gelu_tanh_grad_matches_autograd_and_the_sigmoid_form():
+    # the oracle's derivative against torch's autograd of F.gelu(approximate="tanh"), over
+    # the range where it is not 0 or 1 to double precision, and the form the forward GEMM's
+    # epilogue evaluates (fx_linear_fwd act 2): s = sigmoid(2u), gelu = h s,
+    # gelu' = s (1 + h (1 - s) (2c + 6c 0.044715 h^2)), c = sqrt(2/pi)
+    h = torch.linspace(-12.0, 12.0, 4801, dtype=f64, requires_grad=True)
+    F.gelu(h, approximate="tanh").sum().backward()
+    hd = h.detach()
+    g = olin.gelu_tanh_grad(hd)
+    assert torch.allclose(g, h.grad, rtol=0, atol=1e-13)
+    c = math.sqrt(2.0 / math.pi)
+    s = torch.sigmoid(2 * c * (hd + 0.044715 * hd ** 3))
+    assert torch.allclose(hd * s, olin.gelu_tanh(hd), rtol=0, atol=1e-13)
+    assert torch.allclose(s * (1 + hd * (1 - s) * (2 * c + 6 * c * 0.044715 * hd * hd)), g, rtol=0, atol=1e-12)
+    # a dropped term is caught: without the h (1 - s) u' part the slope misses by up to 0.6
+    assert float((s - g).abs().max()) > 0.1
+
+
 # ---------------------------------------------------------------- GPT (CPU baseline model)
 
 def _tiny_gpt(V=64, T=16, L=2, H=2, D=32, seed=0, dtype=f64):
