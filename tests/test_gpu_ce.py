@@ -131,7 +131,7 @@ def test_cfg3_full_size(dev):
     loss = fused_cross_entropy(x, tg)
     loss.backward()
     ref = F.cross_entropy(lg.float(), tg, ignore_index=-100)
-    assert abs(float(loss) - float(ref)) <= RTOL_LOSS * abs(float(ref))
+    assert abs(loss.item() - float(ref)) <= RTOL_LOSS * abs(float(ref))
     rows = torch.arange(0, N, 1024, device=dev)
     sub = lg[rows].float().requires_grad_()
     tsub = tg[rows]
@@ -155,7 +155,7 @@ def test_linear_ce(dev, N, D, V, gs):
     loss = linear_cross_entropy(xq, Wq, tg.to(dev), grad_scale=grad_scale, chunk_rows=128)
     loss.backward()
     rl, _, _ = oce.linear_cross_entropy(x, W, tg)
-    assert abs(float(loss) - float(rl)) <= RTOL_LOSS * abs(float(rl))
+    assert abs(loss.item() - float(rl)) <= RTOL_LOSS * abs(float(rl))
     rdx, rdW = _lin_ce_grads_bf16_points(x, W, tg, chunk_rows=128)
     _assert_lin_grads(xq.grad, Wq.grad, rdx, rdW)
 
@@ -176,7 +176,7 @@ def test_linear_ce_native_head_weight_gradient(dev, monkeypatch, N, V):
     loss = ce.linear_cross_entropy(xq, Wq, tg.to(dev), grad_scale=256.0)
     loss.backward()
     rl, _, _ = oce.linear_cross_entropy(x, W, tg)
-    assert abs(float(loss) - float(rl)) <= RTOL_LOSS * abs(float(rl))
+    assert abs(loss.item() - float(rl)) <= RTOL_LOSS * abs(float(rl))
     rdx, rdW = _lin_ce_grads_bf16_points(x, W, tg)
     _assert_lin_grads(xq.grad, Wq.grad, rdx, rdW)
 
@@ -275,7 +275,7 @@ def test_linear_ce_single_chunk(dev, gs):
     loss = linear_cross_entropy(xq, Wq, tg.to(dev), grad_scale=grad_scale)
     loss.backward()
     rl, _, _ = oce.linear_cross_entropy(x, W, tg)
-    assert abs(float(loss) - float(rl)) <= RTOL_LOSS * abs(float(rl))
+    assert abs(loss.item() - float(rl)) <= RTOL_LOSS * abs(float(rl))
     rdx, rdW = _lin_ce_grads_bf16_points(x, W, tg)
     _assert_lin_grads(xq.grad, Wq.grad, rdx, rdW)
 
@@ -329,7 +329,7 @@ def test_linear_ce_cfg5_head_one_chunk(dev):
         x, w = x0.clone().requires_grad_(), w0.clone().requires_grad_()
         loss = linear_cross_entropy(x, w, tg, grad_scale=1024.0, chunk_rows=chunk)
         loss.backward()
-        res[chunk] = (float(loss), x.grad, w.grad)
+        res[chunk] = (loss.item(), x.grad, w.grad)
     ref = F.cross_entropy(x0.float() @ w0.float().t(), tg, ignore_index=-100)
     for chunk, (l, gx, gw) in res.items():
         assert abs(l - float(ref)) <= RTOL_LOSS * abs(float(ref)), chunk

@@ -108,7 +108,7 @@ def test_unsupported_shapes_fall_back(dev):
     with torch.no_grad():
         loss = linear_cross_entropy(x, w, tg)
     ref = F.cross_entropy(x.float() @ w.float().t(), tg)
-    assert abs(float(loss) - float(ref)) <= RTOL_LOSS * abs(float(ref))
+    assert abs(loss.item() - float(ref)) <= RTOL_LOSS * abs(float(ref))
 
 
 def _run(x0, w0, tg, grad, fused_loss, fused_train, chunk_rows=None, grad_scale=1.0):
@@ -122,7 +122,7 @@ def _run(x0, w0, tg, grad, fused_loss, fused_train, chunk_rows=None, grad_scale=
         x, w = x0.clone().requires_grad_(), w0.clone().requires_grad_()
         loss = ce.linear_cross_entropy(x, w, tg, grad_scale=grad_scale, chunk_rows=chunk_rows)
         loss.backward()
-        return float(loss), x.grad, w.grad
+        return loss.item(), x.grad, w.grad
     finally:
         ce.FUSED_LINEAR_CE_LOSS, ce.FUSED_LINEAR_CE_TRAIN = old
 
