@@ -21,12 +21,12 @@ RTOL_ADAMW = 1e-6
 
 
 def max_abs(a, b):
-    return float((a.double().cpu() - b.double().cpu()).abs().max()) if a.numel() else 0.0
+    return float((a.detach().double().cpu() - b.detach().double().cpu()).abs().max()) if a.numel() else 0.0
 
 
 def bf16_close(ours, ref, atol=ATOL_BF16, rtol=RTOL_BF16):
     """True when |ours - ref| <= atol + rtol |ref| elementwise."""
-    o, r = ours.double().cpu(), ref.double().cpu()
+    o, r = ours.detach().double().cpu(), ref.detach().double().cpu()
     return bool(((o - r).abs() <= atol + rtol * r.abs()).all())
 
 
@@ -36,11 +36,11 @@ FRAC_GRAD = 4e-3
 
 def oracle_close(ours, ref, frac=FRAC_GRAD):
     """|ours - ref| <= 2^-8 |ref| + frac * max|ref| elementwise (bf16 results)."""
-    r = ref.double().cpu()
+    r = ref.detach().double().cpu()
     return bf16_close(ours, r, atol=frac * float(r.abs().max()) + 1e-9, rtol=RTOL_BF16)
 
 
 def rel_err(ours, ref):
-    o, r = ours.double().cpu(), ref.double().cpu()
+    o, r = ours.detach().double().cpu(), ref.detach().double().cpu()
     den = r.abs().max().clamp_min(1e-30)
     return float((o - r).abs().max() / den)
