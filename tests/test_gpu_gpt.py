@@ -80,7 +80,7 @@ def test_fused_vs_torch_paths(dev):
     l_t.backward()
     l_r.backward()
     # the reference's rule: our error <= 2 * (torch bf16 error) + 1e-3, against fp32
-    e_f, e_t = abs(float(l_f) - float(l_r)), abs(float(l_t) - float(l_r))
+    e_f, e_t = abs(l_f.item() - l_r.item()), abs(l_t.item() - l_r.item())
     assert e_f <= 2 * e_t + 1e-3
     rp = dict(m_r.named_parameters())
     tp = dict(m_t.named_parameters())
@@ -121,7 +121,7 @@ def _parity_vs_oracle(dev, V, T, L, H, D, B, seed):
     l_t.backward()
     ok, e, et = _rule_ok(l_f.detach(), l_r.detach(), l_t.detach())
     assert ok, ("loss", e, et)
-    assert abs(float(l_r) - math.log(V)) < 0.5        # N(0, 0.02) init: near-uniform logits
+    assert abs(l_r.item() - math.log(V)) < 0.5        # N(0, 0.02) init: near-uniform logits
     rp, tp = dict(m_r.named_parameters()), dict(m_t.named_parameters())
     for name, p in m_f.named_parameters():
         assert bool(torch.isfinite(p.grad).all()), name
@@ -135,7 +135,7 @@ def _parity_vs_oracle(dev, V, T, L, H, D, B, seed):
         l_e = m_f(idx.to(dev), tgt.to(dev))
     ok, e, et = _rule_ok(l_e, l_r.detach(), l_t.detach())
     assert ok, ("eval loss", e, et)
-    assert abs(float(l_e) - float(l_f)) <= 1e-4 * abs(float(l_f))
+    assert abs(l_e.item() - l_f.item()) <= 1e-4 * abs(l_f.item())
 
 
 def test_cfg1_gpt_vs_oracle(dev):
@@ -380,7 +380,7 @@ def test_head_dim_128_model(dev):
     for l in (l_f, l_t, l_r):
         l.backward()
     # the reference's rule, as in test_fused_vs_torch_paths: error <= 2 x torch bf16's + 1e-3
-    assert abs(float(l_f) - float(l_r)) <= 2 * abs(float(l_t) - float(l_r)) + 1e-3
+    assert abs(l_f.item() - l_r.item()) <= 2 * abs(l_t.item() - l_r.item()) + 1e-3
     rp, tp = dict(m_r.named_parameters()), dict(m_t.named_parameters())
     for name, p in m_f.named_parameters():
         ef = float((p.grad.float().cpu() - rp[name].grad).abs().max())
